@@ -1,0 +1,96 @@
+"""Pins for the deterministic arithmetic in `oracle/numerics.py`.
+
+exp_det is checked against float64 `math.exp` rounded to fp32 (a library
+routine), for monotonicity (the nucleus order relies on it), and at its
+special points; fixed62 / rn32 / uniform_threshold against exact rational
+arithmetic.
+"""
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+from oracle.numerics import (LN2_HI, exp_det, fixed62, fixed62_sum, rn32, rn32_u64,
+                             uniform_threshold)
+
+
+def _rn32_fraction(fr):
+    """Reference fp32 rounding of an exact rational via float64 (exact when the
+    rational has < 53 significant bits, as in these tests)."""
+    return np.float32(float(fr))
+
+
+def test_exp_det_matches_rounded_libm():
+    rs = np.random.RandomState(0)
+    d = np.concatenate([-np.abs(rs.randn(200000).astype(np.float32)) * 20,
+                        -rs.uniform(0, 104, 100000).astype(np.float32),
+                        np.float32([0.0, -1e-30, -1e-8, -0.5, -1.0, -87.3, -103.9])])
+    got = exp_det(d)
+    ref = np.array([math.exp(float(x)) for x in d]).astype(np.float32)
+    diff = np.abs(got.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+    assert diff.max() <= 1
+    assert (diff == 0).mean() > 0.9999
+
+
+def test_exp_det_special_points():
+    assert exp_det(np.float32([0.0]))[0] == np.float32(1.0)
+    assert exp_det(np.float32([-104.01]))[0] == 0.0
+    assert exp_det(np.float32([-np.inf]))[0] == 0.0
+    # denormal range is produced, not flushed
+    v = exp_det(np.float32([-100.0]))[0]
+    assert 0 < v < np.finfo(np.float32).tiny
+
+
+def test_exp_det_monotone():
+    # dense sweep plus every fp32 input within +-64 ulps of each range-reduction
+    # boundary (k + 1/2) * ln2, where a Cody-Waite evaluation could step backwards
+    rs = np.random.RandomState(1)
+    d = np.sort(-rs.uniform(0, 104, 400000).astype(np.float32))
+    e = exp_det(d)
+    assert np.all(np.diff(e) >= 0)
+    pts = []
+    for k in range(-151, 1):
+        c = np.float32((k + 0.5) * math.log(2))
+        base = c.view(np.int32)
+        pts.append((base + np.arange(-64, 65, dtype=np.int32)).view(np.float32))
+    d = np.sort(np.concatenate(pts))
+    d = d[(d <= 0) & (d >= -104)]
+    assert np.all(np.diff(exp_det(d)) >= 0)
+    assert LN2_HI * 151 == float(Fraction(LN2_HI) * 151)   # k * LN2_HI is exact
+
+
+def test_fixed62_and_rn32_exact():
+    rs = np.random.RandomState(2)
+    x = rs.uniform(2.0 ** -39, 1.0, 20000).astype(np.float32)
+    f = fixed62(x)
+    for xi, fi in zip(x[:500], f[:500]):
+        assert Fraction(int(fi), 2 ** 62) == Fraction(float(xi))
+    back = rn32_u64(f)
+    assert np.array_equal(back, x)
+    # sums: rn32 of an exact integer equals fp32 rounding of the rational
+    s = fixed62_sum(x[:3])
+    assert rn32(s) == _rn32_fraction(sum(Fraction(float(v)) for v in x[:3]))
+
+
+def test_rn32_ties_to_even():
+    one = 2 ** 62
+    ulp = 2 ** (62 - 23)                   # fp32 ulp at 1.0 in fixed62 units
+    assert rn32(one + ulp // 2) == np.float32(1.0)                    # tie -> even (1.0)
+    assert rn32(one + ulp + ulp // 2) == np.float32(1.0 + 2 * 2.0 ** -23)   # tie -> even
+    assert rn32(one + ulp // 2 + 1) == np.float32(1.0 + 2.0 ** -23)
+    big = (3 << 62) + 12345
+    assert rn32(big) == np.float32(3.0)
+    a = np.array([one + ulp // 2, one + ulp + ulp // 2, 12345, 0], np.uint64)
+    assert np.array_equal(rn32_u64(a), np.array([rn32(int(v)) for v in a], np.float32))
+
+
+def test_uniform_threshold_exact():
+    rs = np.random.RandomState(3)
+    for _ in range(2000):
+        u = np.float32(rs.uniform(0, 1))
+        tot = int(rs.randint(1, 2 ** 62, dtype=np.int64))
+        assert uniform_threshold(u, tot) == math.floor(Fraction(float(u)) * tot)
+    assert uniform_threshold(np.float32(0.0), 10 ** 18) == 0
+    with pytest.raises(ValueError):
+        uniform_threshold(np.float32(1.0), 5)
