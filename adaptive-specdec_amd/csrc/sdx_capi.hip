@@ -1,0 +1,442 @@
+// extern "C" entry points of libspecdec_amd.so (declared in include/specdec_amd.h):
+// argument checks, workspace carving and kernel launches. No allocation.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "sdx_launch.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t e, const char* where) {
+  if (e == hipSuccess) return SDX_OK;
+  return fail(SDX_EHIP, "%s: %s", where, hipGetErrorString(e));
+}
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+// Bump allocator over the caller's workspace.
+struct Carve {
+  uint8_t* base;
+  size_t used = 0;
+  template <typename T>
+  T* take(size_t count) {
+    T* p = base ? reinterpret_cast<T*>(base + used) : nullptr;
+    used += align256(count * sizeof(T));
+    return p;
+  }
+};
+
+bool dtype_ok(int d) { return d == SDX_F32 || d == SDX_BF16 || d == SDX_F16; }
+size_t dsize(int d) { return d == SDX_F32 ? 4 : 2; }
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+struct Switches {
+  bool greedy, use_p, use_k;
+};
+Switches switches(float T, float top_p, int32_t top_k, int64_t V) {
+  Switches s;
+  s.greedy = !(T > 0.0f);
+  s.use_p = top_p > 0.0f && top_p < 1.0f;
+  s.use_k = top_k > 0 && (int64_t)top_k < V;
+  return s;
+}
+
+// Chunking of the id range for the draw / output kernels: chunks of a
+// multiple of 8 ids, at most 64 per row.
+void chunking(int64_t V, int64_t* chunk, int* nchunk) {
+  int64_t n = (V + 2047) / 2048;
+  if (n > 64) n = 64;
+  if (n < 1) n = 1;
+  int64_t c = (V + n - 1) / n;
+  c = (c + 7) / 8 * 8;
+  *chunk = c;
+  *nchunk = (int)((V + c - 1) / c);
+}
+
+constexpr int64_t kMaxVocab16 = 16 * 20 * 512;  // register capacity of the row kernel
+
+// Workspace of the transform + draw pipeline over `rows` rows and `njobs` draws.
+size_t transform_ws(Carve& c, int64_t rows, int64_t V, int dtype, int64_t njobs,
+                    sdx::RowStat** stats, float** tables, float** dense, sdx::SampleJob** jobs,
+                    uint64_t** sums) {
+  int64_t chunk;
+  int nchunk;
+  chunking(V, &chunk, &nchunk);
+  *stats = c.take<sdx::RowStat>(rows);
+  *tables = dtype == SDX_F32 ? nullptr : c.take<float>((size_t)rows * sdx::kTbl);
+  *dense = dtype == SDX_F32 ? c.take<float>((size_t)rows * V) : nullptr;
+  *jobs = njobs ? c.take<sdx::SampleJob>(njobs) : nullptr;
+  *sums = njobs ? c.take<uint64_t>((size_t)njobs * nchunk * 2) : nullptr;
+  return c.used;
+}
+
+int check_vocab(int dtype, int64_t V) {
+  if (V < 1) return fail(SDX_EINVAL, "vocab must be >= 1");
+  if (dtype == SDX_F32 && V > sdx::kF32MaxVocab)
+    return fail(SDX_EUNSUPPORTED, "fp32 logits support vocab <= %lld (got %lld)",
+                (long long)sdx::kF32MaxVocab, (long long)V);
+  if (dtype != SDX_F32 && V > kMaxVocab16)
+    return fail(SDX_EUNSUPPORTED, "16-bit logits support vocab <= %lld (got %lld)",
+                (long long)kMaxVocab16, (long long)V);
+  return SDX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* sdx_last_error(void) { return g_err; }
+int sdx_version(void) { return 1; }
+
+// ------------------------------------------------------------------ to_probs
+size_t sdx_to_probs_workspace(int64_t rows, int64_t vocab, int dtype) {
+  Carve c{nullptr};
+  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; uint64_t* sm;
+  // fp32 rows are written straight to the output: no dense scratch
+  transform_ws(c, rows, vocab, dtype == SDX_F32 ? SDX_BF16 : dtype, 0, &st, &tb, &dn, &jb, &sm);
+  return dtype == SDX_F32 ? align256(rows * sizeof(sdx::RowStat)) : c.used;
+}
+
+int sdx_to_probs(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+                 float temperature, float top_p, int32_t top_k, float* probs, int64_t ld_out,
+                 void* workspace, size_t workspace_bytes, sdx_stream_t stream) {
+  if (!logits || !probs || rows < 0 || ld < vocab || ld_out < vocab || !dtype_ok(dtype))
+    return fail(SDX_EINVAL, "sdx_to_probs: bad arguments");
+  if (int e = check_vocab(dtype, vocab)) return e;
+  if (rows == 0) return SDX_OK;
+  const size_t need = sdx_to_probs_workspace(rows, vocab, dtype);
+  if (!workspace || workspace_bytes < need)
+    return fail(SDX_EWORKSPACE, "sdx_to_probs: workspace %zu < %zu", workspace_bytes, need);
+  hipStream_t s = (hipStream_t)stream;
+  const Switches sw = switches(temperature, top_p, top_k, vocab);
+  Carve c{(uint8_t*)workspace};
+  if (dtype == SDX_F32) {
+    sdx::F32Args a = {};
+    a.base[0] = (const float*)logits; a.nrows[0] = rows; a.ld[0] = ld;
+    a.base[1] = a.base[0]; a.nrows[1] = 0; a.ld[1] = ld;
+    a.V = vocab; a.ids = nullptr; a.k = 0;
+    a.T = temperature; a.top_p = top_p; a.top_k = top_k;
+    a.use_p = sw.use_p; a.use_k = sw.use_k; a.greedy = sw.greedy;
+    a.out = probs; a.ld_out = ld_out;
+    a.stats = c.take<sdx::RowStat>(rows);
+    return hip_status(sdx::launch_to_probs_f32(a, rows, s), "to_probs_f32");
+  }
+  if (!aligned16(logits) || (ld % 8) != 0)
+    return fail(SDX_EINVAL, "sdx_to_probs: 16-bit rows must start 16-byte aligned (ld %% 8 == 0)");
+  if (sw.greedy) {
+    int64_t* am = c.take<int64_t>(rows);
+    if (int e = hip_status(sdx::launch_argmax(dtype, logits, rows, vocab, ld, true, am, s), "argmax"))
+      return e;
+    return hip_status(sdx::launch_onehot(am, rows, vocab, probs, ld_out, s), "onehot");
+  }
+  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; uint64_t* sm;
+  transform_ws(c, rows, vocab, dtype, 0, &st, &tb, &dn, &jb, &sm);
+  sdx::RowStatArgs a = {};
+  a.base[0] = (const uint16_t*)logits; a.nrows[0] = rows; a.ld[0] = ld;
+  a.base[1] = a.base[0]; a.nrows[1] = 0; a.ld[1] = ld;
+  a.V = vocab; a.ids = nullptr; a.k = 0;
+  a.T = temperature; a.top_p = top_p; a.top_k = top_k;
+  a.use_p = sw.use_p; a.use_k = sw.use_k; a.greedy = sw.greedy;
+  a.stats = st; a.tables = tb;
+  if (int e = hip_status(sdx::launch_rowstat16(dtype, a, rows, s), "rowstat16")) return e;
+  int64_t chunk;
+  int nchunk;
+  chunking(vocab, &chunk, &nchunk);
+  sdx::RowSource16 src{(const uint16_t*)logits, ld, (const uint16_t*)logits, ld, rows, true};
+  return hip_status(sdx::launch_materialize16(dtype, src, st, tb, temperature, rows, vocab, chunk,
+                                              nchunk, probs, ld_out, s),
+                    "materialize16");
+}
+
+// ------------------------------------------------------------------ sample_from_probs
+size_t sdx_sample_probs_workspace(int64_t rows, int64_t vocab) {
+  int64_t chunk;
+  int nchunk;
+  chunking(vocab, &chunk, &nchunk);
+  Carve c{nullptr};
+  c.take<sdx::SampleJob>(rows);
+  c.take<uint64_t>((size_t)rows * nchunk * 2);
+  return c.used;
+}
+
+__global__ void sdx_jobs_from_u(sdx::SampleJob* jobs, const float* u, int64_t rows,
+                                int64_t qsplit) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  sdx::SampleJob j;
+  j.prow = r;
+  j.qrow = qsplit >= 0 ? qsplit + r : -1;
+  j.u = u ? u[r] : 0.0f;
+  j.pad = 0;
+  jobs[r] = j;
+}
+
+int sdx_sample_probs(const float* probs, int64_t rows, int64_t vocab, int64_t ld, const float* u,
+                     int64_t* ids, void* workspace, size_t workspace_bytes, sdx_stream_t stream) {
+  if (!probs || !u || !ids || rows < 0 || vocab < 1 || ld < vocab)
+    return fail(SDX_EINVAL, "sdx_sample_probs: bad arguments");
+  if (rows == 0) return SDX_OK;
+  const size_t need = sdx_sample_probs_workspace(rows, vocab);
+  if (!workspace || workspace_bytes < need)
+    return fail(SDX_EWORKSPACE, "sdx_sample_probs: workspace %zu < %zu", workspace_bytes, need);
+  hipStream_t s = (hipStream_t)stream;
+  int64_t chunk;
+  int nchunk;
+  chunking(vocab, &chunk, &nchunk);
+  Carve c{(uint8_t*)workspace};
+  sdx::SampleJob* jobs = c.take<sdx::SampleJob>(rows);
+  uint64_t* sums = c.take<uint64_t>((size_t)rows * nchunk * 2);
+  hipLaunchKernelGGL(sdx_jobs_from_u, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, jobs,
+                     u, rows, (int64_t)-1);
+  if (int e = hip_status(hipGetLastError(), "jobs")) return e;
+  const bool vec = aligned16(probs) && (ld % 4) == 0;
+  sdx::RowSourceF32 src{probs, ld, probs, ld, rows, vec};
+  return hip_status(sdx::launch_draw_probs(src, jobs, rows, vocab, chunk, nchunk, sums, ids, s),
+                    "draw_probs");
+}
+
+// ------------------------------------------------------------------ residual_probs
+size_t sdx_residual_probs_workspace(int64_t rows, int64_t vocab) {
+  return sdx_sample_probs_workspace(rows, vocab);
+}
+
+int sdx_residual_probs(const float* p, const float* q, int64_t rows, int64_t vocab, int64_t ld,
+                       float* out, int64_t ld_out, void* workspace, size_t workspace_bytes,
+                       sdx_stream_t stream) {
+  if (!p || !q || !out || rows < 0 || vocab < 1 || ld < vocab || ld_out < vocab)
+    return fail(SDX_EINVAL, "sdx_residual_probs: bad arguments");
+  if (rows == 0) return SDX_OK;
+  const size_t need = sdx_residual_probs_workspace(rows, vocab);
+  if (!workspace || workspace_bytes < need)
+    return fail(SDX_EWORKSPACE, "sdx_residual_probs: workspace %zu < %zu", workspace_bytes, need);
+  hipStream_t s = (hipStream_t)stream;
+  int64_t chunk;
+  int nchunk;
+  chunking(vocab, &chunk, &nchunk);
+  Carve c{(uint8_t*)workspace};
+  sdx::SampleJob* jobs = c.take<sdx::SampleJob>(rows);
+  uint64_t* sums = c.take<uint64_t>((size_t)rows * nchunk * 2);
+  hipLaunchKernelGGL(sdx_jobs_from_u, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, jobs,
+                     (const float*)nullptr, rows, rows);
+  if (int e = hip_status(hipGetLastError(), "jobs")) return e;
+  const bool vec = aligned16(p) && aligned16(q) && (ld % 4) == 0;
+  sdx::RowSourceF32 src{p, ld, q, ld, rows, vec};
+  if (int e = hip_status(sdx::launch_chunk_mass_probs(src, jobs, rows, vocab, chunk, nchunk, sums, s),
+                         "chunk_mass"))
+    return e;
+  sdx::ResidualNormArgs a{p, q, ld, vocab, chunk, nchunk, sums, out, ld_out};
+  return hip_status(sdx::launch_residual_norm(a, rows, s), "residual_norm");
+}
+
+// ------------------------------------------------------------------ gather_prob
+int sdx_gather_prob(const float* probs, int64_t rows, int64_t vocab, int64_t ld, const int64_t* ids,
+                    float* out, sdx_stream_t stream) {
+  if (!probs || !ids || !out || rows < 0 || vocab < 1 || ld < vocab)
+    return fail(SDX_EINVAL, "sdx_gather_prob: bad arguments");
+  if (rows == 0) return SDX_OK;
+  return hip_status(sdx::launch_gather(probs, rows, vocab, ld, ids, out, (hipStream_t)stream),
+                    "gather");
+}
+
+// ------------------------------------------------------------------ verify
+size_t sdx_verify_workspace(int64_t batch, int32_t k, int64_t vocab, int dtype) {
+  Carve c{nullptr};
+  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; uint64_t* sm;
+  const int64_t rows = batch * (2 * (int64_t)k + 1);
+  transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jb, &sm);
+  c.take<int64_t>(batch * ((int64_t)k + 1));  // greedy argmax
+  return c.used;
+}
+
+int sdx_verify(const void* target_logits, const void* draft_logits, int dtype, int64_t batch,
+               int32_t k, int64_t vocab, const int64_t* draft_ids, const float* u_accept,
+               const float* u_final, const uint8_t* active, float temperature, float top_p,
+               int32_t top_k, int64_t* n_acc, int64_t* y, uint8_t* flags, void* workspace,
+               size_t workspace_bytes, sdx_stream_t stream) {
+  if (!target_logits || !draft_ids || !u_accept || !u_final || !n_acc || !y || !flags ||
+      batch < 0 || k < 1 || !dtype_ok(dtype))
+    return fail(SDX_EINVAL, "sdx_verify: bad arguments");
+  if (int e = check_vocab(dtype, vocab)) return e;
+  if (batch == 0) return SDX_OK;
+  const size_t need = sdx_verify_workspace(batch, k, vocab, dtype);
+  if (!workspace || workspace_bytes < need)
+    return fail(SDX_EWORKSPACE, "sdx_verify: workspace %zu < %zu", workspace_bytes, need);
+  hipStream_t s = (hipStream_t)stream;
+  const Switches sw = switches(temperature, top_p, top_k, vocab);
+  Carve c{(uint8_t*)workspace};
+  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jobs; uint64_t* sums;
+  const int64_t ntgt = batch * ((int64_t)k + 1), ndrf = batch * (int64_t)k;
+  const int64_t rows = ntgt + ndrf;
+  transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jobs, &sums);
+  int64_t* am = c.take<int64_t>(ntgt);
+  if (sw.greedy) {
+    // one-hot p: only the target argmax matters (see sdx_verify_greedy)
+    const bool vec = aligned16(target_logits) && (vocab % (dtype == SDX_F32 ? 4 : 8)) == 0;
+    if (int e = hip_status(sdx::launch_argmax(dtype, target_logits, ntgt, vocab, vocab, vec, am, s),
+                           "argmax"))
+      return e;
+    return hip_status(sdx::launch_greedy_accept(am, batch, k, draft_ids, u_accept, active, n_acc,
+                                                y, flags, s),
+                      "greedy_accept");
+  }
+  if (!draft_logits) return fail(SDX_EINVAL, "sdx_verify: draft_logits required when T > 0");
+  int64_t chunk;
+  int nchunk;
+  chunking(vocab, &chunk, &nchunk);
+  if (dtype == SDX_F32) {
+    sdx::F32Args a = {};
+    a.base[0] = (const float*)target_logits; a.nrows[0] = ntgt; a.ld[0] = vocab;
+    a.base[1] = (const float*)draft_logits; a.nrows[1] = ndrf; a.ld[1] = vocab;
+    a.V = vocab; a.ids = draft_ids; a.k = k;
+    a.T = temperature; a.top_p = top_p; a.top_k = top_k;
+    a.use_p = sw.use_p; a.use_k = sw.use_k; a.greedy = 0;
+    a.out = dn; a.ld_out = vocab; a.stats = st;
+    if (int e = hip_status(sdx::launch_to_probs_f32(a, rows, s), "to_probs_f32")) return e;
+  } else {
+    if (!aligned16(target_logits) || !aligned16(draft_logits) || (vocab % 8) != 0)
+      return fail(SDX_EINVAL,
+                  "sdx_verify: 16-bit logits must be 16-byte aligned with vocab %% 8 == 0");
+    sdx::RowStatArgs a = {};
+    a.base[0] = (const uint16_t*)target_logits; a.nrows[0] = ntgt; a.ld[0] = vocab;
+    a.base[1] = (const uint16_t*)draft_logits; a.nrows[1] = ndrf; a.ld[1] = vocab;
+    a.V = vocab; a.ids = draft_ids; a.k = k;
+    a.T = temperature; a.top_p = top_p; a.top_k = top_k;
+    a.use_p = sw.use_p; a.use_k = sw.use_k; a.greedy = 0;
+    a.stats = st; a.tables = tb;
+    if (int e = hip_status(sdx::launch_rowstat16(dtype, a, rows, s), "rowstat16")) return e;
+  }
+  sdx::AcceptArgs aa{st, batch, k, u_accept, u_final, active, jobs, n_acc, flags};
+  if (int e = hip_status(sdx::launch_accept(aa, s), "accept")) return e;
+  if (dtype == SDX_F32) {
+    sdx::RowSourceF32 src{dn, vocab, dn, vocab, rows, (vocab % 4) == 0};
+    return hip_status(sdx::launch_draw_probs(src, jobs, batch, vocab, chunk, nchunk, sums, y, s),
+                      "draw_probs");
+  }
+  sdx::RowSource16 src{(const uint16_t*)target_logits, vocab, (const uint16_t*)draft_logits, vocab,
+                       ntgt, true};
+  return hip_status(sdx::launch_draw16(dtype, src, st, tb, temperature, jobs, batch, vocab, chunk,
+                                       nchunk, sums, y, s),
+                    "draw16");
+}
+
+size_t sdx_verify_greedy_workspace(int64_t batch, int32_t k) {
+  return align256((size_t)batch * ((size_t)k + 1) * sizeof(int64_t));
+}
+
+int sdx_verify_greedy(const void* target_logits, int dtype, int64_t batch, int32_t k,
+                      int64_t vocab, const int64_t* draft_ids, const float* u_accept,
+                      const uint8_t* active, int64_t* n_acc, int64_t* y, uint8_t* flags,
+                      void* workspace, size_t workspace_bytes, sdx_stream_t stream) {
+  if (!target_logits || !draft_ids || !n_acc || !y || !flags || batch < 0 || k < 1 ||
+      vocab < 1 || !dtype_ok(dtype))
+    return fail(SDX_EINVAL, "sdx_verify_greedy: bad arguments");
+  if (batch == 0) return SDX_OK;
+  const size_t need = sdx_verify_greedy_workspace(batch, k);
+  if (!workspace || workspace_bytes < need)
+    return fail(SDX_EWORKSPACE, "sdx_verify_greedy: workspace %zu < %zu", workspace_bytes, need);
+  hipStream_t s = (hipStream_t)stream;
+  int64_t* am = (int64_t*)workspace;
+  const int64_t ntgt = batch * ((int64_t)k + 1);
+  const bool vec = aligned16(target_logits) && (vocab % (dtype == SDX_F32 ? 4 : 8)) == 0;
+  if (int e = hip_status(sdx::launch_argmax(dtype, target_logits, ntgt, vocab, vocab, vec, am, s),
+                         "argmax"))
+    return e;
+  return hip_status(
+      sdx::launch_greedy_accept(am, batch, k, draft_ids, u_accept, active, n_acc, y, flags, s),
+      "greedy_accept");
+}
+
+// ------------------------------------------------------------------ proposer
+int sdx_argmax(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+               int64_t* ids, sdx_stream_t stream) {
+  if (!logits || !ids || rows < 0 || vocab < 1 || ld < vocab || !dtype_ok(dtype))
+    return fail(SDX_EINVAL, "sdx_argmax: bad arguments");
+  if (rows == 0) return SDX_OK;
+  const bool vec = aligned16(logits) && (ld % (dtype == SDX_F32 ? 4 : 8)) == 0;
+  return hip_status(sdx::launch_argmax(dtype, logits, rows, vocab, ld, vec, ids, (hipStream_t)stream),
+                    "argmax");
+}
+
+int sdx_slot_mapping(const int32_t* block_table, int64_t rows, int64_t max_blocks,
+                     const int64_t* positions, int32_t block_size, int64_t max_model_len,
+                     int64_t padding_slot, int64_t* clamped_positions, int64_t* slots,
+                     sdx_stream_t stream) {
+  if (!block_table || !positions || !slots || rows < 0 || max_blocks < 1 || block_size < 1)
+    return fail(SDX_EINVAL, "sdx_slot_mapping: bad arguments");
+  if (rows == 0) return SDX_OK;
+  return hip_status(sdx::launch_slot_mapping(block_table, rows, max_blocks, positions, block_size,
+                                             max_model_len, padding_slot, clamped_positions, slots,
+                                             (hipStream_t)stream),
+                    "slot_mapping");
+}
+
+// ------------------------------------------------------------------ KV cache
+int sdx_kv_advance(int64_t* lengths, int64_t batch, int64_t q, sdx_stream_t stream) {
+  if (!lengths || batch < 0) return fail(SDX_EINVAL, "sdx_kv_advance: bad arguments");
+  if (batch == 0) return SDX_OK;
+  return hip_status(sdx::launch_kv_advance(lengths, batch, q, (hipStream_t)stream), "kv_advance");
+}
+
+int sdx_kv_rollback(int64_t* lengths, int64_t batch, const int64_t* n, int32_t* error,
+                    sdx_stream_t stream) {
+  if (!lengths || !n || batch < 0) return fail(SDX_EINVAL, "sdx_kv_rollback: bad arguments");
+  if (batch == 0) return SDX_OK;
+  return hip_status(sdx::launch_kv_rollback(lengths, batch, n, error, (hipStream_t)stream),
+                    "kv_rollback");
+}
+
+int sdx_ragged_update(void* keys, void* values, const void* k_new, const void* v_new, int dtype,
+                      int64_t batch, int64_t heads, int64_t capacity, int64_t head_dim, int64_t q,
+                      const int64_t* lengths, int32_t* error, sdx_stream_t stream) {
+  if (!keys || !values || !k_new || !v_new || !lengths || !dtype_ok(dtype) || batch < 0 ||
+      heads < 1 || capacity < 1 || head_dim < 1 || q < 0)
+    return fail(SDX_EINVAL, "sdx_ragged_update: bad arguments");
+  if (batch == 0 || q == 0) return SDX_OK;
+  return hip_status(sdx::launch_ragged_update(dtype, keys, values, k_new, v_new, batch, heads,
+                                              capacity, head_dim, q, lengths, error,
+                                              (hipStream_t)stream),
+                    "ragged_update");
+}
+
+int sdx_attn_mask(const int64_t* lengths, const int64_t* valid, int64_t batch, int64_t q,
+                  int64_t kv_len, float neg, int dtype, void* out, sdx_stream_t stream) {
+  if (!lengths || !out || batch < 0 || q < 0 || kv_len < 0 || !dtype_ok(dtype))
+    return fail(SDX_EINVAL, "sdx_attn_mask: bad arguments");
+  if (batch * q * kv_len == 0) return SDX_OK;
+  return hip_status(
+      sdx::launch_attn_mask(lengths, valid, batch, q, kv_len, neg, dtype, out, (hipStream_t)stream),
+      "attn_mask");
+}
+
+int sdx_kv_append_paged(void* pool, int64_t layer_stride, int64_t side_stride, const void* staged,
+                        int dtype, int32_t layers, int64_t batch, int64_t q, int64_t row_elems,
+                        const int32_t* block_table, int64_t max_blocks, int32_t block_size,
+                        int64_t num_blocks, const int64_t* lengths, int32_t* error,
+                        sdx_stream_t stream) {
+  if (!pool || !staged || !block_table || !lengths || !dtype_ok(dtype) || layers < 1 ||
+      batch < 0 || q < 0 || row_elems < 1 || max_blocks < 1 || block_size < 1 || num_blocks < 1)
+    return fail(SDX_EINVAL, "sdx_kv_append_paged: bad arguments");
+  const int64_t es = (int64_t)dsize(dtype);
+  if ((row_elems * es) % 16 != 0 || !aligned16(pool) || !aligned16(staged) ||
+      (layer_stride * es) % 16 != 0 || (side_stride * es) % 16 != 0)
+    return fail(SDX_EINVAL, "sdx_kv_append_paged: rows and strides must be 16-byte multiples");
+  if (batch == 0 || q == 0) return SDX_OK;
+  return hip_status(sdx::launch_kv_append_paged(pool, layer_stride * es, side_stride * es, staged,
+                                                layers, batch, q, row_elems * es, block_table,
+                                                max_blocks, block_size, num_blocks, lengths, error,
+                                                (hipStream_t)stream),
+                    "kv_append_paged");
+}
+
+}  // extern "C"

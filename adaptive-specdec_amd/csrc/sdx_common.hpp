@@ -1,0 +1,223 @@
+// Shared device code for the gfx950 verify path: 16-bit logit keys, the
+// deterministic exp / fixed-point rules, and wave64 reductions.
+//
+// The arithmetic here is restated, operation for operation, by the numpy
+// oracle; every routine that feeds a discrete decision uses only IEEE
+// operations (no FMA contraction, correctly rounded fp32 division) so the two
+// agree bit for bit.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/specdec_amd.h"
+
+namespace sdx {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- 16-bit keys
+// bf16 and fp16 are sign-magnitude: flipping all bits of negatives and the
+// sign bit of positives gives an unsigned key whose order is the value order
+// (-0 sorts just below +0; key 0 is the all-ones code, a negative NaN, which
+// this build treats as padding/ignored).
+__device__ __forceinline__ uint32_t key_of_code16(uint32_t c) {
+  return (c & 0x8000u) ? (~c & 0xFFFFu) : (c | 0x8000u);
+}
+__device__ __forceinline__ uint32_t code_of_key16(uint32_t k) {
+  return (k & 0x8000u) ? (k & 0x7FFFu) : (~k & 0xFFFFu);
+}
+// Two packed codes -> two packed keys.
+__device__ __forceinline__ uint32_t keys2_of_codes2(uint32_t w) {
+  const uint32_t neg = (w >> 15) & 0x00010001u;  // sign of each half at bit 0 / 16
+  return w ^ ((neg * 0x7FFFu) | 0x80008000u);
+}
+
+template <int FMT>
+__device__ __forceinline__ float decode16(uint32_t code) {
+  if constexpr (FMT == SDX_BF16) {
+    return __uint_as_float(code << 16);
+  } else {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)code);
+  }
+}
+// Key of +inf: keys at or above it are +inf / +NaN.
+template <int FMT>
+constexpr uint32_t kPosInfKey = FMT == SDX_BF16 ? 0xFF80u : 0xFC00u;
+
+// 32-bit key for fp32 logits (same construction).
+__device__ __forceinline__ uint32_t key_of_f32(float x) {
+  const uint32_t b = __float_as_uint(x);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// ---------------------------------------------------------------- exp_det
+// fp32 exp(d): Cody-Waite reduction and a degree-13 Taylor polynomial in
+// float64 with plain multiply/add, one rounding to fp32 at the end; 0 below
+// -104 (under half the smallest fp32 denormal).
+__device__ __forceinline__ float exp_det(float d) {
+#pragma clang fp contract(off)
+  if (!(d >= -104.0f)) return 0.0f;
+  const double kInvLn2 = 0x1.71547652b82fep+0;
+  const double kLn2Hi = 0x1.62e42fee00000p-1;
+  const double kLn2Lo = 0x1.a39ef35793c76p-33;
+  const double dd = (double)d;
+  const double k = rint(dd * kInvLn2);
+  const double r = (dd - k * kLn2Hi) - k * kLn2Lo;
+  double p = 0x1.6124613a86d09p-33;
+  p = p * r + 0x1.1eed8eff8d898p-29;
+  p = p * r + 0x1.ae64567f544e4p-26;
+  p = p * r + 0x1.27e4fb7789f5cp-22;
+  p = p * r + 0x1.71de3a556c734p-19;
+  p = p * r + 0x1.a01a01a01a01ap-16;
+  p = p * r + 0x1.a01a01a01a01ap-13;
+  p = p * r + 0x1.6c16c16c16c17p-10;
+  p = p * r + 0x1.1111111111111p-7;
+  p = p * r + 0x1.5555555555555p-5;
+  p = p * r + 0x1.5555555555555p-3;
+  p = p * r + 0x1.0000000000000p-1;
+  p = p * r + 0x1.0000000000000p+0;
+  p = p * r + 0x1.0000000000000p+0;
+  return (float)ldexp(p, (int)k);
+}
+
+// ---------------------------------------------------------------- fixed point
+// floor(x * 2^62) for fp32 x in [0, 1].
+__device__ __forceinline__ uint64_t fixed62(float x) {
+  const uint32_t b = __float_as_uint(x);
+  const uint32_t e = b >> 23;
+  const uint64_t mant = (uint64_t)((b & 0x7FFFFFu) | (e ? 0x800000u : 0u));
+  const int sh = (int)(e ? e : 1u) - 88;  // value = mant * 2^(eff - 150)
+  if (sh >= 0) return mant << sh;
+  if (sh <= -64) return 0;
+  return mant >> (-sh);
+}
+
+// i * 2^-62 rounded once to fp32 (nearest, ties to even).
+__device__ __forceinline__ float rn32_u64(uint64_t i) {
+  if (i == 0) return 0.0f;
+  const int nb = 64 - __clzll((long long)i);
+  int shift = nb - 24;
+  if (shift <= 0) return ldexpf((float)(uint32_t)i, -62);
+  uint64_t mant = i >> shift;
+  const uint64_t rem = i & ((1ull << shift) - 1);
+  const uint64_t half = 1ull << (shift - 1);
+  if (rem > half || (rem == half && (mant & 1))) {
+    ++mant;
+    if (mant == (1ull << 24)) {
+      mant >>= 1;
+      ++shift;
+    }
+  }
+  return ldexpf((float)(uint32_t)mant, shift - 62);
+}
+
+// 128-bit unsigned accumulator as two words (hi:lo).
+struct U128 {
+  uint64_t lo, hi;
+};
+__device__ __forceinline__ U128 u128_add(U128 a, U128 b) {
+  U128 r;
+  r.lo = a.lo + b.lo;
+  r.hi = a.hi + b.hi + (r.lo < a.lo ? 1 : 0);
+  return r;
+}
+// c * f with c < 2^32, f < 2^64.
+__device__ __forceinline__ U128 u128_mul32(uint32_t c, uint64_t f) {
+  const uint64_t lo = (uint64_t)c * (uint32_t)f;
+  const uint64_t mid = (uint64_t)c * (uint32_t)(f >> 32);
+  U128 r;
+  r.lo = lo + (mid << 32);
+  r.hi = (mid >> 32) + (r.lo < lo ? 1 : 0);
+  return r;
+}
+__device__ __forceinline__ float rn32_u128(U128 v) {
+  if (v.hi == 0) return rn32_u64(v.lo);
+  const int nb = 128 - __clzll((long long)v.hi);
+  int shift = nb - 24;  // > 40
+  // mantissa = v >> shift (fits in 24 bits)
+  uint64_t mant = (shift >= 64) ? (v.hi >> (shift - 64))
+                                : ((v.hi << (64 - shift)) | (v.lo >> shift));
+  // remainder vs half: bit (shift-1) and the bits below it
+  const int hb = shift - 1;
+  const uint64_t halfbit = hb >= 64 ? ((v.hi >> (hb - 64)) & 1) : ((v.lo >> hb) & 1);
+  bool below_nonzero;
+  if (hb >= 64) {
+    const int h2 = hb - 64;
+    below_nonzero = v.lo != 0 || (h2 > 0 && (v.hi & ((1ull << h2) - 1)) != 0);
+  } else {
+    below_nonzero = hb > 0 && (v.lo & ((1ull << hb) - 1)) != 0;
+  }
+  if (halfbit && (below_nonzero || (mant & 1))) {
+    ++mant;
+    if (mant == (1ull << 24)) {
+      mant >>= 1;
+      ++shift;
+    }
+  }
+  return ldexpf((float)(uint32_t)mant, shift - 62);
+}
+
+// floor(u * total) for fp32 u in [0, 1): the inverse-CDF target.
+__device__ __forceinline__ uint64_t uniform_threshold(float u, uint64_t total) {
+  const uint32_t b = __float_as_uint(u);
+  if ((b & 0x7FFFFFFFu) == 0) return 0;
+  const uint32_t e = b >> 23;
+  const uint32_t mant = (b & 0x7FFFFFu) | (e ? 0x800000u : 0u);
+  const int s = 150 - (int)(e ? e : 1u);  // u = mant * 2^-s, s >= 24
+  const U128 prod = u128_mul32(mant, total);
+  if (s >= 128) return 0;
+  if (s >= 64) return prod.hi >> (s - 64);
+  return (prod.lo >> s) | (prod.hi << (64 - s));
+}
+
+// ---------------------------------------------------------------- reductions
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, kWave));
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += (uint64_t)__shfl_xor((long long)v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ int64_t wave_min_i64(int64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, (int64_t)__shfl_xor((long long)v, o, kWave));
+  return v;
+}
+__device__ __forceinline__ U128 wave_sum_u128(U128 v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    U128 w;
+    w.lo = (uint64_t)__shfl_xor((long long)v.lo, o, kWave);
+    w.hi = (uint64_t)__shfl_xor((long long)v.hi, o, kWave);
+    v = u128_add(v, w);
+  }
+  return v;
+}
+// Inclusive prefix sum across the 64 lanes.
+__device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v, int lane) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint64_t t = (uint64_t)__shfl_up((long long)v, o, kWave);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v, int lane) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t t = (uint32_t)__shfl_up((int)v, o, kWave);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+}  // namespace sdx

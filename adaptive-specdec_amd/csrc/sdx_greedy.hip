@@ -1,0 +1,149 @@
+// Greedy paths: row argmax (vllm_draft_spec/proposer.py:262-263,331-332 and the
+// T = 0 one-hot of specdec/sampling.py:43-48) and the greedy verify that
+// follows from it (specdec/engine.py:285-303 with one-hot p).
+//
+// A row is scanned with 16-byte loads; each lane keeps the best
+// (key, first index) pair packed as (key << 32) | ~index so one max reduction
+// gives the largest value and, among equal values, the lowest index. -0 is
+// folded onto +0 so equal values compare equal, as torch.argmax does.
+#include "sdx_launch.hpp"
+
+namespace sdx {
+
+constexpr int AM_NT = 512;
+
+template <int DT>
+__device__ __forceinline__ uint64_t pack_best(uint32_t key, int64_t idx) {
+  return ((uint64_t)key << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)idx);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(AM_NT) argmax_kernel(const void* data, int64_t V, int64_t ld,
+                                                       bool vec, int64_t* out) {
+  __shared__ uint64_t red[AM_NT / kWave];
+  const int64_t row = blockIdx.x;
+  uint64_t best = 0;
+  if constexpr (DT == SDX_F32) {
+    const float* p = static_cast<const float*>(data) + row * ld;
+    for (int64_t i0 = (int64_t)threadIdx.x * 4; i0 < V; i0 += (int64_t)AM_NT * 4) {
+      float x[4];
+      if (vec && i0 + 4 <= V) {
+        const float4 v = *reinterpret_cast<const float4*>(p + i0);
+        x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+      } else {
+        for (int t = 0; t < 4; ++t) x[t] = i0 + t < V ? p[i0 + t] : -INFINITY;
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (i0 + t < V) {
+          uint32_t k = key_of_f32(x[t]);
+          if (k == 0x7FFFFFFFu) k = 0x80000000u;  // -0 == +0
+          const uint64_t c = pack_best<DT>(k, i0 + t);
+          best = c > best ? c : best;
+        }
+      }
+    }
+  } else {
+    const uint16_t* p = static_cast<const uint16_t*>(data) + row * ld;
+    for (int64_t i0 = (int64_t)threadIdx.x * 8; i0 < V; i0 += (int64_t)AM_NT * 8) {
+      uint32_t w[4];
+      if (vec && i0 + 8 <= V) {
+        const uint4 v = *reinterpret_cast<const uint4*>(p + i0);
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+      } else {
+        for (int t = 0; t < 4; ++t) {
+          const uint32_t c0 = i0 + 2 * t < V ? p[i0 + 2 * t] : 0xFFFFu;
+          const uint32_t c1 = i0 + 2 * t + 1 < V ? p[i0 + 2 * t + 1] : 0xFFFFu;
+          w[t] = c0 | (c1 << 16);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        if (i0 + t < V) {
+          const uint32_t code = (t & 1) ? (w[t >> 1] >> 16) : (w[t >> 1] & 0xFFFFu);
+          uint32_t k = key_of_code16(code);
+          if (k == 0x7FFFu) k = 0x8000u;  // -0 == +0
+          const uint64_t c = pack_best<DT>(k, i0 + t);
+          best = c > best ? c : best;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint64_t v = (uint64_t)__shfl_xor((long long)best, o, kWave);
+    best = v > best ? v : best;
+  }
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t b = 0;
+    for (int w = 0; w < AM_NT / kWave; ++w) b = red[w] > b ? red[w] : b;
+    out[row] = (int64_t)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFu));
+  }
+}
+
+// Greedy accept: argmax of target rows [batch, k+1] already in `am`.
+__global__ void greedy_accept_kernel(const int64_t* am, int64_t batch, int32_t k,
+                                     const int64_t* ids, const float* u_accept,
+                                     const uint8_t* active, int64_t* n_acc, int64_t* y,
+                                     uint8_t* flags) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  bool alive = active ? active[b] != 0 : true;
+  int n = 0;
+  uint32_t fl = 0;
+  for (int i = 0; i < k; ++i) {
+    // p is one-hot at the argmax, q(x) = 1: ratio = p(x) in {0, 1}
+    const float r1 = ids[b * k + i] == am[b * (k + 1) + i] ? 1.0f : 0.0f;
+    const float u = u_accept ? u_accept[b * k + i] : 0.0f;
+    const bool evaluated = alive && n == i;
+    const bool ok = evaluated && (u < r1);
+    if (evaluated && fabsf(u - r1) < 1e-5f) fl |= SDX_FLAG_ACCEPT_NEAR_TIE;
+    n += ok ? 1 : 0;
+    alive = alive && ok;
+  }
+  n_acc[b] = n;
+  y[b] = am[b * (k + 1) + n];
+  flags[b] = (uint8_t)fl;
+}
+
+// Greedy to_probs output: one-hot at the row argmax (sampling.py:46-48).
+__global__ void onehot_kernel(const int64_t* am, int64_t V, int64_t per_row, float* out,
+                              int64_t ld_out) {
+  const int64_t row = (int64_t)blockIdx.x / per_row;
+  const int64_t i = ((int64_t)blockIdx.x % per_row) * blockDim.x + threadIdx.x;
+  if (i < V) out[row * ld_out + i] = i == am[row] ? 1.0f : 0.0f;
+}
+
+hipError_t launch_onehot(const int64_t* am, int64_t rows, int64_t V, float* out, int64_t ld_out,
+                         hipStream_t s) {
+  const int nt = 256;
+  const int64_t per_row = (V + nt - 1) / nt;
+  hipLaunchKernelGGL(onehot_kernel, dim3((unsigned)(per_row * rows)), dim3(nt), 0, s, am, V,
+                     per_row, out, ld_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_argmax(int dtype, const void* data, int64_t rows, int64_t V, int64_t ld,
+                         bool vec, int64_t* out, hipStream_t s) {
+  const dim3 grid((unsigned)rows), block(AM_NT);
+  if (dtype == SDX_F32)
+    hipLaunchKernelGGL((argmax_kernel<SDX_F32>), grid, block, 0, s, data, V, ld, vec, out);
+  else if (dtype == SDX_BF16)
+    hipLaunchKernelGGL((argmax_kernel<SDX_BF16>), grid, block, 0, s, data, V, ld, vec, out);
+  else
+    hipLaunchKernelGGL((argmax_kernel<SDX_F16>), grid, block, 0, s, data, V, ld, vec, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_greedy_accept(const int64_t* am, int64_t batch, int32_t k, const int64_t* ids,
+                                const float* u_accept, const uint8_t* active, int64_t* n_acc,
+                                int64_t* y, uint8_t* flags, hipStream_t s) {
+  const int nt = 128;
+  hipLaunchKernelGGL(greedy_accept_kernel, dim3((unsigned)((batch + nt - 1) / nt)), dim3(nt), 0,
+                     s, am, batch, k, ids, u_accept, active, n_acc, y, flags);
+  return hipGetLastError();
+}
+
+}  // namespace sdx

@@ -1,0 +1,121 @@
+// Kernel argument records and launch entry points shared between the kernel
+// translation units and the C-ABI layer (sdx_capi.hip).
+#pragma once
+
+#include "sdx_internal.hpp"
+
+namespace sdx {
+
+struct RowStatArgs {
+  const uint16_t* base[2];  // group 0: target rows, group 1: draft rows
+  int64_t nrows[2];
+  int64_t ld[2];
+  int64_t V;
+  const int64_t* ids;  // draft ids [batch, k] (gather source), or null
+  int32_t k;           // target rows are [batch, k+1], draft rows [batch, k]
+  float T;
+  float top_p;
+  int32_t top_k;
+  int32_t use_p, use_k, greedy;
+  RowStat* stats;
+  float* tables;  // [rows, kTbl]
+};
+
+struct F32Args {
+  const float* base[2];
+  int64_t nrows[2];
+  int64_t ld[2];
+  int64_t V;
+  const int64_t* ids;
+  int32_t k;
+  float T, top_p;
+  int32_t top_k, use_p, use_k, greedy;
+  float* out;  // dense probabilities [rows, ld_out]
+  int64_t ld_out;
+  RowStat* stats;  // may be null
+};
+
+// One final draw: weights from row `prow` (and `qrow` for a residual).
+struct SampleJob {
+  int64_t prow;     // row whose probabilities are p
+  int64_t qrow;     // row of q for a residual draw, -1 for a draw from p
+  float u;          // the uniform
+  int32_t pad;
+};
+
+struct AcceptArgs {
+  const RowStat* stats;  // target rows [batch*(k+1)] then draft rows [batch*k]
+  int64_t batch;
+  int32_t k;
+  const float* u_accept;  // [batch, k]
+  const float* u_final;   // [batch]
+  const uint8_t* active;  // [batch] or null
+  SampleJob* jobs;        // [batch]
+  int64_t* n_acc;
+  uint8_t* flags;
+};
+
+struct ResidualNormArgs {
+  const float* p;
+  const float* q;
+  int64_t ld;
+  int64_t V;
+  int64_t chunk;
+  int32_t nchunk;
+  const uint64_t* sums;  // chunk masses of jobs (one job per row)
+  float* out;
+  int64_t ld_out;
+};
+
+// sdx_rowstat.hip
+int rowstat16_nslot(int64_t V);
+hipError_t launch_rowstat16(int fmt, const RowStatArgs& a, int64_t rows, hipStream_t s);
+// sdx_f32.hip
+constexpr int64_t kF32MaxVocab = 8192;
+hipError_t launch_to_probs_f32(const F32Args& a, int64_t rows, hipStream_t s);
+// sdx_sample.hip
+hipError_t launch_accept(const AcceptArgs& a, hipStream_t s);
+hipError_t launch_draw16(int fmt, const RowSource16& src, const RowStat* stats,
+                         const float* tables, float T, const SampleJob* jobs, int64_t njobs,
+                         int64_t V, int64_t chunk, int nchunk, uint64_t* sums, int64_t* y,
+                         hipStream_t s);
+hipError_t launch_draw_probs(const RowSourceF32& src, const SampleJob* jobs, int64_t njobs,
+                             int64_t V, int64_t chunk, int nchunk, uint64_t* sums, int64_t* y,
+                             hipStream_t s);
+hipError_t launch_chunk_mass_probs(const RowSourceF32& src, const SampleJob* jobs, int64_t njobs,
+                                   int64_t V, int64_t chunk, int nchunk, uint64_t* sums,
+                                   hipStream_t s);
+hipError_t launch_materialize16(int fmt, const RowSource16& src, const RowStat* stats,
+                                const float* tables, float T, int64_t rows, int64_t V,
+                                int64_t chunk, int nchunk, float* out, int64_t ld_out,
+                                hipStream_t s);
+hipError_t launch_residual_norm(const ResidualNormArgs& a, int64_t rows, hipStream_t s);
+hipError_t launch_gather(const float* probs, int64_t rows, int64_t V, int64_t ld,
+                         const int64_t* ids, float* out, hipStream_t s);
+// sdx_greedy.hip
+hipError_t launch_argmax(int dtype, const void* data, int64_t rows, int64_t V, int64_t ld,
+                         bool vec, int64_t* out, hipStream_t s);
+hipError_t launch_onehot(const int64_t* am, int64_t rows, int64_t V, float* out, int64_t ld_out,
+                         hipStream_t s);
+hipError_t launch_greedy_accept(const int64_t* am, int64_t batch, int32_t k, const int64_t* ids,
+                                const float* u_accept, const uint8_t* active, int64_t* n_acc,
+                                int64_t* y, uint8_t* flags, hipStream_t s);
+// sdx_kv.hip
+hipError_t launch_kv_advance(int64_t* lengths, int64_t batch, int64_t q, hipStream_t s);
+hipError_t launch_kv_rollback(int64_t* lengths, int64_t batch, const int64_t* n, int32_t* error,
+                              hipStream_t s);
+hipError_t launch_ragged_update(int dtype, void* keys, void* values, const void* kn,
+                                const void* vn, int64_t B, int64_t H, int64_t C, int64_t D,
+                                int64_t q, const int64_t* lengths, int32_t* error, hipStream_t s);
+hipError_t launch_attn_mask(const int64_t* lengths, const int64_t* valid, int64_t B, int64_t q,
+                            int64_t kv, float neg, int dtype, void* out, hipStream_t s);
+hipError_t launch_kv_append_paged(void* pool, int64_t layer_stride_b, int64_t side_stride_b,
+                                  const void* staged, int32_t layers, int64_t batch, int64_t q,
+                                  int64_t row_bytes, const int32_t* bt, int64_t max_blocks,
+                                  int32_t bs, int64_t num_blocks, const int64_t* lengths,
+                                  int32_t* error, hipStream_t s);
+hipError_t launch_slot_mapping(const int32_t* bt, int64_t rows, int64_t max_blocks,
+                               const int64_t* positions, int32_t bs, int64_t max_len,
+                               int64_t pad_slot, int64_t* clamped, int64_t* slots, hipStream_t s);
+
+}  // namespace sdx

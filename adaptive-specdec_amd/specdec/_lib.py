@@ -1,0 +1,109 @@
+"""ctypes binding of libspecdec_amd.so (the C ABI in include/specdec_amd.h).
+
+The library is built in-tree by `adaptive-specdec_amd/build.py` (or
+`__graft_entry__.build()`). There is no fallback: if it is missing, or a tensor
+is not on a ROCm device, calls raise.
+"""
+import ctypes
+import os
+
+import torch
+
+_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libspecdec_amd.so")
+_LIB = None
+
+F32, BF16, F16 = 0, 1, 2
+_DTYPE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+P = ctypes.c_void_p
+I64 = ctypes.c_int64
+I32 = ctypes.c_int32
+F = ctypes.c_float
+SZ = ctypes.c_size_t
+INT = ctypes.c_int
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "sdx_last_error": (ctypes.c_char_p, []),
+    "sdx_version": (INT, []),
+    "sdx_to_probs_workspace": (SZ, [I64, I64, INT]),
+    "sdx_to_probs": (INT, [P, INT, I64, I64, I64, F, F, I32, P, I64, P, SZ, P]),
+    "sdx_sample_probs_workspace": (SZ, [I64, I64]),
+    "sdx_sample_probs": (INT, [P, I64, I64, I64, P, P, P, SZ, P]),
+    "sdx_residual_probs_workspace": (SZ, [I64, I64]),
+    "sdx_residual_probs": (INT, [P, P, I64, I64, I64, P, I64, P, SZ, P]),
+    "sdx_gather_prob": (INT, [P, I64, I64, I64, P, P, P]),
+    "sdx_verify_workspace": (SZ, [I64, I32, I64, INT]),
+    "sdx_verify": (INT, [P, P, INT, I64, I32, I64, P, P, P, P, F, F, I32, P, P, P, P, SZ, P]),
+    "sdx_verify_greedy_workspace": (SZ, [I64, I32]),
+    "sdx_verify_greedy": (INT, [P, INT, I64, I32, I64, P, P, P, P, P, P, P, SZ, P]),
+    "sdx_argmax": (INT, [P, INT, I64, I64, I64, P, P]),
+    "sdx_slot_mapping": (INT, [P, I64, I64, P, I32, I64, I64, P, P, P]),
+    "sdx_kv_advance": (INT, [P, I64, I64, P]),
+    "sdx_kv_rollback": (INT, [P, I64, P, P, P]),
+    "sdx_ragged_update": (INT, [P, P, P, P, INT, I64, I64, I64, I64, I64, P, P, P]),
+    "sdx_attn_mask": (INT, [P, P, I64, I64, I64, F, INT, P, P]),
+    "sdx_kv_append_paged": (INT, [P, I64, I64, P, INT, I32, I64, I64, I64, P, I64, I32, I64, P,
+                                  P, P]),
+}
+
+EXPORTS = tuple(_SIGS)
+
+
+class SpecdecError(RuntimeError):
+    """A libspecdec_amd call returned an error status."""
+
+
+def library_path():
+    return _PATH
+
+
+def lib():
+    """Load (once) and return the ctypes library with typed entry points."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(_PATH):
+            raise ImportError(
+                f"{_PATH} is not built; run `python adaptive-specdec_amd/build.py` "
+                "(hipcc, gfx950) before using specdec")
+        L = ctypes.CDLL(_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def check(rc, what):
+    if rc != 0:
+        msg = lib().sdx_last_error().decode(errors="replace")
+        raise SpecdecError(f"{what} failed ({rc}): {msg}")
+
+
+def dtype_code(t):
+    try:
+        return _DTYPE[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}; expected float32, bfloat16 or float16")
+
+
+def require_gpu(*tensors):
+    """Every tensor must live on the ROCm device; there is no CPU path."""
+    for t in tensors:
+        if t is not None and (not isinstance(t, torch.Tensor) or t.device.type != "cuda"):
+            raise RuntimeError(
+                "specdec (MI355X build) runs on ROCm device tensors only; got "
+                f"{getattr(t, 'device', type(t))}")
+
+
+def ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def workspace(nbytes, device):
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)

@@ -1,0 +1,195 @@
+"""Sampling transforms and exact rejection sampling on MI355X.
+
+Drop-in for the reference's `specdec/sampling.py` (`to_probs`,
+`sample_from_probs`, `residual_probs`, `gather_prob`, `__all__` at :31) plus
+`rejection_sample`, the accept block of `specdec/engine.py:285-303` as one
+call. Every function runs hand-written HIP kernels through
+libspecdec_amd.so; tensors must be on the ROCm device.
+
+Semantics follow the reference exactly where torch is deterministic and fix a
+rule where it is not:
+* transform order `sampling.py:42-67`: fp32 cast, greedy one-hot (first index
+  among maxima) for T <= 0, softmax(l / T), top-k zeroing without
+  renormalisation, top-p keep test `cum - p < top_p` on the top-k-zeroed
+  probabilities with the first token always kept, renormalise;
+* ties inside the top-p boundary group keep the lowest token ids (the
+  reference's CPU sort is unstable, so it leaves this unspecified);
+* the softmax numerator is exp evaluated in float64 and rounded once to fp32,
+  the normaliser and all masses are exact fixed-point sums, so decisions do
+  not depend on summation order;
+* sampling is an inverse-CDF draw on a uniform instead of torch.multinomial's
+  exponential race: the same distribution, reproducible ids.
+"""
+import torch
+
+from . import _lib
+
+__all__ = ["to_probs", "sample_from_probs", "residual_probs", "gather_prob", "rejection_sample"]
+
+FLAG_ACCEPT_NEAR_TIE = 1
+FLAG_NONFINITE = 2
+
+
+def _switch_args(temperature, top_p, top_k):
+    T = 0.0 if temperature is None or temperature <= 0.0 else float(temperature)
+    tp = float(top_p) if (top_p is not None and 0.0 < top_p < 1.0) else 1.0
+    tk = int(top_k) if top_k else 0
+    return T, tp, tk
+
+
+def _kernel_rows(x):
+    """[rows, V] in a layout the row kernels accept: fp32/bf16/fp16, rows
+    starting 16-byte aligned with a stride that is a multiple of 8 (16-bit) or
+    4 (fp32) elements. Returns (tensor, ld)."""
+    if x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        x = x.float()                      # sampling.py:42 upcasts anything else
+    V = x.shape[-1]
+    mult = 4 if x.dtype == torch.float32 else 8
+    if x.is_contiguous() and V % mult == 0 and x.data_ptr() % 16 == 0:
+        return x, V
+    ld = (V + mult - 1) // mult * mult
+    buf = torch.empty((x.shape[0], ld), dtype=x.dtype, device=x.device)
+    buf[:, :V].copy_(x)
+    return buf, ld
+
+
+def to_probs(logits, temperature=1.0, top_p=1.0, top_k=0):
+    """Logits [..., V] -> fp32 probabilities [..., V] (`sampling.py:34-67`)."""
+    _lib.require_gpu(logits)
+    L = _lib.lib()
+    shape = logits.shape
+    V = shape[-1]
+    x, ld = _kernel_rows(logits.reshape(-1, V))
+    rows = x.shape[0]
+    out = torch.empty((rows, V), dtype=torch.float32, device=x.device)
+    if rows == 0:
+        return out.reshape(shape)
+    T, tp, tk = _switch_args(temperature, top_p, top_k)
+    dt = _lib.dtype_code(x)
+    ws = _lib.workspace(L.sdx_to_probs_workspace(rows, V, dt), x.device)
+    rc = L.sdx_to_probs(_lib.ptr(x), dt, rows, V, ld, T, tp, tk, _lib.ptr(out), V,
+                        _lib.ptr(ws), ws.numel(), _lib.stream_of(x))
+    _lib.check(rc, "to_probs")
+    return out.reshape(shape)
+
+
+def sample_from_probs(probs, generator=None, u=None):
+    """One draw per row of probs [..., V] -> ids [...] (`sampling.py:70-74`).
+
+    The draw is inverse-CDF on a uniform per row; `u` (fp32 [...], in [0, 1))
+    may be given, otherwise it is drawn with `torch.rand(..., generator=generator)`.
+    """
+    _lib.require_gpu(probs)
+    L = _lib.lib()
+    V = probs.shape[-1]
+    p, ld = _kernel_rows(probs.reshape(-1, V).float())
+    rows = p.shape[0]
+    if u is None:
+        u = torch.rand(rows, device=p.device, generator=generator)
+    u = u.reshape(-1).to(torch.float32).contiguous()
+    ids = torch.empty(rows, dtype=torch.int64, device=p.device)
+    if rows:
+        ws = _lib.workspace(L.sdx_sample_probs_workspace(rows, V), p.device)
+        rc = L.sdx_sample_probs(_lib.ptr(p), rows, V, ld, _lib.ptr(u), _lib.ptr(ids),
+                                _lib.ptr(ws), ws.numel(), _lib.stream_of(p))
+        _lib.check(rc, "sample_from_probs")
+    return ids.reshape(probs.shape[:-1])
+
+
+def residual_probs(p, q):
+    """norm((p - q)_+), p where that mass is <= 1e-9 (`sampling.py:77-90`)."""
+    _lib.require_gpu(p, q)
+    L = _lib.lib()
+    V = p.shape[-1]
+    pp, ld = _kernel_rows(p.reshape(-1, V).float())
+    qq, ldq = _kernel_rows(q.reshape(-1, V).float())
+    if ldq != ld:
+        raise ValueError("p and q must have the same shape")
+    rows = pp.shape[0]
+    out = torch.empty((rows, V), dtype=torch.float32, device=pp.device)
+    if rows:
+        ws = _lib.workspace(L.sdx_residual_probs_workspace(rows, V), pp.device)
+        rc = L.sdx_residual_probs(_lib.ptr(pp), _lib.ptr(qq), rows, V, ld, _lib.ptr(out), V,
+                                  _lib.ptr(ws), ws.numel(), _lib.stream_of(pp))
+        _lib.check(rc, "residual_probs")
+    return out.reshape(p.shape)
+
+
+def gather_prob(probs, ids):
+    """probs [..., V], ids [...] -> probs at ids, shape [...] (`sampling.py:93-95`)."""
+    _lib.require_gpu(probs, ids)
+    L = _lib.lib()
+    V = probs.shape[-1]
+    p = probs.reshape(-1, V).float().contiguous()
+    i = ids.reshape(-1).to(torch.int64).contiguous()
+    if i.numel() != p.shape[0]:
+        raise ValueError("ids must have the leading shape of probs")
+    out = torch.empty(p.shape[0], dtype=torch.float32, device=p.device)
+    if p.shape[0]:
+        rc = L.sdx_gather_prob(_lib.ptr(p), p.shape[0], V, V, _lib.ptr(i), _lib.ptr(out),
+                               _lib.stream_of(p))
+        _lib.check(rc, "gather_prob")
+    return out.reshape(ids.shape)
+
+
+def rejection_sample(target_logits, draft_logits, draft_ids, u_accept, u_final, *,
+                     temperature=1.0, top_p=1.0, top_k=0, active=None, out=None):
+    """The verify step of `engine.py:281-303` in one device call.
+
+    target_logits [B, k+1, V] and draft_logits [B, k, V] (fp32/bf16/fp16; the
+    same transform is applied to both, `sampling.py:5-19`), draft_ids [B, k],
+    u_accept [B, k] (the per-position uniforms of `engine.py:291`), u_final [B]
+    (the residual/bonus draw), active [B] bool (the engine's ~done; None = all).
+    Returns (n_acc [B] int64, y [B] int64, flags [B] uint8): row b emits
+    draft_ids[b, :n_acc[b]] then y[b] and drops k - n_acc[b] cached positions.
+    flags bit 0 marks rows whose accept decision was within 1e-5 of flipping.
+    With temperature <= 0 the draft logits are not read (may be None).
+    """
+    T, tp, tk = _switch_args(temperature, top_p, top_k)
+    greedy = T == 0.0
+    _lib.require_gpu(target_logits, draft_ids, u_accept, u_final,
+                     None if greedy else draft_logits, active)
+    L = _lib.lib()
+    B, k1, V = target_logits.shape
+    k = k1 - 1
+    if k < 1:
+        raise ValueError("need at least one draft position (target is [B, k+1, V])")
+    dev = target_logits.device
+    tl = target_logits
+    if tl.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        tl = tl.float()
+    dl = None if greedy else draft_logits.to(tl.dtype)
+    if not greedy and tuple(dl.shape) != (B, k, V):
+        raise ValueError(f"draft_logits must be [{B}, {k}, {V}], got {tuple(dl.shape)}")
+    if tl.dtype != torch.float32 and V % 8 != 0:
+        # 16-bit rows must be 16-byte aligned; the fp32 path takes any vocab it supports
+        tl = tl.float()
+        dl = None if dl is None else dl.float()
+    tl = tl.contiguous()
+    dl = None if dl is None else dl.contiguous()
+    ids = draft_ids.to(torch.int64).contiguous()
+    ua = u_accept.to(torch.float32).contiguous()
+    uf = u_final.to(torch.float32).contiguous()
+    act = None if active is None else active.to(torch.uint8).contiguous()
+    if out is None:
+        n_acc = torch.empty(B, dtype=torch.int64, device=dev)
+        y = torch.empty(B, dtype=torch.int64, device=dev)
+        flags = torch.empty(B, dtype=torch.uint8, device=dev)
+    else:
+        n_acc, y, flags = out
+    if B == 0:
+        return n_acc, y, flags
+    dt = _lib.dtype_code(tl)
+    st = _lib.stream_of(tl)
+    if greedy:
+        ws = _lib.workspace(L.sdx_verify_greedy_workspace(B, k), dev)
+        rc = L.sdx_verify_greedy(_lib.ptr(tl), dt, B, k, V, _lib.ptr(ids), _lib.ptr(ua),
+                                 _lib.ptr(act), _lib.ptr(n_acc), _lib.ptr(y), _lib.ptr(flags),
+                                 _lib.ptr(ws), ws.numel(), st)
+    else:
+        ws = _lib.workspace(L.sdx_verify_workspace(B, k, V, dt), dev)
+        rc = L.sdx_verify(_lib.ptr(tl), _lib.ptr(dl), dt, B, k, V, _lib.ptr(ids), _lib.ptr(ua),
+                          _lib.ptr(uf), _lib.ptr(act), T, tp, tk, _lib.ptr(n_acc), _lib.ptr(y),
+                          _lib.ptr(flags), _lib.ptr(ws), ws.numel(), st)
+    _lib.check(rc, "rejection_sample")
+    return n_acc, y, flags

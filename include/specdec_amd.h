@@ -1,0 +1,167 @@
+/*
+ * specdec_amd.h -- C ABI of the MI355X (gfx950) speculative-decoding verify path.
+ *
+ * One shared library, libspecdec_amd.so, built from adaptive-specdec_amd/csrc.
+ * Every entry point:
+ *   - takes plain device pointers, element counts and an explicit stream
+ *     (a hipStream_t; NULL means the null stream) and is asynchronous;
+ *   - returns 0 on success or a negative SDX_E* status, with a message
+ *     retrievable from sdx_last_error() (thread-local);
+ *   - never allocates: scratch comes from a caller workspace sized by the
+ *     matching *_workspace() query.
+ * Token ids are int64 (torch's index type); block tables are int32. All
+ * tensors are row-major; a row stride ("ld") is given in elements.
+ *
+ * Numerics. Every discrete decision (nucleus membership, top-k threshold,
+ * accept/reject, sampled id) is computed with a fixed deterministic rule:
+ * softmax numerator exp evaluated in float64 and rounded once to fp32,
+ * normaliser and every mass/CDF accumulated exactly in 2^-62 fixed point,
+ * stable (lowest id first) tie order, inverse-CDF sampling on caller
+ * uniforms. Identical inputs give identical ids on every run and launch
+ * configuration.
+ */
+#ifndef SPECDEC_AMD_H
+#define SPECDEC_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* sdx_stream_t; /* == hipStream_t */
+
+enum sdx_dtype { SDX_F32 = 0, SDX_BF16 = 1, SDX_F16 = 2 };
+
+enum sdx_status {
+  SDX_OK = 0,
+  SDX_EINVAL = -1,       /* bad argument (null pointer, bad shape, misaligned) */
+  SDX_EUNSUPPORTED = -2, /* valid request outside what this build implements */
+  SDX_EHIP = -3,         /* a HIP runtime call failed */
+  SDX_EWORKSPACE = -4    /* workspace smaller than the *_workspace() query */
+};
+
+/* Per-row flag bits written by the verify entry points. */
+enum sdx_flag {
+  SDX_FLAG_ACCEPT_NEAR_TIE = 1, /* an evaluated accept test had |u - min(p/q,1)| < 1e-5 */
+  SDX_FLAG_NONFINITE = 2        /* a logit row held +inf or NaN: results unspecified */
+};
+
+const char* sdx_last_error(void);
+int sdx_version(void);
+
+/* ---- sampling transforms: specdec/sampling.py ---------------------------
+ * Switches follow sampling.py:43,52,56: temperature <= 0 -> greedy one-hot
+ * (first index among maxima); top_p outside (0, 1) -> no nucleus; top_k <= 0
+ * or >= vocab -> no top-k. */
+
+/* to_probs (sampling.py:34-67): logits [rows, vocab] (dtype) -> probs [rows, vocab] fp32. */
+size_t sdx_to_probs_workspace(int64_t rows, int64_t vocab, int dtype);
+int sdx_to_probs(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+                 float temperature, float top_p, int32_t top_k,
+                 float* probs, int64_t ld_out, void* workspace, size_t workspace_bytes,
+                 sdx_stream_t stream);
+
+/* sample_from_probs (sampling.py:70-74): one inverse-CDF draw per row on u[rows] in [0,1).
+ * ids[r] = first j with prefix(fixed62(probs[r]))[j] > floor(u[r] * sum); -1 for an all-zero row. */
+size_t sdx_sample_probs_workspace(int64_t rows, int64_t vocab);
+int sdx_sample_probs(const float* probs, int64_t rows, int64_t vocab, int64_t ld, const float* u,
+                     int64_t* ids, void* workspace, size_t workspace_bytes, sdx_stream_t stream);
+
+/* residual_probs (sampling.py:77-90): out = norm((p - q)_+), or p when that mass <= 1e-9. */
+size_t sdx_residual_probs_workspace(int64_t rows, int64_t vocab);
+int sdx_residual_probs(const float* p, const float* q, int64_t rows, int64_t vocab, int64_t ld,
+                       float* out, int64_t ld_out, void* workspace, size_t workspace_bytes,
+                       sdx_stream_t stream);
+
+/* gather_prob (sampling.py:93-95): out[r] = probs[r, ids[r]]. */
+int sdx_gather_prob(const float* probs, int64_t rows, int64_t vocab, int64_t ld, const int64_t* ids,
+                    float* out, sdx_stream_t stream);
+
+/* ---- verify: specdec/engine.py:281-312 ----------------------------------
+ * The engine's accept block factored out as one call. Inputs:
+ *   target_logits [batch, k+1, vocab], draft_logits [batch, k, vocab] (dtype, contiguous),
+ *   draft_ids [batch, k], u_accept [batch, k] (the per-position uniforms of engine.py:291),
+ *   u_final [batch] (the residual/bonus uniform), active [batch] (nullable; 0 = row done,
+ *   the engine's ~done, engine.py:287).
+ * Outputs: n_acc [batch] accepted drafts, y [batch] the token emitted after them
+ * (residual draw at position n_acc, or the bonus draw from p_{k+1} when n_acc == k),
+ * flags [batch] (sdx_flag bits). Emitted tokens of row b: draft_ids[b, :n_acc[b]] then y[b];
+ * KV rows to drop: k - n_acc[b] (engine.py:310). */
+size_t sdx_verify_workspace(int64_t batch, int32_t k, int64_t vocab, int dtype);
+int sdx_verify(const void* target_logits, const void* draft_logits, int dtype,
+               int64_t batch, int32_t k, int64_t vocab,
+               const int64_t* draft_ids, const float* u_accept, const float* u_final,
+               const uint8_t* active, float temperature, float top_p, int32_t top_k,
+               int64_t* n_acc, int64_t* y, uint8_t* flags,
+               void* workspace, size_t workspace_bytes, sdx_stream_t stream);
+
+/* Greedy verify (temperature 0): row b accepts position i iff draft_ids[b,i] ==
+ * argmax(target[b,i]) and u_accept[b,i] < 1 (u_accept nullable = all zero); y[b] =
+ * argmax(target[b, n_acc[b]]). Draft logits are not needed: with one-hot p the accept
+ * ratio is 0 or >= 1 whatever q is. Same outputs as sdx_verify at temperature 0. */
+size_t sdx_verify_greedy_workspace(int64_t batch, int32_t k);
+int sdx_verify_greedy(const void* target_logits, int dtype, int64_t batch, int32_t k,
+                      int64_t vocab, const int64_t* draft_ids, const float* u_accept,
+                      const uint8_t* active, int64_t* n_acc, int64_t* y, uint8_t* flags,
+                      void* workspace, size_t workspace_bytes, sdx_stream_t stream);
+
+/* ---- proposer-side calls: vllm_draft_spec/proposer.py -------------------- */
+
+/* Greedy draft token, logits.argmax(dim=-1) (proposer.py:262-263,331-332): first index
+ * among maxima, -0 == +0. logits [rows, vocab] (dtype) -> ids [rows]. */
+int sdx_argmax(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
+               int64_t* ids, sdx_stream_t stream);
+
+/* Drafting-step slot mapping (proposer.py:295-314): positions >= max_model_len are parked
+ * at 0 with slot padding_slot; else slot = block_table[r, pos / bs] * bs + pos % bs.
+ * block_table [rows, max_blocks] int32. clamped_positions may be NULL. */
+int sdx_slot_mapping(const int32_t* block_table, int64_t rows, int64_t max_blocks,
+                     const int64_t* positions, int32_t block_size, int64_t max_model_len,
+                     int64_t padding_slot, int64_t* clamped_positions, int64_t* slots,
+                     sdx_stream_t stream);
+
+/* ---- KV cache: specdec/kvcache.py ---------------------------------------- */
+
+/* RaggedCache.advance (kvcache.py:165-168): lengths[b] += q. */
+int sdx_kv_advance(int64_t* lengths, int64_t batch, int64_t q, sdx_stream_t stream);
+
+/* RaggedCache.rollback (kvcache.py:174-190) with device counts: lengths[b] -= n[b]. If any
+ * row would go below zero no length changes and *error (device int32) is set to 1;
+ * otherwise *error is left untouched. error may be NULL. */
+int sdx_kv_rollback(int64_t* lengths, int64_t batch, const int64_t* n, int32_t* error,
+                    sdx_stream_t stream);
+
+/* _RaggedLayer.update (kvcache.py:61-74): write k_new/v_new [batch, heads, q, head_dim]
+ * into keys/values [batch, heads, capacity, head_dim] at slots lengths[b] + j.
+ * dtype is the element type of all four tensors (SDX_BF16, SDX_F16 or SDX_F32). Rows that
+ * would overflow capacity set *error (nullable) and are not written. */
+int sdx_ragged_update(void* keys, void* values, const void* k_new, const void* v_new,
+                      int dtype, int64_t batch, int64_t heads, int64_t capacity,
+                      int64_t head_dim, int64_t q, const int64_t* lengths, int32_t* error,
+                      sdx_stream_t stream);
+
+/* RaggedCache.attn_mask (kvcache.py:138-162): out [batch, 1, q, kv_len] (dtype) with 0
+ * where slot s <= lengths[b] + j and s < valid[b] (valid nullable), else `neg`. */
+int sdx_attn_mask(const int64_t* lengths, const int64_t* valid, int64_t batch, int64_t q,
+                  int64_t kv_len, float neg, int dtype, void* out, sdx_stream_t stream);
+
+/* Paged append of q candidate positions per row into L layers that share one block
+ * table (the 36 target + 28 draft layers of one vLLM KV group, proposer.py:18-22).
+ * Pool of layer l, side s (0 = K, 1 = V): pool + l*layer_stride + s*side_stride, laid
+ * out [num_blocks, block_size, row_elems] (row_elems = kv_heads * head_dim, bf16/f16).
+ * New rows: staged + ((l*2 + s)*batch + b)*q*row_elems + j*row_elems.
+ * Position of (b, j) is lengths[b] + j; block_table [batch, max_blocks] int32 with ids
+ * in [0, num_blocks). Out-of-range positions or block ids set *error (nullable) and are
+ * skipped. Strides are in elements; row_elems * sizeof(dtype) must be a multiple of 16. */
+int sdx_kv_append_paged(void* pool, int64_t layer_stride, int64_t side_stride,
+                        const void* staged, int dtype, int32_t layers, int64_t batch,
+                        int64_t q, int64_t row_elems, const int32_t* block_table,
+                        int64_t max_blocks, int32_t block_size, int64_t num_blocks,
+                        const int64_t* lengths, int32_t* error, sdx_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SPECDEC_AMD_H */

@@ -1,0 +1,169 @@
+"""GPU parity of the HIP sampling path against the oracle (`oracle/sampling.py`).
+
+The kernels are designed to reproduce the oracle bit for bit (same exp rule,
+exact fixed-point sums, stable tie order), so probabilities are compared for
+exact equality as well as against the 1e-5 absolute tolerance, and every id
+/ count / flag is compared exactly.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampling as O
+from specdec import sampling as S
+from specdec.workloads import uniforms, verify_inputs, zipf_logits
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+TRANSFORMS = [(1.0, 1.0, 0), (0.8, 0.95, 0), (0.7, 0.9, 50), (1.3, 0.5, 7), (0.6, 0.95, 20),
+              (0.0, 1.0, 0)]
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _assert_probs_equal(got, ref):
+    assert got.shape == ref.shape
+    assert np.max(np.abs(got - ref)) < 1e-5
+    bad = np.nonzero(got.view(np.uint32) != ref.view(np.uint32))
+    assert bad[0].size == 0, f"{bad[0].size} elements differ, first at {tuple(b[0] for b in bad)}"
+
+
+@pytest.mark.parametrize("V,rows", [(64, 16), (1000, 8), (151936, 3)])
+@pytest.mark.parametrize("T,tp,tk", TRANSFORMS)
+def test_to_probs_bf16(V, rows, T, tp, tk):
+    g = torch.Generator(device=DEV).manual_seed(V + rows)
+    x = zipf_logits(rows, V, g, DEV)
+    got = _np(S.to_probs(x, T, tp, tk))
+    ref = O.to_probs(_np(x), T, tp, tk)
+    _assert_probs_equal(got, ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("T,tp,tk", TRANSFORMS[:4])
+def test_to_probs_other_dtypes(dtype, T, tp, tk):
+    g = torch.Generator(device=DEV).manual_seed(11)
+    x = zipf_logits(6, 4096, g, DEV, dtype=dtype)
+    got = _np(S.to_probs(x, T, tp, tk))
+    ref = O.to_probs(_np(x), T, tp, tk)
+    _assert_probs_equal(got, ref)
+
+
+def test_to_probs_edge_rows():
+    V = 256
+    rows = [
+        np.zeros(V, np.float32),                                  # one tie group of V
+        np.where(np.arange(V) % 3 == 0, 2.0, -1.0).astype(np.float32),
+        np.full(V, -np.inf, np.float32),                          # filled below
+        np.linspace(-40, 10, V).astype(np.float32),
+    ]
+    rows[2][[5, 9, 200]] = [1.0, 1.0, 0.5]                        # masked vocab
+    x = torch.tensor(np.stack(rows), device=DEV).to(torch.bfloat16)
+    for T, tp, tk in [(1.0, 0.3, 0), (0.9, 0.95, 0), (1.0, 1.0, 5), (1.0, 0.5, 100), (2.0, 0.99, 1)]:
+        got = _np(S.to_probs(x, T, tp, tk))
+        ref = O.to_probs(_np(x), T, tp, tk)
+        _assert_probs_equal(got, ref)
+
+
+def test_to_probs_nonaligned_vocab():
+    g = torch.Generator(device=DEV).manual_seed(5)
+    x = zipf_logits(4, 1003, g, DEV)
+    got = _np(S.to_probs(x, 0.8, 0.9, 0))
+    ref = O.to_probs(_np(x), 0.8, 0.9, 0)
+    _assert_probs_equal(got, ref)
+
+
+@pytest.mark.parametrize("B,k,V", [(16, 4, 1000), (4, 4, 151936), (8, 1, 512), (6, 8, 4096)])
+@pytest.mark.parametrize("T,tp,tk", [(0.8, 0.95, 0), (1.0, 1.0, 0), (0.7, 0.9, 50)])
+def test_rejection_sample_bf16(B, k, V, T, tp, tk):
+    inp = verify_inputs(B, k, V, seed=B * 100 + k, device=DEV, temperature=T, top_p=tp, top_k=tk)
+    n, y, f = S.rejection_sample(inp["target"], inp["draft"], inp["draft_ids"], inp["u_accept"],
+                                 inp["u_final"], temperature=T, top_p=tp, top_k=tk)
+    rn, ry, rf = O.rejection_sample(_np(inp["target"]), _np(inp["draft"]),
+                                    inp["draft_ids"].cpu().numpy(), _np(inp["u_accept"]),
+                                    _np(inp["u_final"]), T, tp, tk)
+    assert np.array_equal(n.cpu().numpy(), rn)
+    assert np.array_equal(y.cpu().numpy(), ry)
+    assert np.array_equal(f.cpu().numpy(), rf)
+
+
+def test_rejection_sample_active_and_fp32():
+    B, k, V = 12, 3, 640
+    inp = verify_inputs(B, k, V, seed=7, device=DEV, dtype=torch.float32)
+    active = torch.tensor([i % 3 != 0 for i in range(B)], device=DEV)
+    n, y, f = S.rejection_sample(inp["target"].float(), inp["draft"], inp["draft_ids"],
+                                 inp["u_accept"], inp["u_final"], temperature=0.8, top_p=0.95,
+                                 active=active)
+    rn, ry, rf = O.rejection_sample(_np(inp["target"]), _np(inp["draft"]),
+                                    inp["draft_ids"].cpu().numpy(), _np(inp["u_accept"]),
+                                    _np(inp["u_final"]), 0.8, 0.95, 0, active.cpu().numpy())
+    assert np.array_equal(n.cpu().numpy(), rn)
+    assert np.array_equal(y.cpu().numpy(), ry)
+    assert np.array_equal(f.cpu().numpy(), rf)
+    assert np.all(n.cpu().numpy()[~active.cpu().numpy()] == 0)
+
+
+def test_rejection_sample_greedy():
+    B, k, V = 32, 8, 4096
+    g = torch.Generator(device=DEV).manual_seed(3)
+    tgt = zipf_logits(B * (k + 1), V, g, DEV).view(B, k + 1, V)
+    drf = (tgt[:, :k].float() + torch.randn(B, k, V, generator=g, device=DEV)).to(torch.bfloat16)
+    am = tgt[:, :k].float().argmax(-1)
+    ids = torch.where(torch.rand(B, k, generator=g, device=DEV) < 0.6, am, (am + 7) % V)
+    ua = uniforms((B, k), g, DEV)
+    uf = uniforms((B,), g, DEV)
+    n, y, f = S.rejection_sample(tgt, drf, ids, ua, uf, temperature=0.0)
+    rn, ry, rf = O.rejection_sample(_np(tgt), _np(drf), ids.cpu().numpy(), _np(ua), _np(uf), 0.0)
+    assert np.array_equal(n.cpu().numpy(), rn)
+    assert np.array_equal(y.cpu().numpy(), ry)
+    assert np.array_equal(f.cpu().numpy(), rf)
+
+
+def test_sample_from_probs_and_residual():
+    g = torch.Generator(device=DEV).manual_seed(9)
+    V = 3000
+    p = S.to_probs(zipf_logits(10, V, g, DEV), 0.9, 0.95)
+    q = S.to_probs(zipf_logits(10, V, g, DEV), 0.9, 0.95)
+    u = uniforms((10,), g, DEV)
+    ids = S.sample_from_probs(p, u=u).cpu().numpy()
+    assert np.array_equal(ids, O.sample_from_probs(_np(p), _np(u)))
+    r = _np(S.residual_probs(p, q))
+    _assert_probs_equal(r, O.residual_probs(_np(p), _np(q)))
+    r_deg = _np(S.residual_probs(p, p))                  # degenerate: p itself
+    _assert_probs_equal(r_deg, O.residual_probs(_np(p), _np(p)))
+    gi = torch.randint(0, V, (10,), generator=g, device=DEV)
+    assert np.array_equal(_np(S.gather_prob(p, gi)), O.gather_prob(_np(p), gi.cpu().numpy()))
+
+
+def test_g1_config1_on_gpu():
+    """G1 gate on the HIP path: B=1, k=4, V=64, target N(0, 2^2), draft = target +
+    N(0, 0.8^2), T=1, 100,000 trials; first-token TV vs the exact target marginal
+    below 0.02, accepted-length histogram vs closed form, and the first 300
+    trials bit-exact against the oracle."""
+    N, k, V = 100_000, 4, 64
+    g = torch.Generator(device=DEV).manual_seed(20241)
+    tgt1 = torch.randn(k + 1, V, generator=g, device=DEV) * 2.0
+    drf1 = tgt1[:k] + torch.randn(k, V, generator=g, device=DEV) * 0.8
+    tgt = tgt1.expand(N, k + 1, V).contiguous()
+    drf = drf1.expand(N, k, V).contiguous()
+    q = S.to_probs(drf, 1.0)
+    ids = S.sample_from_probs(q, u=uniforms((N, k), g, DEV))
+    ua, uf = uniforms((N, k), g, DEV), uniforms((N,), g, DEV)
+    n, y, _ = S.rejection_sample(tgt, drf, ids, ua, uf, temperature=1.0)
+    first = torch.where(n >= 1, ids[:, 0], y).cpu().numpy()
+    P = O.to_probs(_np(tgt1), 1.0)
+    Q = O.to_probs(_np(drf1), 1.0)
+    emp = np.bincount(first, minlength=V) / N
+    tv = 0.5 * np.abs(emp - P[0]).sum()
+    assert tv < 0.02, tv
+    beta = np.minimum(P[:k].astype(np.float64), Q.astype(np.float64)).sum(-1)
+    expect = np.array([np.prod(beta[:a]) * (1 - beta[a]) for a in range(k)] + [np.prod(beta)])
+    got = np.bincount(n.cpu().numpy(), minlength=k + 1) / N
+    assert np.all(np.abs(got - expect) < 5 * np.sqrt(expect * (1 - expect) / N) + 1e-4)
+    M = 300
+    rn, ry, _ = O.rejection_sample(_np(tgt[:M]), _np(drf[:M]), ids[:M].cpu().numpy(),
+                                   _np(ua[:M]), _np(uf[:M]), 1.0)
+    assert np.array_equal(n[:M].cpu().numpy(), rn)
+    assert np.array_equal(y[:M].cpu().numpy(), ry)
