@@ -78,6 +78,9 @@ class _RaggedLayer(_HFLayer):
     def get_max_cache_shape(self, *args):
         return self.parent.capacity
 
+    def get_max_length(self, *args):
+        return self.parent.capacity
+
 
 class RaggedCache(_HFCache):
     """Per-row-length KV cache with O(1) rollback (`kvcache.py:87-202`).
@@ -92,10 +95,10 @@ class RaggedCache(_HFCache):
 
     def __init__(self, n_layers, batch_size, capacity, device):
         self.capacity = int(capacity)
-        self.batch_size = int(batch_size)
+        self._batch = int(batch_size)
         self.device = torch.device(device)
-        self.lengths_cpu = torch.zeros(self.batch_size, dtype=torch.long)
-        self.lengths = torch.zeros(self.batch_size, dtype=torch.long, device=self.device)
+        self.lengths_cpu = torch.zeros(self._batch, dtype=torch.long)
+        self.lengths = torch.zeros(self._batch, dtype=torch.long, device=self.device)
         # device-side error flag of the scatter / device rollback kernels
         self.error = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.max_len = 0
@@ -105,6 +108,10 @@ class RaggedCache(_HFCache):
             super().__init__(layers=layers)
         else:
             self.layers = layers
+
+    @property
+    def batch_size(self):
+        return self._batch
 
     def _push(self):
         """Mirror host lengths to the device (`kvcache.py:118-122`)."""

@@ -63,3 +63,24 @@ def test_controller_matches_oracle():
                 assert C.best_k(a, c, 8, x) == OC.best_k(a, c, 8, x)
                 assert C.expected_speedup(4, a, c, x) == OC.expected_speedup(4, a, c, x)
     assert C.best_k_rows([0.4, 0.9], 0.1) == [C.best_k(0.4, 0.1), C.best_k(0.9, 0.1)]
+
+
+def test_ragged_cache_host_bookkeeping():
+    """Host half of `kvcache.py:165-202` (no kernel calls): lengths, max_len,
+    uniformity, positions and the below-zero error, on a CPU-placed cache."""
+    from specdec.kvcache import RaggedCache
+    c = RaggedCache(3, 3, 128, "cpu")
+    assert c.batch_size == 3 and len(c.layers) == 3 and c.get_seq_length() == 0
+    c.set_lengths(torch.tensor([7, 5, 6]))
+    assert (c.max_len, c._uniform) == (7, False)
+    c.advance(4)
+    c.rollback([0, 3, 2])
+    assert c.lengths.tolist() == [11, 6, 8] and c.max_len == 11
+    assert c.positions(2).tolist() == [[11, 12], [6, 7], [8, 9]]
+    assert c.cache_position(2).tolist() == [11, 12]
+    assert c.kv_len_for(3) == 14
+    with pytest.raises(RuntimeError, match="below zero"):
+        c.rollback(torch.tensor([12, 0, 0]))
+    c2 = RaggedCache(1, 2, 16, "cpu")
+    c2.set_lengths([4, 4])
+    assert c2.attn_mask(2, torch.float32) is None          # uniform, no pad: no mask
