@@ -259,13 +259,44 @@ size_t sdx_verify_workspace(int64_t batch, int32_t k, int64_t vocab, int dtype) 
   return c.used;
 }
 
+static int verify_impl(const void* target_logits, const void* draft_logits, int dtype,
+                       int64_t batch, int32_t k, int64_t vocab, const int64_t* draft_ids,
+                       const float* u_accept, const float* u_final, const uint8_t* active,
+                       float temperature, float top_p, int32_t top_k, int64_t* n_acc, int64_t* y,
+                       uint8_t* flags, void* workspace, size_t workspace_bytes,
+                       sdx_stream_t stream, bool stats_only);
+
 int sdx_verify(const void* target_logits, const void* draft_logits, int dtype, int64_t batch,
                int32_t k, int64_t vocab, const int64_t* draft_ids, const float* u_accept,
                const float* u_final, const uint8_t* active, float temperature, float top_p,
                int32_t top_k, int64_t* n_acc, int64_t* y, uint8_t* flags, void* workspace,
                size_t workspace_bytes, sdx_stream_t stream) {
-  if (!target_logits || !draft_ids || !u_accept || !u_final || !n_acc || !y || !flags ||
-      batch < 0 || k < 1 || !dtype_ok(dtype))
+  if (!n_acc || !y || !flags) return fail(SDX_EINVAL, "sdx_verify: bad arguments");
+  return verify_impl(target_logits, draft_logits, dtype, batch, k, vocab, draft_ids, u_accept,
+                     u_final, active, temperature, top_p, top_k, n_acc, y, flags, workspace,
+                     workspace_bytes, stream, false);
+}
+
+int sdx_verify_stats(const void* target_logits, const void* draft_logits, int dtype,
+                     int64_t batch, int32_t k, int64_t vocab, const int64_t* draft_ids,
+                     float temperature, float top_p, int32_t top_k, void* workspace,
+                     size_t workspace_bytes, sdx_stream_t stream) {
+  static const float dummy_u = 0.0f;
+  if (!(temperature > 0.0f))
+    return fail(SDX_EINVAL, "sdx_verify_stats: temperature must be > 0 (greedy has no phase 1)");
+  return verify_impl(target_logits, draft_logits, dtype, batch, k, vocab, draft_ids, &dummy_u,
+                     &dummy_u, nullptr, temperature, top_p, top_k, nullptr, nullptr, nullptr,
+                     workspace, workspace_bytes, stream, true);
+}
+
+static int verify_impl(const void* target_logits, const void* draft_logits, int dtype,
+                       int64_t batch, int32_t k, int64_t vocab, const int64_t* draft_ids,
+                       const float* u_accept, const float* u_final, const uint8_t* active,
+                       float temperature, float top_p, int32_t top_k, int64_t* n_acc, int64_t* y,
+                       uint8_t* flags, void* workspace, size_t workspace_bytes,
+                       sdx_stream_t stream, bool stats_only) {
+  if (!target_logits || !draft_ids || !u_accept || !u_final || batch < 0 || k < 1 ||
+      !dtype_ok(dtype))
     return fail(SDX_EINVAL, "sdx_verify: bad arguments");
   if (int e = check_vocab(dtype, vocab)) return e;
   if (batch == 0) return SDX_OK;
@@ -316,6 +347,7 @@ int sdx_verify(const void* target_logits, const void* draft_logits, int dtype, i
     a.stats = st; a.tables = tb;
     if (int e = hip_status(sdx::launch_rowstat16(dtype, a, rows, s), "rowstat16")) return e;
   }
+  if (stats_only) return SDX_OK;
   sdx::AcceptArgs aa{st, batch, k, u_accept, u_final, active, jobs, n_acc, flags};
   if (int e = hip_status(sdx::launch_accept(aa, s), "accept")) return e;
   if (dtype == SDX_F32) {

@@ -24,7 +24,8 @@ import torch
 
 from . import _lib
 
-__all__ = ["to_probs", "sample_from_probs", "residual_probs", "gather_prob", "rejection_sample"]
+__all__ = ["to_probs", "sample_from_probs", "residual_probs", "gather_prob", "rejection_sample",
+           "Verifier"]
 
 FLAG_ACCEPT_NEAR_TIE = 1
 FLAG_NONFINITE = 2
@@ -193,3 +194,72 @@ def rejection_sample(target_logits, draft_logits, draft_ids, u_accept, u_final, 
                           _lib.ptr(flags), _lib.ptr(ws), ws.numel(), st)
     _lib.check(rc, "rejection_sample")
     return n_acc, y, flags
+
+
+class Verifier:
+    """`rejection_sample` prepared for fixed shapes: workspace and outputs are
+    allocated once, each call is one C-ABI call (capturable in a HIP graph).
+
+    v = Verifier(B, k, V, torch.bfloat16, temperature=0.8, top_p=0.95)
+    n_acc, y, flags = v(target, draft, draft_ids, u_accept, u_final)
+    """
+
+    def __init__(self, batch, k, vocab, dtype, temperature=1.0, top_p=1.0, top_k=0,
+                 device="cuda"):
+        self.B, self.k, self.V = int(batch), int(k), int(vocab)
+        self.T, self.tp, self.tk = _switch_args(temperature, top_p, top_k)
+        self.greedy = self.T == 0.0
+        self.dt = _lib.dtype_code(torch.empty(0, dtype=dtype))
+        if self.dt != _lib.F32 and self.V % 8 != 0:
+            raise ValueError("16-bit logits need vocab % 8 == 0 for the prepared path")
+        self.dtype = dtype
+        L = _lib.lib()
+        self.L = L
+        dev = torch.device(device)
+        nbytes = (L.sdx_verify_greedy_workspace(self.B, self.k) if self.greedy
+                  else L.sdx_verify_workspace(self.B, self.k, self.V, self.dt))
+        self.ws = _lib.workspace(nbytes, dev)
+        self.n_acc = torch.empty(self.B, dtype=torch.int64, device=dev)
+        self.y = torch.empty(self.B, dtype=torch.int64, device=dev)
+        self.flags = torch.empty(self.B, dtype=torch.uint8, device=dev)
+
+    def _check(self, target, draft, ids, ua, uf):
+        if target.dtype != self.dtype or tuple(target.shape) != (self.B, self.k + 1, self.V):
+            raise ValueError("target does not match the prepared shape/dtype")
+        if not self.greedy and (draft.dtype != self.dtype or
+                                tuple(draft.shape) != (self.B, self.k, self.V)):
+            raise ValueError("draft does not match the prepared shape/dtype")
+        for t, dt in ((ids, torch.int64), (ua, torch.float32), (uf, torch.float32)):
+            if t.dtype != dt or not t.is_contiguous():
+                raise ValueError("draft_ids int64, u_accept/u_final fp32, all contiguous")
+        for t in (target, draft):
+            if t is not None and not t.is_contiguous():
+                raise ValueError("logits must be contiguous")
+
+    def __call__(self, target, draft, draft_ids, u_accept, u_final, active=None):
+        self._check(target, draft, draft_ids, u_accept, u_final)
+        act = None if active is None else active.to(torch.uint8)
+        st = _lib.stream_of(target)
+        if self.greedy:
+            rc = self.L.sdx_verify_greedy(_lib.ptr(target), self.dt, self.B, self.k, self.V,
+                                          _lib.ptr(draft_ids), _lib.ptr(u_accept), _lib.ptr(act),
+                                          _lib.ptr(self.n_acc), _lib.ptr(self.y),
+                                          _lib.ptr(self.flags), _lib.ptr(self.ws),
+                                          self.ws.numel(), st)
+        else:
+            rc = self.L.sdx_verify(_lib.ptr(target), _lib.ptr(draft), self.dt, self.B, self.k,
+                                   self.V, _lib.ptr(draft_ids), _lib.ptr(u_accept),
+                                   _lib.ptr(u_final), _lib.ptr(act), self.T, self.tp, self.tk,
+                                   _lib.ptr(self.n_acc), _lib.ptr(self.y), _lib.ptr(self.flags),
+                                   _lib.ptr(self.ws), self.ws.numel(), st)
+        _lib.check(rc, "Verifier")
+        return self.n_acc, self.y, self.flags
+
+    def stats(self, target, draft, draft_ids):
+        """Phase 1 only (fused to_probs statistics of all rows), for timing."""
+        if self.greedy:
+            raise ValueError("greedy verify has no statistics phase")
+        rc = self.L.sdx_verify_stats(_lib.ptr(target), _lib.ptr(draft), self.dt, self.B, self.k,
+                                     self.V, _lib.ptr(draft_ids), self.T, self.tp, self.tk,
+                                     _lib.ptr(self.ws), self.ws.numel(), _lib.stream_of(target))
+        _lib.check(rc, "Verifier.stats")

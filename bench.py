@@ -1,0 +1,291 @@
+#!/usr/bin/env python
+"""Benchmark of the speculative-decoding verify path on one MI355X.
+
+Default workload (the headline): fused verify, B=64 rows, k=4 drafts (5 target
+positions per row), V=151,936, bf16 logits, T=0.8, top-p 0.95. One step =
+one call of the verify path over one batch: fused to_probs on all 576 target
+and draft rows, accept test, residual/bonus draw. Inputs (seeded synthetic
+logits with a Zipf head, draft = target + N(0,1), draft ids drawn from q) are
+resident in HBM; three input sets (525 MB, more than the 256 MB MALL) rotate so
+no step reads another step's bytes from cache.
+
+    python bench.py [--steps K] [--warmup W] [--workload verify|greedy|kv]
+
+Prints one JSON line: verified tokens/s (sum over rows of n_acc + 1 per
+step), the roofline of the dominant kernel (row statistics: algorithmic
+bytes = every logit read once, timed with HIP events on the launch stream),
+and the CPU baseline (the numpy oracle on a bounded sample of the same
+inputs, one core).
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (REPO, os.path.join(REPO, "adaptive-specdec_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "verified tokens/sec at B=64,k=4,V=151936; % of HBM peak; speedup vs host CPU"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def timed_graphs(graphs, steps, torch):
+    """Replay graphs round-robin `steps` times between two events; ms per replay."""
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        graphs[i % len(graphs)].replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def capture(fn, torch):
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+def bench_verify(args, torch):
+    import numpy as np
+    from specdec.sampling import Verifier
+    from specdec.workloads import verify_inputs
+
+    B, k, V, T, tp = 64, 4, 151936, 0.8, 0.95
+    dev = "cuda:0"
+    log(f"generating {args.sets} input sets B={B} k={k} V={V}")
+    sets = [verify_inputs(B, k, V, seed=1000 + i, device=dev, temperature=T, top_p=tp)
+            for i in range(args.sets)]
+    vers = [Verifier(B, k, V, torch.bfloat16, temperature=T, top_p=tp, device=dev)
+            for _ in sets]
+    calls = [(lambda v=v, s=s: v(s["target"], s["draft"], s["draft_ids"], s["u_accept"],
+                                 s["u_final"])) for v, s in zip(vers, sets)]
+    stat_calls = [(lambda v=v, s=s: v.stats(s["target"], s["draft"], s["draft_ids"]))
+                  for v, s in zip(vers, sets)]
+    # eager reference results, then warm up
+    eager = []
+    for c in calls:
+        n, y, f = c()
+        eager.append((n.clone(), y.clone(), f.clone()))
+    for i in range(args.warmup):
+        calls[i % len(calls)]()
+        stat_calls[i % len(calls)]()
+    torch.cuda.synchronize()
+    tokens = [int((n + 1).sum().item()) for n, _, _ in eager]
+    if args.no_graph:
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(args.steps):
+            calls[i % len(calls)]()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        stat_ms = None
+    else:
+        graphs = [capture(c, torch) for c in calls]
+        sgraphs = [capture(c, torch) for c in stat_calls]
+        for rep in range(3):                       # every replay must equal the eager result
+            for g, v, (n, y, f) in zip(graphs, vers, eager):
+                g.replay()
+                torch.cuda.synchronize()
+                ok = (torch.equal(v.n_acc, n) and torch.equal(v.y, y) and torch.equal(v.flags, f))
+                if not ok:
+                    raise RuntimeError("graph replay differs from the eager verify")
+        ms = timed_graphs(graphs, args.steps, torch)
+        stat_ms = timed_graphs(sgraphs, args.steps, torch)
+    # eager timing too (host launch path), for the record
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(min(args.steps, 100)):
+        calls[i % len(calls)]()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / min(args.steps, 100)
+
+    total_tokens = sum(tokens[i % len(tokens)] for i in range(args.steps))
+    value = total_tokens / (ms * args.steps / 1e3)
+    rows = B * (2 * k + 1)
+    alg_bytes = rows * V * 2                     # every bf16 logit read once
+    out_bytes = B * (8 + 8 + 1)
+    roof = None
+    if stat_ms is not None:
+        achieved = alg_bytes / (stat_ms / 1e3) / 1e9
+        roof = {"bound": "hbm", "kernel": "rowstat16_kernel (verify phase 1)",
+                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_per_launch(),
+                "algorithmic_bytes": alg_bytes, "avg_launch_us": round(stat_ms * 1e3, 2)}
+    cpu = None if args.skip_cpu else cpu_baseline(sets[0], eager[0], args, T, tp, np, torch)
+    result = {
+        "metric": METRIC, "value": round(value, 1), "unit": "verified tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "fused verify B=64 k=4 V=151936 bf16 T=0.8 top-p 0.95",
+                   "batch": B, "k": k, "vocab": V, "logits": "bf16", "temperature": T,
+                   "top_p": tp, "input_sets": len(sets), "hip_graph": not args.no_graph},
+        "rows_per_s": round(rows / (ms / 1e3), 1),
+        "step_bytes_algorithmic": alg_bytes + out_bytes,
+        "step_hbm_frac": round((alg_bytes + out_bytes) / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+        "eager_ms_per_step": round(eager_ms, 4),
+        "mean_accepted": round(sum(tokens) / len(tokens) / B - 1, 4),
+        "roofline": roof, "cpu_baseline": cpu,
+    }
+    if cpu:
+        result["speedup_vs_cpu"] = round(value / cpu["value"], 1)
+    return result
+
+
+def traffic_per_launch():
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE summary (scaled by the copy-kernel calibration), or None."""
+    p = os.path.join(REPO, "profiles", "traffic_verify.json")
+    try:
+        with open(p) as f:
+            return json.load(f).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(s, eager, args, T, tp, np, torch):
+    """The oracle (numpy restatement of the reference path) on the first
+    `cpu_rows` batch rows of input set 0, one core; checked against the GPU."""
+    from oracle import sampling as O
+    r = args.cpu_rows
+    tl = s["target"][:r].float().cpu().numpy()
+    dl = s["draft"][:r].float().cpu().numpy()
+    ids = s["draft_ids"][:r].cpu().numpy()
+    ua = s["u_accept"][:r].cpu().numpy()
+    uf = s["u_final"][:r].cpu().numpy()
+    log(f"cpu baseline: oracle on {r} rows")
+    t0 = time.perf_counter()
+    n, y, f = O.rejection_sample(tl, dl, ids, ua, uf, T, tp, 0)
+    dt = time.perf_counter() - t0
+    gn, gy, gf = (t[:r].cpu().numpy() for t in eager)
+    parity = bool(np.array_equal(n, gn) and np.array_equal(y, gy) and np.array_equal(f, gf))
+    toks = int((n + 1).sum())
+    return {"value": round(toks / dt, 2), "unit": "verified tokens/s", "cores": 1,
+            "kind": "port", "seconds": round(dt, 2),
+            "sample": f"{r} of 64 batch rows of input set 0 ({r * 9} vocab rows), same inputs "
+                      f"as the GPU run; oracle ids {'equal' if parity else 'DIFFER from'} GPU ids",
+            "cpu": cpu_model(), "parity": parity}
+
+
+def bench_greedy(args, torch):
+    from specdec.sampling import Verifier
+    from specdec.workloads import greedy_inputs
+    B, k, V = 256, 8, 151936
+    dev = "cuda:0"
+    sets = [greedy_inputs(B, k, V, seed=2000 + i, device=dev) for i in range(args.sets)]
+    vers = [Verifier(B, k, V, torch.bfloat16, temperature=0.0, device=dev) for _ in sets]
+    calls = [(lambda v=v, s=s: v(s["target"], None, s["draft_ids"], s["u_accept"],
+                                 s["u_accept"][:, 0].contiguous())) for v, s in zip(vers, sets)]
+    for i in range(args.warmup):
+        calls[i % len(calls)]()
+    torch.cuda.synchronize()
+    tokens = []
+    for c in calls:
+        n, _, _ = c()
+        tokens.append(int((n + 1).sum().item()))
+    graphs = [capture(c, torch) for c in calls]
+    ms = timed_graphs(graphs, args.steps, torch)
+    alg = B * (k + 1) * V * 2
+    value = sum(tokens[i % len(tokens)] for i in range(args.steps)) / (ms * args.steps / 1e3)
+    ach = alg / (ms / 1e3) / 1e9
+    return {"metric": "verified tokens/sec, greedy verify B=256,k=8,V=151936", "value": round(value, 1),
+            "unit": "verified tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "greedy verify B=256 k=8 V=151936 bf16", "batch": B, "k": k,
+                       "vocab": V},
+            "roofline": {"bound": "hbm", "kernel": "argmax_kernel + greedy_accept_kernel",
+                         "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                         "algorithmic_bytes": alg},
+            "cpu_baseline": None}
+
+
+def bench_kv(args, torch):
+    from specdec.kvcache import PagedKVCache
+    from specdec.workloads import kv_inputs
+    L, B, q, H, D, bs = 64, 64, 5, 8, 128, 16
+    dev = "cuda:0"
+    inp = kv_inputs(L, B, q, H, D, bs, 512, 4096, seed=3, device=dev)
+    c = PagedKVCache(L, B, inp["num_blocks"], bs, H, D, inp["max_blocks"], device=dev)
+    c.block_table.copy_(inp["block_table"])
+    c.lengths.copy_(inp["lengths"])
+    drop = (q - inp["keep"]).contiguous()
+    staged = inp["staged"]
+
+    def step():
+        c.append(staged)
+        c.commit(q)
+        c.rollback(drop)
+        c.lengths.copy_(inp["lengths"])          # keep the workload stationary
+
+    for _ in range(args.warmup):
+        step()
+    g = capture(step, torch)
+    ms = timed_graphs([g], args.steps, torch)
+    ga = capture(lambda: c.append(staged), torch)
+    ms_append = timed_graphs([ga], args.steps, torch)
+    alg = 2 * L * 2 * B * q * H * D * 2            # staged read + pool written
+    ach = alg / (ms_append / 1e3) / 1e9
+    return {"metric": "KV append+commit+rollback, 64 layers x B=64 x 5 pos, GB/s",
+            "value": round(ach, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "paged KV append 64 layers, B=64, 5 positions, 8x128 bf16, "
+                                   "block 16, seq 512-4096", "layers": L, "batch": B, "q": q},
+            "roofline": {"bound": "hbm", "kernel": "kv_append_paged_kernel",
+                         "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                         "algorithmic_bytes": alg, "avg_launch_us": round(ms_append * 1e3, 2)},
+            "cpu_baseline": None}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="verify", choices=["verify", "greedy", "kv"])
+    ap.add_argument("--sets", type=int, default=3)
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=32)
+    ap.add_argument("--skip-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the verify path is row-parallel; "
+              "see DESIGN.md for how it shards); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm device visible", file=sys.stderr)
+        sys.exit(1)
+    fn = {"verify": bench_verify, "greedy": bench_greedy, "kv": bench_kv}[args.workload]
+    print(json.dumps(fn(args, torch)), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -97,6 +97,15 @@ int sdx_verify(const void* target_logits, const void* draft_logits, int dtype,
                int64_t* n_acc, int64_t* y, uint8_t* flags,
                void* workspace, size_t workspace_bytes, sdx_stream_t stream);
 
+/* Phase 1 of sdx_verify alone: the fused to_probs statistics of every target and draft
+ * row (normaliser, top-k/top-p boundary, drafted-token probabilities) into the workspace,
+ * without the accept test or the final draw. Lets a caller time or overlap the
+ * vocabulary pass; temperature must be > 0. Same workspace as sdx_verify. */
+int sdx_verify_stats(const void* target_logits, const void* draft_logits, int dtype,
+                     int64_t batch, int32_t k, int64_t vocab, const int64_t* draft_ids,
+                     float temperature, float top_p, int32_t top_k, void* workspace,
+                     size_t workspace_bytes, sdx_stream_t stream);
+
 /* Greedy verify (temperature 0): row b accepts position i iff draft_ids[b,i] ==
  * argmax(target[b,i]) and u_accept[b,i] < 1 (u_accept nullable = all zero); y[b] =
  * argmax(target[b, n_acc[b]]). Draft logits are not needed: with one-hot p the accept
