@@ -53,10 +53,11 @@ Switches switches(float T, float top_p, int32_t top_k, int64_t V) {
 }
 
 // Chunking of the id range for the draw / output kernels: chunks of a
-// multiple of 8 ids, at most 64 per row.
+// multiple of 8 ids, at most 2048 ids (one block round) where the chunk count
+// allows, at most kMaxChunks per row.
 void chunking(int64_t V, int64_t* chunk, int* nchunk) {
   int64_t n = (V + 2047) / 2048;
-  if (n > 64) n = 64;
+  if (n > sdx::kMaxChunks) n = sdx::kMaxChunks;
   if (n < 1) n = 1;
   int64_t c = (V + n - 1) / n;
   c = (c + 7) / 8 * 8;
@@ -69,7 +70,7 @@ constexpr int64_t kMaxVocab16 = 16 * 20 * 512;  // register capacity of the row 
 // Workspace of the transform + draw pipeline over `rows` rows and `njobs` draws.
 size_t transform_ws(Carve& c, int64_t rows, int64_t V, int dtype, int64_t njobs,
                     sdx::RowStat** stats, float** tables, float** dense, sdx::SampleJob** jobs,
-                    uint64_t** sums) {
+                    sdx::ChunkRec** recs) {
   int64_t chunk;
   int nchunk;
   chunking(V, &chunk, &nchunk);
@@ -77,8 +78,22 @@ size_t transform_ws(Carve& c, int64_t rows, int64_t V, int dtype, int64_t njobs,
   *tables = dtype == SDX_F32 ? nullptr : c.take<float>((size_t)rows * sdx::kTbl);
   *dense = dtype == SDX_F32 ? c.take<float>((size_t)rows * V) : nullptr;
   *jobs = njobs ? c.take<sdx::SampleJob>(njobs) : nullptr;
-  *sums = njobs ? c.take<uint64_t>((size_t)njobs * nchunk * 2) : nullptr;
+  *recs = njobs ? c.take<sdx::ChunkRec>((size_t)njobs * nchunk) : nullptr;
   return c.used;
+}
+
+// Row statistics of 16-bit rows: bf16 rows stream through the fixed-window
+// kernel, and the register-resident kernel recomputes the rows it declines;
+// fp16 rows go to the register-resident kernel directly.
+int row_stats16(int dtype, sdx::RowStatArgs a, int64_t rows, hipStream_t s) {
+  if (dtype == SDX_BF16) {
+    a.fallback_only = 0;
+    if (int e = hip_status(sdx::launch_rowstream_bf16(a, rows, s), "rowstream_bf16")) return e;
+    a.fallback_only = 1;
+  } else {
+    a.fallback_only = 0;
+  }
+  return hip_status(sdx::launch_rowstat16(dtype, a, rows, s), "rowstat16");
 }
 
 int check_vocab(int dtype, int64_t V) {
@@ -102,9 +117,13 @@ int sdx_version(void) { return 1; }
 // ------------------------------------------------------------------ to_probs
 size_t sdx_to_probs_workspace(int64_t rows, int64_t vocab, int dtype) {
   Carve c{nullptr};
-  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; uint64_t* sm;
+  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; sdx::ChunkRec* rc;
   // fp32 rows are written straight to the output: no dense scratch
-  transform_ws(c, rows, vocab, dtype == SDX_F32 ? SDX_BF16 : dtype, 0, &st, &tb, &dn, &jb, &sm);
+  transform_ws(c, rows, vocab, dtype == SDX_F32 ? SDX_BF16 : dtype, 0, &st, &tb, &dn, &jb, &rc);
+  int64_t chunk;
+  int nchunk;
+  chunking(vocab, &chunk, &nchunk);
+  c.take<uint32_t>((size_t)rows * nchunk);  // group members per chunk
   return dtype == SDX_F32 ? align256(rows * sizeof(sdx::RowStat)) : c.used;
 }
 
@@ -140,8 +159,12 @@ int sdx_to_probs(const void* logits, int dtype, int64_t rows, int64_t vocab, int
       return e;
     return hip_status(sdx::launch_onehot(am, rows, vocab, probs, ld_out, s), "onehot");
   }
-  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; uint64_t* sm;
-  transform_ws(c, rows, vocab, dtype, 0, &st, &tb, &dn, &jb, &sm);
+  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; sdx::ChunkRec* rc;
+  transform_ws(c, rows, vocab, dtype, 0, &st, &tb, &dn, &jb, &rc);
+  int64_t chunk;
+  int nchunk;
+  chunking(vocab, &chunk, &nchunk);
+  uint32_t* counts = c.take<uint32_t>((size_t)rows * nchunk);
   sdx::RowStatArgs a = {};
   a.base[0] = (const uint16_t*)logits; a.nrows[0] = rows; a.ld[0] = ld;
   a.base[1] = a.base[0]; a.nrows[1] = 0; a.ld[1] = ld;
@@ -149,13 +172,10 @@ int sdx_to_probs(const void* logits, int dtype, int64_t rows, int64_t vocab, int
   a.T = temperature; a.top_p = top_p; a.top_k = top_k;
   a.use_p = sw.use_p; a.use_k = sw.use_k; a.greedy = sw.greedy;
   a.stats = st; a.tables = tb;
-  if (int e = hip_status(sdx::launch_rowstat16(dtype, a, rows, s), "rowstat16")) return e;
-  int64_t chunk;
-  int nchunk;
-  chunking(vocab, &chunk, &nchunk);
+  if (int e = row_stats16(dtype, a, rows, s)) return e;
   sdx::RowSource16 src{(const uint16_t*)logits, ld, (const uint16_t*)logits, ld, rows, true};
   return hip_status(sdx::launch_materialize16(dtype, src, st, tb, temperature, rows, vocab, chunk,
-                                              nchunk, probs, ld_out, s),
+                                              nchunk, counts, probs, ld_out, s),
                     "materialize16");
 }
 
@@ -166,7 +186,7 @@ size_t sdx_sample_probs_workspace(int64_t rows, int64_t vocab) {
   chunking(vocab, &chunk, &nchunk);
   Carve c{nullptr};
   c.take<sdx::SampleJob>(rows);
-  c.take<uint64_t>((size_t)rows * nchunk * 2);
+  c.take<sdx::ChunkRec>((size_t)rows * nchunk);
   return c.used;
 }
 
@@ -196,14 +216,15 @@ int sdx_sample_probs(const float* probs, int64_t rows, int64_t vocab, int64_t ld
   chunking(vocab, &chunk, &nchunk);
   Carve c{(uint8_t*)workspace};
   sdx::SampleJob* jobs = c.take<sdx::SampleJob>(rows);
-  uint64_t* sums = c.take<uint64_t>((size_t)rows * nchunk * 2);
+  sdx::ChunkRec* recs = c.take<sdx::ChunkRec>((size_t)rows * nchunk);
   hipLaunchKernelGGL(sdx_jobs_from_u, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, jobs,
                      u, rows, (int64_t)-1);
   if (int e = hip_status(hipGetLastError(), "jobs")) return e;
   const bool vec = aligned16(probs) && (ld % 4) == 0;
   sdx::RowSourceF32 src{probs, ld, probs, ld, rows, vec};
-  return hip_status(sdx::launch_draw_probs(src, jobs, rows, vocab, chunk, nchunk, sums, ids, s),
-                    "draw_probs");
+  return hip_status(
+      sdx::launch_draw_probs(src, nullptr, jobs, rows, vocab, chunk, nchunk, recs, ids, s),
+      "draw_probs");
 }
 
 // ------------------------------------------------------------------ residual_probs
@@ -226,16 +247,16 @@ int sdx_residual_probs(const float* p, const float* q, int64_t rows, int64_t voc
   chunking(vocab, &chunk, &nchunk);
   Carve c{(uint8_t*)workspace};
   sdx::SampleJob* jobs = c.take<sdx::SampleJob>(rows);
-  uint64_t* sums = c.take<uint64_t>((size_t)rows * nchunk * 2);
+  sdx::ChunkRec* recs = c.take<sdx::ChunkRec>((size_t)rows * nchunk);
   hipLaunchKernelGGL(sdx_jobs_from_u, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, jobs,
                      (const float*)nullptr, rows, rows);
   if (int e = hip_status(hipGetLastError(), "jobs")) return e;
   const bool vec = aligned16(p) && aligned16(q) && (ld % 4) == 0;
   sdx::RowSourceF32 src{p, ld, q, ld, rows, vec};
-  if (int e = hip_status(sdx::launch_chunk_mass_probs(src, jobs, rows, vocab, chunk, nchunk, sums, s),
+  if (int e = hip_status(sdx::launch_chunk_mass_probs(src, jobs, rows, vocab, chunk, nchunk, recs, s),
                          "chunk_mass"))
     return e;
-  sdx::ResidualNormArgs a{p, q, ld, vocab, chunk, nchunk, sums, out, ld_out};
+  sdx::ResidualNormArgs a{p, q, ld, vocab, chunk, nchunk, recs, out, ld_out};
   return hip_status(sdx::launch_residual_norm(a, rows, s), "residual_norm");
 }
 
@@ -252,9 +273,9 @@ int sdx_gather_prob(const float* probs, int64_t rows, int64_t vocab, int64_t ld,
 // ------------------------------------------------------------------ verify
 size_t sdx_verify_workspace(int64_t batch, int32_t k, int64_t vocab, int dtype) {
   Carve c{nullptr};
-  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; uint64_t* sm;
+  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; sdx::ChunkRec* rc;
   const int64_t rows = batch * (2 * (int64_t)k + 1);
-  transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jb, &sm);
+  transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jb, &rc);
   c.take<int64_t>(batch * ((int64_t)k + 1));  // greedy argmax
   return c.used;
 }
@@ -306,10 +327,10 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
   hipStream_t s = (hipStream_t)stream;
   const Switches sw = switches(temperature, top_p, top_k, vocab);
   Carve c{(uint8_t*)workspace};
-  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jobs; uint64_t* sums;
+  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jobs; sdx::ChunkRec* recs;
   const int64_t ntgt = batch * ((int64_t)k + 1), ndrf = batch * (int64_t)k;
   const int64_t rows = ntgt + ndrf;
-  transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jobs, &sums);
+  transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jobs, &recs);
   int64_t* am = c.take<int64_t>(ntgt);
   if (sw.greedy) {
     // one-hot p: only the target argmax matters (see sdx_verify_greedy)
@@ -345,20 +366,20 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
     a.T = temperature; a.top_p = top_p; a.top_k = top_k;
     a.use_p = sw.use_p; a.use_k = sw.use_k; a.greedy = 0;
     a.stats = st; a.tables = tb;
-    if (int e = hip_status(sdx::launch_rowstat16(dtype, a, rows, s), "rowstat16")) return e;
+    if (int e = row_stats16(dtype, a, rows, s)) return e;
   }
   if (stats_only) return SDX_OK;
   sdx::AcceptArgs aa{st, batch, k, u_accept, u_final, active, jobs, n_acc, flags};
-  if (int e = hip_status(sdx::launch_accept(aa, s), "accept")) return e;
   if (dtype == SDX_F32) {
     sdx::RowSourceF32 src{dn, vocab, dn, vocab, rows, (vocab % 4) == 0};
-    return hip_status(sdx::launch_draw_probs(src, jobs, batch, vocab, chunk, nchunk, sums, y, s),
-                      "draw_probs");
+    return hip_status(
+        sdx::launch_draw_probs(src, &aa, jobs, batch, vocab, chunk, nchunk, recs, y, s),
+        "draw_probs");
   }
   sdx::RowSource16 src{(const uint16_t*)target_logits, vocab, (const uint16_t*)draft_logits, vocab,
                        ntgt, true};
-  return hip_status(sdx::launch_draw16(dtype, src, st, tb, temperature, jobs, batch, vocab, chunk,
-                                       nchunk, sums, y, s),
+  return hip_status(sdx::launch_draw16(dtype, src, st, tb, temperature, &aa, jobs, batch, vocab,
+                                       chunk, nchunk, recs, y, s),
                     "draw16");
 }
 

@@ -86,7 +86,7 @@ __global__ void __launch_bounds__(F32_NT) to_probs_f32_kernel(F32Args a) {
       RowStat st = {};
       st.flags = kRowGreedy | kRowProbs;
       st.argmax = am;
-      st.zf = 1.0f; st.totf = 1.0f; st.glo = 1; st.ghi = 0; st.cut = -1;
+      st.zf = 1.0f; st.totf = 1.0f; st.glo = 1; st.ghi = 0;
       st.pgather = gid >= 0 ? (gid == am ? 1.0f : 0.0f) : 0.0f;
       a.stats[row] = st;
     }
@@ -232,7 +232,7 @@ __global__ void __launch_bounds__(F32_NT) to_probs_f32_kernel(F32Args a) {
     RowStat st = {};
     st.flags = kRowProbs;
     st.m = m; st.zf = zf; st.totf = totf; st.mass = tot;
-    st.glo = 1; st.ghi = 0; st.cut = -1; st.argmax = -1;
+    st.glo = 1; st.ghi = 0; st.argmax = -1;
     st.pgather = (gid >= 0 && gid < V) ? s_f[2] : 0.0f;
     a.stats[row] = st;
   }

@@ -19,10 +19,13 @@ enum RowFlag : uint32_t {
   kRowNonfinite = 1u << 1,   // +inf / +NaN in the row (results unspecified)
   kRowUnsupported = 1u << 2, // decision fell outside the histogram window
   kRowBelowWindow = 1u << 3, // elements below the histogram window carry mass
-  kRowProbs = 1u << 4        // final probabilities stored densely (fp32 path)
+  kRowProbs = 1u << 4,       // final probabilities stored densely (fp32 path)
+  kRowFallback = 1u << 5     // streaming kernel declined the row: recompute it
 };
 
-// 64 bytes per row.
+// 64 bytes per row. Keys in [glo, ghi] form the tie group that straddles the
+// nucleus boundary: its first `rstar` members in id order are kept, the
+// other gcount - rstar are dropped. Consumers count members as they stream.
 struct RowStat {
   float m;          // max over s = fl32(x / T)
   float zf;         // rn32(sum fixed62(exp_det(s - m)))
@@ -30,14 +33,59 @@ struct RowStat {
   float pgather;    // final probability of the row's gathered (draft) token
   int32_t kmax;     // largest key in the row
   int32_t klo;      // keys below klo are dropped (top-k / top-p)
-  int32_t glo, ghi; // boundary tie group: keys in [glo, ghi] kept iff id <= cut
-  int64_t cut;      // last kept id of the boundary group (-1: none kept)
+  int32_t glo, ghi; // boundary tie group key range (empty when glo > ghi)
+  int32_t rstar;    // group members kept, lowest ids first
+  int32_t gcount;   // group members in the row
   uint64_t mass;    // exact kept mass, fixed62
   uint32_t flags;   // RowFlag bits
   int32_t ntbl;     // table holds keys [kmax - ntbl + 1, kmax]
   int64_t argmax;   // greedy rows: first index of the maximum
 };
 static_assert(sizeof(RowStat) == 64, "RowStat layout");
+
+// Number of tie-group members (keys in [glo, ghi]) among ids [0, end) of a
+// 16-bit row, counted by the whole block (blockDim a multiple of 64; `red`
+// holds blockDim/64 + 1 words of LDS). Used to rank a drafted token that sits
+// inside its row's boundary group.
+__device__ inline uint32_t block_count_members(const uint16_t* ptr, int64_t end, int32_t glo,
+                                               int32_t ghi, uint32_t* red) {
+  uint32_t cnt = 0;
+  for (int64_t i = threadIdx.x; i < end; i += blockDim.x) {
+    const int32_t k2 = (int32_t)key_of_code16(ptr[i]);
+    cnt += (k2 >= glo && k2 <= ghi) ? 1u : 0u;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) cnt += (uint32_t)__shfl_xor((int)cnt, o, kWave);
+  const int nw = blockDim.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = cnt;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t t = 0;
+    for (int w = 0; w < nw; ++w) t += red[w];
+    red[nw] = t;
+  }
+  __syncthreads();
+  const uint32_t total = red[nw];
+  __syncthreads();
+  return total;
+}
+
+// Class of an element under its row's statistics: 0 dropped, 1 member of the
+// boundary tie group (kept iff its member rank < rstar), 2 kept.
+__device__ __forceinline__ int cls16(const RowStat& st, int32_t key) {
+  if (key < st.klo) return 0;
+  return (key >= st.glo && key <= st.ghi) ? 1 : 2;
+}
+// Final probability of a kept (class 2) or kept-member element.
+template <int FMT>
+__device__ __forceinline__ float val16(const RowStat& st, const float* tbl, uint32_t code,
+                                       float T) {
+  const int32_t t = st.kmax - (int32_t)key_of_code16(code);
+  if (t < st.ntbl) return tbl[t];
+  const float s = decode16<FMT>(code) / T;
+  const float p = exp_det(s - st.m) / st.zf;
+  return p / st.totf;
+}
 
 // Where rows live: rows [0, split) at base + row*ld, the rest at
 // base2 + (row - split)*ld2 (target then draft rows; p then q rows).
@@ -57,20 +105,5 @@ struct RowSourceF32 {
   int64_t split;
   bool vec;
 };
-
-// Final probability of a 16-bit-coded element under the row's statistics.
-template <int FMT>
-__device__ __forceinline__ float pfinal16(const RowStat& st, const float* tbl, int64_t idx,
-                                          uint32_t code, float T) {
-  if (st.flags & kRowGreedy) return idx == st.argmax ? 1.0f : 0.0f;
-  const int32_t key = (int32_t)key_of_code16(code);
-  if (key < st.klo) return 0.0f;
-  if (key <= st.ghi && key >= st.glo && idx > st.cut) return 0.0f;
-  const int32_t t = st.kmax - key;
-  if (t < st.ntbl) return tbl[t];
-  const float s = decode16<FMT>(code) / T;
-  const float p = exp_det(s - st.m) / st.zf;
-  return p / st.totf;
-}
 
 }  // namespace sdx

@@ -17,6 +17,7 @@ struct RowStatArgs {
   float top_p;
   int32_t top_k;
   int32_t use_p, use_k, greedy;
+  int32_t fallback_only;  // register kernel: only rows flagged kRowFallback
   RowStat* stats;
   float* tables;  // [rows, kTbl]
 };
@@ -55,6 +56,25 @@ struct AcceptArgs {
   uint8_t* flags;
 };
 
+// Partial sums of one draw over one chunk of ids, before the member ranks of
+// the boundary tie groups are known (f = fixed62, vp / vq = group values of
+// the p / q rows, "member" = element of its row's boundary tie group):
+struct ChunkRec {
+  uint64_t p2;  // sum f(p) over non-members of p
+  uint64_t r0;  // sum f(max(p - q, 0)) over non-members of p and of q
+  uint64_t ra;  // sum f(max(p - vq, 0)) over non-members of p that are members of q
+  uint64_t rb;  // sum f(p) over the same elements (their q member dropped)
+  uint64_t rp;  // sum f(max(vp - q, 0)) over members of p that are non-members of q
+  uint32_t np;  // members of p
+  uint32_t nq;  // members of q
+  uint32_t ndbl;  // members of both
+  uint32_t pad;
+  uint64_t pad2;
+};
+static_assert(sizeof(ChunkRec) == 64, "ChunkRec layout");
+
+constexpr int kMaxChunks = 128;
+
 struct ResidualNormArgs {
   const float* p;
   const float* q;
@@ -62,7 +82,7 @@ struct ResidualNormArgs {
   int64_t V;
   int64_t chunk;
   int32_t nchunk;
-  const uint64_t* sums;  // chunk masses of jobs (one job per row)
+  const ChunkRec* recs;  // chunk records of jobs (one job per row)
   float* out;
   int64_t ld_out;
 };
@@ -70,25 +90,30 @@ struct ResidualNormArgs {
 // sdx_rowstat.hip
 int rowstat16_nslot(int64_t V);
 hipError_t launch_rowstat16(int fmt, const RowStatArgs& a, int64_t rows, hipStream_t s);
+// sdx_rowstream.hip
+hipError_t launch_rowstream_bf16(const RowStatArgs& a, int64_t rows, hipStream_t s);
 // sdx_f32.hip
 constexpr int64_t kF32MaxVocab = 8192;
 hipError_t launch_to_probs_f32(const F32Args& a, int64_t rows, hipStream_t s);
 // sdx_sample.hip
-hipError_t launch_accept(const AcceptArgs& a, hipStream_t s);
+// Draw pipeline: chunk records (with the accept chain when `acc` is given:
+// jobs are then written by the kernel) and the per-job select. Without `acc`,
+// `jobs` must hold the draws already.
 hipError_t launch_draw16(int fmt, const RowSource16& src, const RowStat* stats,
-                         const float* tables, float T, const SampleJob* jobs, int64_t njobs,
-                         int64_t V, int64_t chunk, int nchunk, uint64_t* sums, int64_t* y,
-                         hipStream_t s);
-hipError_t launch_draw_probs(const RowSourceF32& src, const SampleJob* jobs, int64_t njobs,
-                             int64_t V, int64_t chunk, int nchunk, uint64_t* sums, int64_t* y,
-                             hipStream_t s);
-hipError_t launch_chunk_mass_probs(const RowSourceF32& src, const SampleJob* jobs, int64_t njobs,
-                                   int64_t V, int64_t chunk, int nchunk, uint64_t* sums,
+                         const float* tables, float T, const AcceptArgs* acc, SampleJob* jobs,
+                         int64_t njobs, int64_t V, int64_t chunk, int nchunk, ChunkRec* recs,
+                         int64_t* y, hipStream_t s);
+hipError_t launch_draw_probs(const RowSourceF32& src, const AcceptArgs* acc, SampleJob* jobs,
+                             int64_t njobs, int64_t V, int64_t chunk, int nchunk, ChunkRec* recs,
+                             int64_t* y, hipStream_t s);
+hipError_t launch_chunk_mass_probs(const RowSourceF32& src, SampleJob* jobs, int64_t njobs,
+                                   int64_t V, int64_t chunk, int nchunk, ChunkRec* recs,
                                    hipStream_t s);
+// to_probs output of 16-bit rows; `counts` holds rows * nchunk words.
 hipError_t launch_materialize16(int fmt, const RowSource16& src, const RowStat* stats,
                                 const float* tables, float T, int64_t rows, int64_t V,
-                                int64_t chunk, int nchunk, float* out, int64_t ld_out,
-                                hipStream_t s);
+                                int64_t chunk, int nchunk, uint32_t* counts, float* out,
+                                int64_t ld_out, hipStream_t s);
 hipError_t launch_residual_norm(const ResidualNormArgs& a, int64_t rows, hipStream_t s);
 hipError_t launch_gather(const float* probs, int64_t rows, int64_t V, int64_t ld,
                          const int64_t* ids, float* out, hipStream_t s);

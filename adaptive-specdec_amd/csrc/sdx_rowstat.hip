@@ -13,10 +13,13 @@
 //   * top-k threshold and the top-p nucleus boundary, found by a wave-0
 //     walk down from the maximum key with exact fixed-point cumulative mass
 //     and the reference's fp32 keep test `cum - p < top_p`;
-//   * the kept count inside the boundary tie group, then its index cutoff
-//     (lowest ids first) by a ballot scan of the register-resident keys.
+//   * the kept count inside the boundary tie group (lowest ids kept first);
+//     consumers rank group members by id as they stream the row.
 // Keys below the window (logits more than ~2^28 below the maximum at
 // ordinary temperatures) carry exp_det == 0 and are checked to do so.
+//
+// This kernel serves every fp16 row, and the bf16 rows the streaming kernel
+// (sdx_rowstream.hip) declines (`fallback_only`: rows flagged kRowFallback).
 #include "sdx_launch.hpp"
 
 namespace sdx {
@@ -84,6 +87,7 @@ __global__ void __launch_bounds__(RS_NT) rowstat16_kernel(RowStatArgs a) {
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int64_t row = blockIdx.x;
+  if (a.fallback_only && !(a.stats[row].flags & kRowFallback)) return;  // uniform per block
   const int g = row < a.nrows[0] ? 0 : 1;
   const int64_t r = g ? row - a.nrows[0] : row;
   const uint16_t* __restrict__ ptr = a.base[g] + r * a.ld[g];
@@ -114,18 +118,19 @@ __global__ void __launch_bounds__(RS_NT) rowstat16_kernel(RowStatArgs a) {
   uint32_t kmx = 0;
 #pragma unroll
   for (int j = 0; j < NSLOT; ++j) {
-    // Rows are read in whole 16-byte units (the caller's row stride is a
-    // multiple of 8 elements); ids at or past the row end become code 0xFFFF,
-    // key 0, and are excluded by the `< rem` checks of every stage.
+    // Whole 16-byte loads (rows start 16-byte aligned); the row's last partial
+    // group is read element by element. Ids at or past the row end become
+    // code 0xFFFF, key 0, and are excluded by the `< rem` checks of every stage.
     uint32_t w[4] = {0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu};
-    if (j * 512 < rem) {
+    if (j * 512 + 8 <= rem) {
       const uint4 v = *reinterpret_cast<const uint4*>(lptr + j * 512);
       w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
-      if (j * 512 + 8 > rem) {
+    } else if (j * 512 < rem) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
-          if (j * 512 + t >= rem) w[t >> 1] |= 0xFFFFu << (16 * (t & 1));
-      }
+      for (int t = 0; t < 8; ++t)
+        if (j * 512 + t < rem)
+          w[t >> 1] = (w[t >> 1] & ~(0xFFFFu << (16 * (t & 1)))) |
+                      ((uint32_t)lptr[j * 512 + t] << (16 * (t & 1)));
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -148,7 +153,7 @@ __global__ void __launch_bounds__(RS_NT) rowstat16_kernel(RowStatArgs a) {
     if (tid == 0) {
       RowStat st = {};
       st.flags = kRowNonfinite;
-      st.zf = 1.0f; st.totf = 1.0f; st.klo = 0x7FFFFFFF; st.glo = 1; st.ghi = 0; st.cut = -1;
+      st.zf = 1.0f; st.totf = 1.0f; st.klo = 0x7FFFFFFF; st.glo = 1; st.ghi = 0;
       *st_out = st;
     }
     return;
@@ -339,7 +344,7 @@ __global__ void __launch_bounds__(RS_NT) rowstat16_kernel(RowStatArgs a) {
   }
   __syncthreads();
   const int32_t klo = s_i32[0], glo = s_i32[1], ghi = s_i32[2];
-  const int32_t rstar = s_i32[3], needcut = s_i32[5];
+  const int32_t rstar = s_i32[3];
   uint32_t rflags = (uint32_t)s_i32[6];
 
   // ---- 5. kept mass when there is no nucleus: sum over kept keys
@@ -377,71 +382,13 @@ __global__ void __launch_bounds__(RS_NT) rowstat16_kernel(RowStatArgs a) {
   }
   const float totf = fmaxf(rn32_u64(kept_mass), 1e-12f);
 
-  // ---- 6. index cutoff inside the boundary tie group (lowest ids kept first)
-  int64_t cut = -1;
-  if (needcut) {
-    uint32_t cnt = 0;
-    launder_keys(key);
-#pragma unroll
-    for (int j = 0; j < NSLOT; ++j) {
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const int32_t kk = (int32_t)((t & 1) ? (key[j][t >> 1] >> 16) : (key[j][t >> 1] & 0xFFFFu));
-        cnt += (j * 512 + t < rem && kk >= glo && kk <= ghi) ? 1u : 0u;
-      }
-    }
-    cnt = wave_sum_u32(cnt);
-    if (lane == 0) s_u32[wave] = cnt;
-    __syncthreads();
-    if (tid == 0) {
-      uint32_t run = 0;
-      int ws = RS_NW - 1;
-      uint32_t need = (uint32_t)rstar;
-      for (int w2 = 0; w2 < RS_NW; ++w2) {
-        if (run + s_u32[w2] >= (uint32_t)rstar) { ws = w2; need = (uint32_t)rstar - run; break; }
-        run += s_u32[w2];
-      }
-      s_u32[RS_NW] = (uint32_t)ws;
-      s_u32[RS_NW + 1] = need;
-    }
-    __syncthreads();
-    if (wave == (int)s_u32[RS_NW]) {
-      launder_keys(key);
-      const uint32_t need = s_u32[RS_NW + 1];
-      uint32_t run = 0;
-      int32_t fslot = -1, ft = 0;  // slot and in-lane element of the member
-      uint32_t flane = 0;
-#pragma unroll
-      for (int j = 0; j < NSLOT; ++j) {
-        if (fslot < 0) {
-          uint32_t mine = 0;
-#pragma unroll
-          for (int t = 0; t < 8; ++t) {
-            const int32_t kk = (int32_t)((t & 1) ? (key[j][t >> 1] >> 16) : (key[j][t >> 1] & 0xFFFFu));
-            if (j * 512 + t < rem && kk >= glo && kk <= ghi) mine |= 1u << t;
-          }
-          const uint32_t my = __popc(mine);
-          const uint32_t incl = wave_incl_scan_u32(my, lane);
-          const uint32_t tot = (uint32_t)__shfl((int)incl, kWave - 1, kWave);
-          if (run + tot >= need) {
-            const uint32_t want = need - run;  // 1-based rank inside this slot
-            const bool here = incl >= want && incl - my < want;
-            // in-lane element: the (want - (incl - my))-th set bit of `mine`
-            uint32_t bits = mine;
-            for (uint32_t k2 = want - (incl - my); here && k2 > 1; --k2) bits &= bits - 1;
-            const int tl = here ? __ffs((int)bits) - 1 : 0;
-            const uint64_t hitm = __ballot(here);
-            flane = (uint32_t)(__ffsll((unsigned long long)hitm) - 1);
-            ft = __shfl(tl, (int)flane, kWave);
-            fslot = j;
-          }
-          run += tot;
-        }
-      }
-      if (lane == 0) s_i64[0] = fslot < 0 ? -1 : wb + (int64_t)flane * 8 + fslot * 512 + ft;
-    }
-    __syncthreads();
-    cut = s_i64[0];
+  // ---- 6. drafted token inside a partial boundary group: its member rank
+  // (members with lower ids) decides whether it is among the rstar kept.
+  bool g_kept = true;
+  if (gid >= 0 && gid < V && rstar > 0 && rstar < s_i32[4]) {
+    const int32_t kg = (int32_t)key_of_code16(ptr[gid]);
+    if (kg >= glo && kg <= ghi)
+      g_kept = block_count_members(ptr, gid, glo, ghi, s_u32) < (uint32_t)rstar;
   }
 
   // ---- 7. table of final probabilities for the top keys, gathered token, record
@@ -461,7 +408,8 @@ __global__ void __launch_bounds__(RS_NT) rowstat16_kernel(RowStatArgs a) {
     st.klo = klo;
     st.glo = glo;
     st.ghi = ghi;
-    st.cut = needcut ? cut : (rstar > 0 ? INT64_MAX : -1);
+    st.rstar = rstar;
+    st.gcount = s_i32[4];
     st.mass = kept_mass;
     st.flags = rflags;
     st.ntbl = ntbl;
@@ -470,7 +418,7 @@ __global__ void __launch_bounds__(RS_NT) rowstat16_kernel(RowStatArgs a) {
     if (gid >= 0 && gid < V) {
       const uint32_t code = ptr[gid];
       const int32_t kk = (int32_t)key_of_code16(code);
-      const bool kept = kk >= klo && !(kk >= glo && kk <= ghi && gid > st.cut);
+      const bool kept = kk >= klo && (!(kk >= glo && kk <= ghi) || (rstar > 0 && g_kept));
       pg = kept ? p_of_key((uint32_t)kk) / totf : 0.0f;
     }
     st.pgather = pg;

@@ -167,3 +167,99 @@ def test_g1_config1_on_gpu():
                                    _np(ua[:M]), _np(uf[:M]), 1.0)
     assert np.array_equal(n[:M].cpu().numpy(), rn)
     assert np.array_equal(y[:M].cpu().numpy(), ry)
+
+
+def _window_edge_rows(V):
+    """bf16 rows outside the streaming kernel's fixed value window (its
+    fallback recomputes them), mixed with ordinary rows."""
+    g = np.random.default_rng(17)
+    base = (g.standard_normal((8, V)) * 3).astype(np.float32)
+    rows = [base[0].copy() for _ in range(8)]
+    rows[0][[3, 77]] = [3.0e6, 2.5e6]                     # >= 2^21: exception bin
+    rows[1] = (g.standard_normal(V) * 1e-13).astype(np.float32)   # max among tiny values
+    rows[1][[10, 11]] = [0.0, -0.0]
+    rows[2][::7] = -3.0e6                                 # <= -2^21: bin 0, zero mass
+    rows[3][::5] = 1e-20                                  # tiny values share exp(-m)
+    rows[3][1::5] = -1e-30
+    rows[4][:] = -np.inf
+    rows[4][[1, 2, 3]] = [-1e-14, -2e-14, -2e-14]         # max inside the merged tiny bin
+    rows[5] = base[5]                                     # ordinary
+    rows[6][::3] = -2.0e6                                 # just inside the window
+    rows[7][[0, V - 1]] = [2.0e6, 2.0e6]                  # top of the window, tie at both ends
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("T,tp,tk", [(1.0, 1.0, 0), (0.8, 0.95, 0), (0.7, 0.9, 50),
+                                     (4.0e6, 0.9, 0)])
+def test_to_probs_bf16_window_edges(T, tp, tk):
+    V = 4096
+    x = torch.tensor(_window_edge_rows(V), device=DEV).to(torch.bfloat16)
+    got = _np(S.to_probs(x, T, tp, tk))
+    ref = O.to_probs(_np(x), T, tp, tk)
+    _assert_probs_equal(got, ref)
+
+
+def test_rejection_sample_window_edges_and_nonfinite():
+    B, k, V = 4, 1, 4096
+    rows = _window_edge_rows(V)
+    tgt = torch.tensor(rows, device=DEV).to(torch.bfloat16).view(B, 2, V)
+    drf = torch.tensor(rows[::-1].copy(), device=DEV).to(torch.bfloat16)[:B].view(B, 1, V)
+    g = torch.Generator(device=DEV).manual_seed(4)
+    ids = torch.tensor([[3], [10], [0], [1]], device=DEV)
+    ua, uf = uniforms((B, k), g, DEV), uniforms((B,), g, DEV)
+    for T, tp in [(1.0, 1.0), (0.8, 0.95)]:
+        n, y, f = S.rejection_sample(tgt, drf, ids, ua, uf, temperature=T, top_p=tp)
+        rn, ry, rf = O.rejection_sample(_np(tgt), _np(drf), ids.cpu().numpy(), _np(ua), _np(uf),
+                                        T, tp, 0)
+        fin = (rf & 2) == 0                    # rows with +inf/NaN are unspecified
+        assert np.array_equal(f.cpu().numpy() & 2, rf & 2)
+        assert np.array_equal(n.cpu().numpy()[fin], rn[fin])
+        assert np.array_equal(y.cpu().numpy()[fin], ry[fin])
+    bad = tgt.clone()
+    bad[1, 0, 9] = float("inf")
+    _, _, f = S.rejection_sample(bad, drf, ids, ua, uf, temperature=1.0)
+    assert int(f[1]) & 2
+
+
+def _tie_heavy(shape, g, step=0.5, sigma=2.0):
+    """Logits on a coarse grid: boundary tie groups of thousands of members
+    spanning many id chunks."""
+    x = torch.randn(shape, generator=g, device=DEV) * sigma
+    return (torch.round(x / step) * step).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("T,tp,tk", [(1.0, 0.9, 0), (0.8, 0.5, 0), (1.0, 0.97, 3000)])
+def test_to_probs_bf16_large_tie_groups(T, tp, tk):
+    g = torch.Generator(device=DEV).manual_seed(31)
+    x = _tie_heavy((4, 151936), g)
+    got = _np(S.to_probs(x, T, tp, tk))
+    ref = O.to_probs(_np(x), T, tp, tk)
+    _assert_probs_equal(got, ref)
+
+
+@pytest.mark.parametrize("T,tp", [(1.0, 0.9), (0.8, 0.6)])
+def test_rejection_sample_large_tie_groups(T, tp):
+    """Draft tokens drawn from inside the target's boundary tie group (some
+    kept, some dropped by id order), residual draws across group chunks."""
+    B, k, V = 6, 3, 151936
+    g = torch.Generator(device=DEV).manual_seed(41)
+    tgt = _tie_heavy((B, k + 1, V), g)
+    drf = _tie_heavy((B, k, V), g, sigma=2.2)
+    P = O.to_probs(_np(tgt[:, :k]).reshape(B * k, V), T, tp, 0)
+    xt = _np(tgt[:, :k]).reshape(B * k, V)
+    rng = np.random.default_rng(5)
+    ids = np.empty(B * k, np.int64)
+    for r in range(B * k):
+        vmin = xt[r][P[r] > 0].min()              # boundary value of the nucleus
+        grp = np.nonzero(xt[r] == vmin)[0]
+        ids[r] = grp[rng.integers(len(grp))]
+    ids = torch.tensor(ids.reshape(B, k), device=DEV)
+    ua = uniforms((B, k), g, DEV) * 0.05             # mostly accept: exercise later positions
+    ua[::2] = uniforms((B // 2, k), g, DEV)
+    uf = uniforms((B,), g, DEV)
+    n, y, f = S.rejection_sample(tgt, drf, ids, ua, uf, temperature=T, top_p=tp)
+    rn, ry, rf = O.rejection_sample(_np(tgt), _np(drf), ids.cpu().numpy(), _np(ua), _np(uf),
+                                    T, tp, 0)
+    assert np.array_equal(n.cpu().numpy(), rn)
+    assert np.array_equal(y.cpu().numpy(), ry)
+    assert np.array_equal(f.cpu().numpy(), rf)
