@@ -52,12 +52,12 @@ Switches switches(float T, float top_p, int32_t top_k, int64_t V) {
   return s;
 }
 
-// Chunking of the id range for the draw / output kernels: chunks of a
+// Chunking of the id range for the to_probs output kernels: chunks of a
 // multiple of 8 ids, at most 2048 ids (one block round) where the chunk count
-// allows, at most kMaxChunks per row.
+// allows, at most 128 per row.
 void chunking(int64_t V, int64_t* chunk, int* nchunk) {
   int64_t n = (V + 2047) / 2048;
-  if (n > sdx::kMaxChunks) n = sdx::kMaxChunks;
+  if (n > 128) n = 128;
   if (n < 1) n = 1;
   int64_t c = (V + n - 1) / n;
   c = (c + 7) / 8 * 8;
@@ -70,29 +70,24 @@ constexpr int64_t kMaxVocab16 = 16 * 20 * 512;  // register capacity of the row 
 // Workspace of the transform + draw pipeline over `rows` rows and `njobs` draws.
 size_t transform_ws(Carve& c, int64_t rows, int64_t V, int dtype, int64_t njobs,
                     sdx::RowStat** stats, float** tables, float** dense, sdx::SampleJob** jobs,
-                    sdx::ChunkRec** recs) {
-  int64_t chunk;
-  int nchunk;
-  chunking(V, &chunk, &nchunk);
+                    sdx::ChunkRec** recs, uint32_t** counters) {
+  int64_t rec_ids;
+  int nrec;
+  sdx::draw_layout(V, &rec_ids, &nrec);
   *stats = c.take<sdx::RowStat>(rows);
   *tables = dtype == SDX_F32 ? nullptr : c.take<float>((size_t)rows * sdx::kTbl);
   *dense = dtype == SDX_F32 ? c.take<float>((size_t)rows * V) : nullptr;
   *jobs = njobs ? c.take<sdx::SampleJob>(njobs) : nullptr;
-  *recs = njobs ? c.take<sdx::ChunkRec>((size_t)njobs * nchunk) : nullptr;
+  *recs = njobs ? c.take<sdx::ChunkRec>((size_t)njobs * nrec) : nullptr;
+  *counters = njobs ? c.take<uint32_t>((size_t)njobs) : nullptr;
   return c.used;
 }
 
-// Row statistics of 16-bit rows: bf16 rows stream through the fixed-window
-// kernel, and the register-resident kernel recomputes the rows it declines;
-// fp16 rows go to the register-resident kernel directly.
-int row_stats16(int dtype, sdx::RowStatArgs a, int64_t rows, hipStream_t s) {
-  if (dtype == SDX_BF16) {
-    a.fallback_only = 0;
-    if (int e = hip_status(sdx::launch_rowstream_bf16(a, rows, s), "rowstream_bf16")) return e;
-    a.fallback_only = 1;
-  } else {
-    a.fallback_only = 0;
-  }
+// Row statistics of 16-bit rows: bf16 rows stream through the histogram
+// kernel, fp16 rows go to the register-resident kernel.
+int row_stats16(int dtype, const sdx::RowStatArgs& a, int64_t rows, hipStream_t s) {
+  if (dtype == SDX_BF16)
+    return hip_status(sdx::launch_rowstream_bf16(a, rows, s), "rowstream_bf16");
   return hip_status(sdx::launch_rowstat16(dtype, a, rows, s), "rowstat16");
 }
 
@@ -117,9 +112,9 @@ int sdx_version(void) { return 1; }
 // ------------------------------------------------------------------ to_probs
 size_t sdx_to_probs_workspace(int64_t rows, int64_t vocab, int dtype) {
   Carve c{nullptr};
-  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; sdx::ChunkRec* rc;
+  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; sdx::ChunkRec* rc; uint32_t* ct;
   // fp32 rows are written straight to the output: no dense scratch
-  transform_ws(c, rows, vocab, dtype == SDX_F32 ? SDX_BF16 : dtype, 0, &st, &tb, &dn, &jb, &rc);
+  transform_ws(c, rows, vocab, dtype == SDX_F32 ? SDX_BF16 : dtype, 0, &st, &tb, &dn, &jb, &rc, &ct);
   int64_t chunk;
   int nchunk;
   chunking(vocab, &chunk, &nchunk);
@@ -159,8 +154,8 @@ int sdx_to_probs(const void* logits, int dtype, int64_t rows, int64_t vocab, int
       return e;
     return hip_status(sdx::launch_onehot(am, rows, vocab, probs, ld_out, s), "onehot");
   }
-  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; sdx::ChunkRec* rc;
-  transform_ws(c, rows, vocab, dtype, 0, &st, &tb, &dn, &jb, &rc);
+  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; sdx::ChunkRec* rc; uint32_t* ct;
+  transform_ws(c, rows, vocab, dtype, 0, &st, &tb, &dn, &jb, &rc, &ct);
   int64_t chunk;
   int nchunk;
   chunking(vocab, &chunk, &nchunk);
@@ -181,19 +176,21 @@ int sdx_to_probs(const void* logits, int dtype, int64_t rows, int64_t vocab, int
 
 // ------------------------------------------------------------------ sample_from_probs
 size_t sdx_sample_probs_workspace(int64_t rows, int64_t vocab) {
-  int64_t chunk;
-  int nchunk;
-  chunking(vocab, &chunk, &nchunk);
+  int64_t rec_ids;
+  int nrec;
+  sdx::draw_layout(vocab, &rec_ids, &nrec);
   Carve c{nullptr};
   c.take<sdx::SampleJob>(rows);
-  c.take<sdx::ChunkRec>((size_t)rows * nchunk);
+  c.take<sdx::ChunkRec>((size_t)rows * nrec);
+  c.take<uint32_t>((size_t)rows);  // draw counters
   return c.used;
 }
 
 __global__ void sdx_jobs_from_u(sdx::SampleJob* jobs, const float* u, int64_t rows,
-                                int64_t qsplit) {
+                                int64_t qsplit, uint32_t* counters) {
   const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= rows) return;
+  if (counters) counters[r] = 0u;
   sdx::SampleJob j;
   j.prow = r;
   j.qrow = qsplit >= 0 ? qsplit + r : -1;
@@ -211,19 +208,20 @@ int sdx_sample_probs(const float* probs, int64_t rows, int64_t vocab, int64_t ld
   if (!workspace || workspace_bytes < need)
     return fail(SDX_EWORKSPACE, "sdx_sample_probs: workspace %zu < %zu", workspace_bytes, need);
   hipStream_t s = (hipStream_t)stream;
-  int64_t chunk;
-  int nchunk;
-  chunking(vocab, &chunk, &nchunk);
+  int64_t rec_ids;
+  int nrec;
+  sdx::draw_layout(vocab, &rec_ids, &nrec);
   Carve c{(uint8_t*)workspace};
   sdx::SampleJob* jobs = c.take<sdx::SampleJob>(rows);
-  sdx::ChunkRec* recs = c.take<sdx::ChunkRec>((size_t)rows * nchunk);
+  sdx::ChunkRec* recs = c.take<sdx::ChunkRec>((size_t)rows * nrec);
+  uint32_t* counters = c.take<uint32_t>((size_t)rows);
   hipLaunchKernelGGL(sdx_jobs_from_u, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, jobs,
-                     u, rows, (int64_t)-1);
+                     u, rows, (int64_t)-1, counters);
   if (int e = hip_status(hipGetLastError(), "jobs")) return e;
   const bool vec = aligned16(probs) && (ld % 4) == 0;
   sdx::RowSourceF32 src{probs, ld, probs, ld, rows, vec};
   return hip_status(
-      sdx::launch_draw_probs(src, nullptr, jobs, rows, vocab, chunk, nchunk, recs, ids, s),
+      sdx::launch_draw_probs(src, nullptr, jobs, rows, vocab, recs, counters, ids, s),
       "draw_probs");
 }
 
@@ -242,21 +240,21 @@ int sdx_residual_probs(const float* p, const float* q, int64_t rows, int64_t voc
   if (!workspace || workspace_bytes < need)
     return fail(SDX_EWORKSPACE, "sdx_residual_probs: workspace %zu < %zu", workspace_bytes, need);
   hipStream_t s = (hipStream_t)stream;
-  int64_t chunk;
-  int nchunk;
-  chunking(vocab, &chunk, &nchunk);
+  int64_t rec_ids;
+  int nrec;
+  sdx::draw_layout(vocab, &rec_ids, &nrec);
   Carve c{(uint8_t*)workspace};
   sdx::SampleJob* jobs = c.take<sdx::SampleJob>(rows);
-  sdx::ChunkRec* recs = c.take<sdx::ChunkRec>((size_t)rows * nchunk);
+  sdx::ChunkRec* recs = c.take<sdx::ChunkRec>((size_t)rows * nrec);
   hipLaunchKernelGGL(sdx_jobs_from_u, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, jobs,
-                     (const float*)nullptr, rows, rows);
+                     (const float*)nullptr, rows, rows, (uint32_t*)nullptr);
   if (int e = hip_status(hipGetLastError(), "jobs")) return e;
   const bool vec = aligned16(p) && aligned16(q) && (ld % 4) == 0;
   sdx::RowSourceF32 src{p, ld, q, ld, rows, vec};
-  if (int e = hip_status(sdx::launch_chunk_mass_probs(src, jobs, rows, vocab, chunk, nchunk, recs, s),
+  if (int e = hip_status(sdx::launch_chunk_mass_probs(src, jobs, rows, vocab, recs, s),
                          "chunk_mass"))
     return e;
-  sdx::ResidualNormArgs a{p, q, ld, vocab, chunk, nchunk, recs, out, ld_out};
+  sdx::ResidualNormArgs a{p, q, ld, vocab, rec_ids, nrec, recs, out, ld_out};
   return hip_status(sdx::launch_residual_norm(a, rows, s), "residual_norm");
 }
 
@@ -273,9 +271,9 @@ int sdx_gather_prob(const float* probs, int64_t rows, int64_t vocab, int64_t ld,
 // ------------------------------------------------------------------ verify
 size_t sdx_verify_workspace(int64_t batch, int32_t k, int64_t vocab, int dtype) {
   Carve c{nullptr};
-  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; sdx::ChunkRec* rc;
+  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; sdx::ChunkRec* rc; uint32_t* ct;
   const int64_t rows = batch * (2 * (int64_t)k + 1);
-  transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jb, &rc);
+  transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jb, &rc, &ct);
   c.take<int64_t>(batch * ((int64_t)k + 1));  // greedy argmax
   return c.used;
 }
@@ -328,9 +326,10 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
   const Switches sw = switches(temperature, top_p, top_k, vocab);
   Carve c{(uint8_t*)workspace};
   sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jobs; sdx::ChunkRec* recs;
+  uint32_t* counters;
   const int64_t ntgt = batch * ((int64_t)k + 1), ndrf = batch * (int64_t)k;
   const int64_t rows = ntgt + ndrf;
-  transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jobs, &recs);
+  transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jobs, &recs, &counters);
   int64_t* am = c.take<int64_t>(ntgt);
   if (sw.greedy) {
     // one-hot p: only the target argmax matters (see sdx_verify_greedy)
@@ -343,9 +342,6 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
                       "greedy_accept");
   }
   if (!draft_logits) return fail(SDX_EINVAL, "sdx_verify: draft_logits required when T > 0");
-  int64_t chunk;
-  int nchunk;
-  chunking(vocab, &chunk, &nchunk);
   if (dtype == SDX_F32) {
     sdx::F32Args a = {};
     a.base[0] = (const float*)target_logits; a.nrows[0] = ntgt; a.ld[0] = vocab;
@@ -354,6 +350,7 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
     a.T = temperature; a.top_p = top_p; a.top_k = top_k;
     a.use_p = sw.use_p; a.use_k = sw.use_k; a.greedy = 0;
     a.out = dn; a.ld_out = vocab; a.stats = st;
+    a.zero = counters; a.nzero = batch;
     if (int e = hip_status(sdx::launch_to_probs_f32(a, rows, s), "to_probs_f32")) return e;
   } else {
     if (!aligned16(target_logits) || !aligned16(draft_logits) || (vocab % 8) != 0)
@@ -366,20 +363,21 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
     a.T = temperature; a.top_p = top_p; a.top_k = top_k;
     a.use_p = sw.use_p; a.use_k = sw.use_k; a.greedy = 0;
     a.stats = st; a.tables = tb;
+    a.zero = counters; a.nzero = batch;
     if (int e = row_stats16(dtype, a, rows, s)) return e;
   }
   if (stats_only) return SDX_OK;
   sdx::AcceptArgs aa{st, batch, k, u_accept, u_final, active, jobs, n_acc, flags};
   if (dtype == SDX_F32) {
     sdx::RowSourceF32 src{dn, vocab, dn, vocab, rows, (vocab % 4) == 0};
-    return hip_status(
-        sdx::launch_draw_probs(src, &aa, jobs, batch, vocab, chunk, nchunk, recs, y, s),
-        "draw_probs");
+    return hip_status(sdx::launch_draw_probs(src, &aa, jobs, batch, vocab, recs,
+                                             counters, y, s),
+                      "draw_probs");
   }
   sdx::RowSource16 src{(const uint16_t*)target_logits, vocab, (const uint16_t*)draft_logits, vocab,
                        ntgt, true};
   return hip_status(sdx::launch_draw16(dtype, src, st, tb, temperature, &aa, jobs, batch, vocab,
-                                       chunk, nchunk, recs, y, s),
+                                       recs, counters, y, s),
                     "draw16");
 }
 

@@ -82,15 +82,15 @@ __device__ __forceinline__ float exp_det(float d) {
 }
 
 // ---------------------------------------------------------------- fixed point
-// floor(x * 2^62) for fp32 x in [0, 1].
+// floor(x * 2^62) for fp32 x in [0, 1] (branch-free: both shifts, one select).
 __device__ __forceinline__ uint64_t fixed62(float x) {
   const uint32_t b = __float_as_uint(x);
   const uint32_t e = b >> 23;
   const uint64_t mant = (uint64_t)((b & 0x7FFFFFu) | (e ? 0x800000u : 0u));
-  const int sh = (int)(e ? e : 1u) - 88;  // value = mant * 2^(eff - 150)
-  if (sh >= 0) return mant << sh;
-  if (sh <= -64) return 0;
-  return mant >> (-sh);
+  const int sh = (int)(e ? e : 1u) - 88;  // value = mant * 2^(eff - 150), sh <= 39
+  const uint64_t up = mant << (sh & 63);
+  const uint64_t dn = mant >> ((-sh) & 63);
+  return sh >= 0 ? up : (sh <= -64 ? 0ull : dn);
 }
 
 // i * 2^-62 rounded once to fp32 (nearest, ties to even).
@@ -172,20 +172,64 @@ __device__ __forceinline__ uint64_t uniform_threshold(float u, uint64_t total) {
 }
 
 // ---------------------------------------------------------------- reductions
+// Wave-wide scans and sums: a Hillis-Steele scan inside each 16-lane row with
+// DPP row shifts (lanes shifted in from outside the row read 0), then the row
+// totals (lanes 15, 31, 47) are added through scalar registers.
+__device__ __forceinline__ uint32_t dpp_shr(uint32_t v, int n) {
+  switch (n) {
+    case 1: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, true);
+    case 2: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, true);
+    case 4: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, true);
+    default: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, true);
+  }
+}
+__device__ __forceinline__ uint32_t rdlane(uint32_t v, int l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
+}
+// Inclusive prefix sum across the 64 lanes.
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) v += dpp_shr(v, o);
+  const uint32_t r0 = rdlane(v, 15), r1 = rdlane(v, 31), r2 = rdlane(v, 47);
+  const int row = lane >> 4;
+  v += row >= 1 ? r0 : 0u;
+  v += row >= 2 ? r1 : 0u;
+  v += row >= 3 ? r2 : 0u;
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v, int lane) {
+  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) {
+    const uint32_t tl = dpp_shr(lo, o), th = dpp_shr(hi, o);
+    const uint32_t nl = lo + tl;
+    hi += th + (nl < lo ? 1u : 0u);
+    lo = nl;
+  }
+  const uint64_t r0 = ((uint64_t)rdlane(hi, 15) << 32) | rdlane(lo, 15);
+  const uint64_t r1 = ((uint64_t)rdlane(hi, 31) << 32) | rdlane(lo, 31);
+  const uint64_t r2 = ((uint64_t)rdlane(hi, 47) << 32) | rdlane(lo, 47);
+  uint64_t x = ((uint64_t)hi << 32) | lo;
+  const int row = lane >> 4;
+  x += row >= 1 ? r0 : 0ull;
+  x += row >= 2 ? r1 : 0ull;
+  x += row >= 3 ? r2 : 0ull;
+  return x;
+}
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, kWave));
-  return v;
+  for (int o = 1; o < 16; o <<= 1) v = max(v, dpp_shr(v, o));
+  return max(max(rdlane(v, 15), rdlane(v, 31)), max(rdlane(v, 47), rdlane(v, 63)));
 }
+// Sums: the result is uniform across the wave.
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o, kWave);
-  return v;
+  for (int o = 1; o < 16; o <<= 1) v += dpp_shr(v, o);
+  return rdlane(v, 15) + rdlane(v, 31) + rdlane(v, 47) + rdlane(v, 63);
 }
 __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += (uint64_t)__shfl_xor((long long)v, o, kWave);
-  return v;
+  const uint64_t x = wave_incl_scan_u64(v, (int)(threadIdx.x & 63));
+  return ((uint64_t)rdlane((uint32_t)(x >> 32), 63) << 32) | rdlane((uint32_t)x, 63);
 }
 __device__ __forceinline__ int64_t wave_min_i64(int64_t v) {
 #pragma unroll
@@ -199,23 +243,6 @@ __device__ __forceinline__ U128 wave_sum_u128(U128 v) {
     w.lo = (uint64_t)__shfl_xor((long long)v.lo, o, kWave);
     w.hi = (uint64_t)__shfl_xor((long long)v.hi, o, kWave);
     v = u128_add(v, w);
-  }
-  return v;
-}
-// Inclusive prefix sum across the 64 lanes.
-__device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v, int lane) {
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint64_t t = (uint64_t)__shfl_up((long long)v, o, kWave);
-    if (lane >= o) v += t;
-  }
-  return v;
-}
-__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v, int lane) {
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint32_t t = (uint32_t)__shfl_up((int)v, o, kWave);
-    if (lane >= o) v += t;
   }
   return v;
 }

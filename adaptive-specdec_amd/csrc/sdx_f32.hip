@@ -37,6 +37,7 @@ __global__ void __launch_bounds__(F32_NT) to_probs_f32_kernel(F32Args a) {
 
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
+  if (tid == 0 && row < a.nzero) a.zero[row] = 0u;
   const int g = row < a.nrows[0] ? 0 : 1;
   const int64_t r = g ? row - a.nrows[0] : row;
   const float* x = a.base[g] + r * a.ld[g];

@@ -19,8 +19,7 @@ enum RowFlag : uint32_t {
   kRowNonfinite = 1u << 1,   // +inf / +NaN in the row (results unspecified)
   kRowUnsupported = 1u << 2, // decision fell outside the histogram window
   kRowBelowWindow = 1u << 3, // elements below the histogram window carry mass
-  kRowProbs = 1u << 4,       // final probabilities stored densely (fp32 path)
-  kRowFallback = 1u << 5     // streaming kernel declined the row: recompute it
+  kRowProbs = 1u << 4        // final probabilities stored densely (fp32 path)
 };
 
 // 64 bytes per row. Keys in [glo, ghi] form the tie group that straddles the
@@ -76,15 +75,21 @@ __device__ __forceinline__ int cls16(const RowStat& st, int32_t key) {
   if (key < st.klo) return 0;
   return (key >= st.glo && key <= st.ghi) ? 1 : 2;
 }
+// Final probability of a key below the table (out of line, so the compiler
+// cannot if-convert the fp64 exp into every table lookup).
+template <int FMT>
+__device__ __noinline__ float val16_exp(uint32_t code, float T, float m, float zf, float totf) {
+  const float s = decode16<FMT>(code) / T;
+  const float p = exp_det(s - m) / zf;
+  return p / totf;
+}
 // Final probability of a kept (class 2) or kept-member element.
 template <int FMT>
 __device__ __forceinline__ float val16(const RowStat& st, const float* tbl, uint32_t code,
                                        float T) {
   const int32_t t = st.kmax - (int32_t)key_of_code16(code);
   if (t < st.ntbl) return tbl[t];
-  const float s = decode16<FMT>(code) / T;
-  const float p = exp_det(s - st.m) / st.zf;
-  return p / st.totf;
+  return val16_exp<FMT>(code, T, st.m, st.zf, st.totf);
 }
 
 // Where rows live: rows [0, split) at base + row*ld, the rest at

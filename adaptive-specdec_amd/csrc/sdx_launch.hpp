@@ -17,9 +17,10 @@ struct RowStatArgs {
   float top_p;
   int32_t top_k;
   int32_t use_p, use_k, greedy;
-  int32_t fallback_only;  // register kernel: only rows flagged kRowFallback
   RowStat* stats;
   float* tables;  // [rows, kTbl]
+  uint32_t* zero;  // words [0, nzero) cleared (block `row` clears word `row`), or null
+  int64_t nzero;
 };
 
 struct F32Args {
@@ -34,6 +35,8 @@ struct F32Args {
   float* out;  // dense probabilities [rows, ld_out]
   int64_t ld_out;
   RowStat* stats;  // may be null
+  uint32_t* zero;  // words [0, nzero) cleared (block `row` clears word `row`), or null
+  int64_t nzero;
 };
 
 // One final draw: weights from row `prow` (and `qrow` for a residual).
@@ -73,16 +76,25 @@ struct ChunkRec {
 };
 static_assert(sizeof(ChunkRec) == 64, "ChunkRec layout");
 
-constexpr int kMaxChunks = 128;
+// Draw records: one ChunkRec per `rec_ids` consecutive ids of a job's rows, a
+// multiple of one wave round (64 lanes x 8 ids); at most kMaxRecs per job.
+constexpr int kDrawSub = 512;
+constexpr int kMaxRecs = 4096;
+inline void draw_layout(int64_t V, int64_t* rec_ids, int* nrec) {
+  const int64_t span = (int64_t)kDrawSub * kMaxRecs;
+  const int64_t rounds = V > span ? (V + span - 1) / span : 1;
+  *rec_ids = rounds * kDrawSub;
+  *nrec = (int)((V + *rec_ids - 1) / *rec_ids);
+}
 
 struct ResidualNormArgs {
   const float* p;
   const float* q;
   int64_t ld;
   int64_t V;
-  int64_t chunk;
-  int32_t nchunk;
-  const ChunkRec* recs;  // chunk records of jobs (one job per row)
+  int64_t rec_ids;
+  int32_t nrec;
+  const ChunkRec* recs;  // draw records of the rows (one job per row)
   float* out;
   int64_t ld_out;
 };
@@ -96,19 +108,21 @@ hipError_t launch_rowstream_bf16(const RowStatArgs& a, int64_t rows, hipStream_t
 constexpr int64_t kF32MaxVocab = 8192;
 hipError_t launch_to_probs_f32(const F32Args& a, int64_t rows, hipStream_t s);
 // sdx_sample.hip
-// Draw pipeline: chunk records (with the accept chain when `acc` is given:
-// jobs are then written by the kernel) and the per-job select. Without `acc`,
-// `jobs` must hold the draws already.
+// Draw: chunk records and the per-job select in one launch (with the accept
+// chain when `acc` is given: jobs are then written by the kernel). Without
+// `acc`, `jobs` must hold the draws already.
+// `counters` ([njobs] words) must be zero on entry: the kernel launched just
+// before the draw clears them (RowStatArgs / F32Args `zero`).
+// `recs` holds njobs * nrec records (draw_layout).
 hipError_t launch_draw16(int fmt, const RowSource16& src, const RowStat* stats,
                          const float* tables, float T, const AcceptArgs* acc, SampleJob* jobs,
-                         int64_t njobs, int64_t V, int64_t chunk, int nchunk, ChunkRec* recs,
-                         int64_t* y, hipStream_t s);
+                         int64_t njobs, int64_t V, ChunkRec* recs, uint32_t* counters, int64_t* y,
+                         hipStream_t s);
 hipError_t launch_draw_probs(const RowSourceF32& src, const AcceptArgs* acc, SampleJob* jobs,
-                             int64_t njobs, int64_t V, int64_t chunk, int nchunk, ChunkRec* recs,
+                             int64_t njobs, int64_t V, ChunkRec* recs, uint32_t* counters,
                              int64_t* y, hipStream_t s);
 hipError_t launch_chunk_mass_probs(const RowSourceF32& src, SampleJob* jobs, int64_t njobs,
-                                   int64_t V, int64_t chunk, int nchunk, ChunkRec* recs,
-                                   hipStream_t s);
+                                   int64_t V, ChunkRec* recs, hipStream_t s);
 // to_probs output of 16-bit rows; `counts` holds rows * nchunk words.
 hipError_t launch_materialize16(int fmt, const RowSource16& src, const RowStat* stats,
                                 const float* tables, float T, int64_t rows, int64_t V,

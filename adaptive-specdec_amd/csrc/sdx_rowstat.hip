@@ -18,8 +18,8 @@
 // Keys below the window (logits more than ~2^28 below the maximum at
 // ordinary temperatures) carry exp_det == 0 and are checked to do so.
 //
-// This kernel serves every fp16 row, and the bf16 rows the streaming kernel
-// (sdx_rowstream.hip) declines (`fallback_only`: rows flagged kRowFallback).
+// This kernel serves fp16 rows; bf16 rows go through the streaming kernel
+// (sdx_rowstream.hip).
 #include "sdx_launch.hpp"
 
 namespace sdx {
@@ -87,7 +87,6 @@ __global__ void __launch_bounds__(RS_NT) rowstat16_kernel(RowStatArgs a) {
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int64_t row = blockIdx.x;
-  if (a.fallback_only && !(a.stats[row].flags & kRowFallback)) return;  // uniform per block
   const int g = row < a.nrows[0] ? 0 : 1;
   const int64_t r = g ? row - a.nrows[0] : row;
   const uint16_t* __restrict__ ptr = a.base[g] + r * a.ld[g];
@@ -106,6 +105,7 @@ __global__ void __launch_bounds__(RS_NT) rowstat16_kernel(RowStatArgs a) {
   const int64_t we = min(V, wb + cw);
   RowStat* st_out = a.stats + row;
   float* tbl_out = a.tables + row * kTbl;
+  if (tid == 0 && row < a.nzero) a.zero[row] = 0u;
 
   // Element (j, t) of this lane is id wb + j*512 + lane*8 + t; it exists iff
   // j*512 + t < rem. All per-slot checks compare one register with constants.

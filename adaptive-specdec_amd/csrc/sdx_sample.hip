@@ -1,22 +1,23 @@
 // Accept test, residual / bonus inverse-CDF sampling and to_probs output.
 //
-// Stages after the row statistics (specdec/engine.py:285-303):
-//   chunk_kernel    (jobs x chunks) grid. With the accept chain fused in, each
-//                   block first replays its batch row's accept chain
-//                   u < min(1, p(x)/max(q(x), 1e-10)) with the first-reject
-//                   scan (sampling.py:117-129; block 0 of the row publishes
-//                   n_acc, flags and the draw: residual at the stop position
-//                   or bonus from p_{k+1}), then reduces one chunk of ids to a
-//                   ChunkRec: exact fixed62 partial sums that do not yet know
-//                   which members of the rows' boundary tie groups are kept.
-//   select_kernel   one workgroup per draw: prefix counts of group members
-//                   over the chunks give every chunk its member ranks, hence
-//                   its exact residual (p - q)_+ and p masses (at most two
-//                   chunks per draw, the ones where a group's kept count runs
-//                   out, are rescanned in id order); the degenerate-residual
-//                   rule (sampling.py:85-88); target floor(u * total); the
-//                   chunk holding it; a block scan in id order for the first
-//                   id whose prefix mass exceeds it.
+// Stages after the row statistics (specdec/engine.py:285-303), one launch:
+//   draw_kernel  (jobs x blocks-per-job) grid. With the accept chain fused in,
+//                wave 0 of each block replays its batch row's accept chain
+//                u < min(1, p(x)/max(q(x), 1e-10)) with the first-reject scan
+//                (sampling.py:117-129), one lane per position; block 0 of the
+//                row publishes n_acc, flags and the draw (residual at the stop
+//                position or bonus from p_{k+1}). Every wave then reduces a run
+//                of 512-id rounds of the draw's rows to ChunkRecs: exact fixed62
+//                partial sums that do not yet know which members of the rows'
+//                boundary tie groups are kept. The block that completes a job's
+//                records (an agent-scope counter) draws: prefix counts of group
+//                members over the records give each its member ranks, hence its
+//                exact residual (p - q)_+ and p masses (at most two records,
+//                where a group's kept count runs out, are rescanned in id order
+//                by one wave each); the degenerate-residual rule
+//                (sampling.py:85-88); target floor(u * total); the record
+//                holding it; a wave scan in id order for the first id whose
+//                prefix mass exceeds it.
 // Element probabilities come from an evaluator: codes + RowStat + table for
 // 16-bit logits, or dense fp32 probability rows (which have no groups).
 #include "sdx_launch.hpp"
@@ -63,13 +64,18 @@ __device__ inline uint64_t block_excl_u64(uint64_t v, uint64_t* s, uint64_t* tot
 }
 
 // ---------------------------------------------------------------- evaluators
-// load8 returns the probabilities of ids idx..idx+7 (0 at or past `lim`) and
-// the bitmask of the ids that belong to the row's boundary tie group; those
-// carry the group value (the value of a kept member) and the caller zeroes
-// the members whose rank is >= rstar.
+// fetch() loads the raw data of ids idx..idx+7 (ids at or past `lim` read as
+// nothing); eval() turns it into probabilities (0 past `lim`) and returns in
+// bits 0..7 the ids in the row's boundary tie group (those carry the group
+// value, the value of a kept member; the caller zeroes the members whose rank
+// is >= rstar) and in bits 8..15 the ids that may carry probability. load8()
+// is both, returning the group bits.
 template <int FMT>
 struct Eval16 {
   static constexpr bool kGroups = true;
+  static constexpr int kFmt = FMT;
+  static constexpr int kLdsTbl = kTbl;
+  using Raw = uint4;
   const uint16_t* base;
   int64_t ld;
   const uint16_t* base2;
@@ -85,43 +91,75 @@ struct Eval16 {
     const float* tbl;
     float vg;  // probability of a kept group member
   };
-  // Whole block: copy the row's table to LDS (call before bind, then sync).
+  // Whole block: copy the row's table to LDS (then sync, then bind with it).
   __device__ void stage(int64_t row, float* lds) const {
     const int n = stats[row].ntbl;
     const float* src = tables + row * kTbl;
     for (int t = threadIdx.x; t < n; t += blockDim.x) lds[t] = src[t];
   }
-  __device__ void bind(Row& r, int64_t row, const float* lds) const {
+  // `tbl`: the staged LDS copy of the row's table.
+  __device__ void bind(Row& r, int64_t row, const float* tbl) const {
     r.ptr = row < split ? base + row * ld : base2 + (row - split) * ld2;
     r.st = stats[row];
-    r.tbl = lds;
-    r.vg = r.st.glo <= r.st.ghi ? val16<FMT>(r.st, lds, code_of_key16((uint32_t)r.st.glo), T)
-                                : 0.0f;
+    r.tbl = tbl;
+    r.vg = r.st.glo <= r.st.ghi
+               ? val16<FMT>(r.st, r.tbl, code_of_key16((uint32_t)r.st.glo), T)
+               : 0.0f;
   }
   __device__ static int32_t rstar(const Row& r) { return r.st.rstar; }
-  __device__ uint32_t load8(const Row& r, int64_t idx, int64_t lim, float v[8]) const {
-    uint32_t c[8];
-    if (idx + 8 <= lim) {  // rows start 16-byte aligned and idx is a multiple of 8
-      const uint4 w = *reinterpret_cast<const uint4*>(r.ptr + idx);
-      c[0] = w.x & 0xFFFFu; c[1] = w.x >> 16; c[2] = w.y & 0xFFFFu; c[3] = w.y >> 16;
-      c[4] = w.z & 0xFFFFu; c[5] = w.z >> 16; c[6] = w.w & 0xFFFFu; c[7] = w.w >> 16;
-    } else {
+  __device__ Raw fetch(const Row& r, int64_t idx, int64_t lim) const {
+    if (idx + 8 <= lim)  // rows start 16-byte aligned and idx is a multiple of 8
+      return *reinterpret_cast<const uint4*>(r.ptr + idx);
+    uint32_t w[4] = {0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu};
 #pragma unroll
-      for (int t = 0; t < 8; ++t) c[t] = idx + t < lim ? r.ptr[idx + t] : 0xFFFFu;
-    }
-    uint32_t mask = 0;
+    for (int t = 0; t < 8; ++t)
+      if (idx + t < lim)
+        w[t >> 1] = (w[t >> 1] & ~(0xFFFFu << (16 * (t & 1)))) |
+                    ((uint32_t)r.ptr[idx + t] << (16 * (t & 1)));
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  // Branch-free: every id reads the table at a clamped index and selects;
+  // kept keys below the table (rare) take the exp path under a wave vote.
+  __device__ uint32_t eval(const Row& r, int64_t idx, int64_t lim, const Raw& raw,
+                           float v[8]) const {
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+    const int32_t klo = r.st.klo, glo = r.st.glo, ghi = r.st.ghi, kmax = r.st.kmax;
+    const int32_t tmax = max(r.st.ntbl - 1, 0);
+    uint32_t mask = 0, slow = 0;
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-      const int cl = idx + t < lim ? cls16(r.st, (int32_t)key_of_code16(c[t])) : 0;
-      v[t] = cl == 2 ? val16<FMT>(r.st, r.tbl, c[t], T) : (cl == 1 ? r.vg : 0.0f);
-      mask |= (cl == 1 ? 1u : 0u) << t;
+      const uint32_t code = (t & 1) ? (w[t >> 1] >> 16) : (w[t >> 1] & 0xFFFFu);
+      const int32_t key = (int32_t)key_of_code16(code);
+      const bool live = idx + t < lim && key >= klo;
+      const bool mem = live && key >= glo && key <= ghi;
+      const int32_t tt = kmax - key;
+      const float tv = r.tbl[min(max(tt, 0), tmax)];
+      v[t] = live ? (mem ? r.vg : tv) : 0.0f;
+      mask |= ((mem ? 1u : 0u) << t) | ((live ? 1u : 0u) << (8 + t));
+      slow |= (live && !mem && tt > tmax ? 1u : 0u) << t;
+    }
+    if (__builtin_expect(__ballot(slow != 0) != 0, 0)) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+        if ((slow >> t) & 1u) {
+          const uint32_t code = (t & 1) ? (w[t >> 1] >> 16) : (w[t >> 1] & 0xFFFFu);
+          v[t] = val16_exp<FMT>(code, T, r.st.m, r.st.zf, r.st.totf);
+        }
     }
     return mask;
+  }
+  __device__ uint32_t load8(const Row& r, int64_t idx, int64_t lim, float v[8]) const {
+    return eval(r, idx, lim, fetch(r, idx, lim), v) & 0xFFu;
   }
 };
 
 struct EvalProb {
   static constexpr bool kGroups = false;
+  static constexpr int kFmt = SDX_F32;
+  static constexpr int kLdsTbl = 1;
+  struct Raw {
+    float4 a, b;
+  };
   const float* base;
   int64_t ld;
   const float* base2;
@@ -130,53 +168,81 @@ struct EvalProb {
   bool vec;
   struct Row {
     const float* ptr;
+    float vg;
   };
   __device__ void stage(int64_t, float*) const {}
   __device__ void bind(Row& r, int64_t row, const float*) const {
     r.ptr = row < split ? base + row * ld : base2 + (row - split) * ld2;
+    r.vg = 0.0f;
   }
   __device__ static int32_t rstar(const Row&) { return 0; }
-  __device__ uint32_t load8(const Row& r, int64_t idx, int64_t lim, float v[8]) const {
+  __device__ Raw fetch(const Row& r, int64_t idx, int64_t lim) const {
+    Raw x;
     if (vec && idx + 8 <= lim) {
-      const float4 a = *reinterpret_cast<const float4*>(r.ptr + idx);
-      const float4 b = *reinterpret_cast<const float4*>(r.ptr + idx + 4);
-      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+      x.a = *reinterpret_cast<const float4*>(r.ptr + idx);
+      x.b = *reinterpret_cast<const float4*>(r.ptr + idx + 4);
     } else {
+      float v[8];
 #pragma unroll
       for (int t = 0; t < 8; ++t) v[t] = idx + t < lim ? r.ptr[idx + t] : 0.0f;
+      x.a = make_float4(v[0], v[1], v[2], v[3]);
+      x.b = make_float4(v[4], v[5], v[6], v[7]);
     }
-    return 0u;
+    return x;
+  }
+  __device__ uint32_t eval(const Row&, int64_t idx, int64_t lim, const Raw& x, float v[8]) const {
+    v[0] = x.a.x; v[1] = x.a.y; v[2] = x.a.z; v[3] = x.a.w;
+    v[4] = x.b.x; v[5] = x.b.y; v[6] = x.b.z; v[7] = x.b.w;
+    uint32_t live = 0;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      if (idx + t >= lim) v[t] = 0.0f;
+      live |= (v[t] > 0.0f ? 1u : 0u) << (8 + t);
+    }
+    return live;  // no tie groups; bits 8..15: nonzero probabilities
+  }
+  __device__ uint32_t load8(const Row& r, int64_t idx, int64_t lim, float v[8]) const {
+    return eval(r, idx, lim, fetch(r, idx, lim), v) & 0xFFu;
   }
 };
 
 // ---------------------------------------------------------------- accept chain
-// The accept chain of batch row b (one thread): fills the draw and returns
-// n_acc; *fl receives the row's SDX_FLAG bits.
-__device__ inline int64_t accept_chain(const AcceptArgs& a, int64_t b, SampleJob* job,
-                                       uint32_t* fl_out) {
+// Wave 0, one lane per draft position (64 at a time): the accept chain of
+// batch row b. Returns n_acc and fills the draw; *fl_out gets the SDX_FLAG bits.
+// Position i is evaluated iff the row is active and every earlier position
+// accepted, so the chain stops at the first rejection.
+__device__ inline int64_t accept_chain_wave(const AcceptArgs& a, int64_t b, SampleJob* job,
+                                            uint32_t* fl_out) {
+  const int lane = threadIdx.x & (kWave - 1);
   const int k = a.k;
   const int64_t trow0 = b * (k + 1);
   const int64_t drow0 = a.batch * (k + 1) + b * k;
-  bool alive = a.active ? a.active[b] != 0 : true;
-  int n = 0;
+  const bool alive = a.active ? a.active[b] != 0 : true;
+  int n = alive ? k : 0;
   uint32_t fl = 0;
-  for (int i = 0; i < k; ++i) {
-    const float px = a.stats[trow0 + i].pgather;
-    const float qx = a.stats[drow0 + i].pgather;
-    const float ratio = px / fmaxf(qx, 1e-10f);
-    const float r1 = fminf(ratio, 1.0f);
-    const float u = a.u_accept[b * k + i];
-    const bool evaluated = alive && n == i;
-    const bool ok = evaluated && (u < r1);
-    if (evaluated && fabsf(u - r1) < 1e-5f) fl |= SDX_FLAG_ACCEPT_NEAR_TIE;
-    n += ok ? 1 : 0;
-    alive = alive && ok;
+  for (int i0 = 0; alive && n == k && i0 < k; i0 += kWave) {  // uniform loop
+    const int i = i0 + lane;
+    bool ok = true, near = false;
+    if (i < k) {
+      const float px = a.stats[trow0 + i].pgather;
+      const float qx = a.stats[drow0 + i].pgather;
+      const float r1 = fminf(px / fmaxf(qx, 1e-10f), 1.0f);
+      const float u = a.u_accept[b * k + i];
+      ok = u < r1;
+      near = fabsf(u - r1) < 1e-5f;
+    }
+    const uint64_t fm = __ballot(!ok);
+    const int first = fm ? __ffsll((unsigned long long)fm) - 1 : kWave;
+    if (__ballot(near && lane <= first)) fl |= SDX_FLAG_ACCEPT_NEAR_TIE;
+    if (fm) n = i0 + first;
   }
-  for (int i = 0; i <= k; ++i)
-    if (a.stats[trow0 + i].flags & kRowNonfinite) fl |= SDX_FLAG_NONFINITE;
-  for (int i = 0; i < k; ++i)
-    if (a.stats[drow0 + i].flags & kRowNonfinite) fl |= SDX_FLAG_NONFINITE;
+  for (int i0 = 0; i0 < 2 * k + 1; i0 += kWave) {
+    const int i = i0 + lane;
+    uint32_t rf = 0;
+    if (i < 2 * k + 1) rf = a.stats[i <= k ? trow0 + i : drow0 + (i - k - 1)].flags;
+    if (__ballot((rf & kRowNonfinite) != 0)) fl |= SDX_FLAG_NONFINITE;
+    if (__ballot((rf & kRowUnsupported) != 0)) fl |= SDX_FLAG_UNSUPPORTED;
+  }
   job->prow = n == k ? trow0 + k : trow0 + n;
   job->qrow = n == k ? -1 : drow0 + n;
   job->u = a.u_final[b];
@@ -185,141 +251,76 @@ __device__ inline int64_t accept_chain(const AcceptArgs& a, int64_t b, SampleJob
   return n;
 }
 
-// ---------------------------------------------------------------- chunk records
-struct ChunkArgs {
-  AcceptArgs acc;   // acc.stats == null: jobs are given
-  SampleJob* jobs;
-  int64_t V;
-  int64_t chunk;    // ids per chunk (multiple of 8)
-  int32_t nchunk;
-  ChunkRec* recs;   // [jobs, nchunk]
-};
-
-template <class Ev>
-__global__ void __launch_bounds__(SM_NT) chunk_kernel(Ev ev, ChunkArgs a) {
-  __shared__ float tbl_p[kTbl];
-  __shared__ float tbl_q[kTbl];
-  __shared__ SampleJob s_job;
-  __shared__ uint64_t red64[5 * SM_NW];
-  __shared__ uint32_t red32[3 * SM_NW];
-  const int64_t j = (int64_t)blockIdx.x / a.nchunk;
-  const int c = (int)((int64_t)blockIdx.x % a.nchunk);
-  if (threadIdx.x == 0) {
-    if (a.acc.stats) {
-      SampleJob jb;
-      uint32_t fl;
-      const int64_t n = accept_chain(a.acc, j, &jb, &fl);
-      if (c == 0) {
-        a.jobs[j] = jb;
-        if (a.acc.n_acc) a.acc.n_acc[j] = n;
-        if (a.acc.flags) a.acc.flags[j] = (uint8_t)fl;
-      }
-      s_job = jb;
-    } else {
-      s_job = a.jobs[j];
-    }
-  }
-  __syncthreads();
-  const SampleJob job = s_job;
-  const bool hasq = job.qrow >= 0;
-  ev.stage(job.prow, tbl_p);
-  if (hasq) ev.stage(job.qrow, tbl_q);
-  __syncthreads();
-  typename Ev::Row rp, rq;
-  ev.bind(rp, job.prow, tbl_p);
-  if (hasq) ev.bind(rq, job.qrow, tbl_q);
-  const int64_t c0 = (int64_t)c * a.chunk;
-  const int64_t c1 = min(a.V, c0 + a.chunk);
-  uint64_t p2 = 0, r0 = 0, ra = 0, rb = 0, rpm = 0;
-  uint32_t np = 0, nq = 0, ndbl = 0;
-  for (int64_t idx = c0 + (int64_t)threadIdx.x * 8; idx < c1; idx += SM_ROUND) {
-    float p[8], q[8];
-    const uint32_t mp = ev.load8(rp, idx, c1, p);
-    if (hasq) {
-      const uint32_t mq = ev.load8(rq, idx, c1, q);
+// ---------------------------------------------------------------- record helpers
+// Records cross blocks on different XCDs: word-wise agent-scope atomics, which
+// no XCD's L2 holds stale.
+__device__ inline void store_rec(ChunkRec* dst, const ChunkRec& r) {
+  uint64_t* d = reinterpret_cast<uint64_t*>(dst);
+  const uint64_t* s = reinterpret_cast<const uint64_t*>(&r);
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const bool ip = (mp >> t) & 1u, iq = (mq >> t) & 1u;
-        const uint64_t wr = fixed62(fmaxf(p[t] - q[t], 0.0f));
-        if (!ip) {
-          p2 += fixed62(p[t]);
-          if (!iq) r0 += wr;
-          else { ra += wr; rb += fixed62(p[t]); }
-        } else {
-          if (!iq) rpm += wr;
-          else ++ndbl;
-        }
-      }
-      nq += __popc(mq);
-    } else {
+  for (int i = 0; i < 8; ++i)
+    __hip_atomic_store(d + i, s[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline ChunkRec load_rec(const ChunkRec* src) {
+  ChunkRec r;
+  const uint64_t* s = reinterpret_cast<const uint64_t*>(src);
+  uint64_t* d = reinterpret_cast<uint64_t*>(&r);
 #pragma unroll
-      for (int t = 0; t < 8; ++t)
-        if (!((mp >> t) & 1u)) p2 += fixed62(p[t]);
-    }
-    np += __popc(mp);
-  }
-  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
-  p2 = wave_sum_u64(p2);
-  r0 = wave_sum_u64(r0);
-  ra = wave_sum_u64(ra);
-  rb = wave_sum_u64(rb);
-  rpm = wave_sum_u64(rpm);
-  np = wave_sum_u32(np);
-  nq = wave_sum_u32(nq);
-  ndbl = wave_sum_u32(ndbl);
-  if (lane == 0) {
-    red64[w] = p2; red64[SM_NW + w] = r0; red64[2 * SM_NW + w] = ra;
-    red64[3 * SM_NW + w] = rb; red64[4 * SM_NW + w] = rpm;
-    red32[w] = np; red32[SM_NW + w] = nq; red32[2 * SM_NW + w] = ndbl;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    ChunkRec rec = {};
-    for (int w2 = 0; w2 < SM_NW; ++w2) {
-      rec.p2 += red64[w2]; rec.r0 += red64[SM_NW + w2]; rec.ra += red64[2 * SM_NW + w2];
-      rec.rb += red64[3 * SM_NW + w2]; rec.rp += red64[4 * SM_NW + w2];
-      rec.np += red32[w2]; rec.nq += red32[SM_NW + w2]; rec.ndbl += red32[2 * SM_NW + w2];
-    }
-    a.recs[j * a.nchunk + c] = rec;
-  }
+  for (int i = 0; i < 8; ++i)
+    d[i] = __hip_atomic_load(s + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return r;
 }
 
-// ---------------------------------------------------------------- exact chunk walk
-struct WalkSmem {
-  uint32_t s32[SM_NW];
-  uint64_t s64[SM_NW];
-  int64_t found;
-};
+// Exact residual / p masses of a record once the member ranks at its start
+// are known; false when a group's kept members run out inside it (then only
+// an id-order walk gives the residual mass).
+__device__ inline bool rec_masses(const ChunkRec& rec, uint32_t bp, uint32_t bq, int32_t sp,
+                                  int32_t sq, float vp, float vq, bool hasq, uint64_t* pmass,
+                                  uint64_t* rmass) {
+  const uint32_t kp = (uint32_t)min<int64_t>(max<int64_t>((int64_t)sp - bp, 0), rec.np);
+  const uint32_t kq = (uint32_t)min<int64_t>(max<int64_t>((int64_t)sq - bq, 0), rec.nq);
+  *pmass = rec.p2 + (uint64_t)kp * fixed62(vp);
+  *rmass = 0;
+  if (!hasq) return true;
+  const bool pall = kp == rec.np, pnone = kp == 0, qall = kq == rec.nq, qnone = kq == 0;
+  if (!((pall || pnone) && (qall || qnone))) return false;
+  uint64_t m = rec.r0 + (qall ? rec.ra : rec.rb);
+  if (pall && rec.np) {
+    m += rec.rp;
+    m += (uint64_t)rec.ndbl * fixed62(fmaxf(vp - (qall ? vq : 0.0f), 0.0f));
+  }
+  *rmass = m;
+  return true;
+}
 
-// Walks ids [c0, c1) in id order with the member ranks at c0 equal to (bp, bq)
-// and returns the chunk's mass (residual when use_r, else p). With t given
-// (base <= t), also sets sm.found to the first id whose prefix mass, counted
-// from `base`, exceeds t. Whole block.
+// One wave walks ids [i0, i1) in id order, the member ranks at i0 being
+// (bp, bq), and returns the mass (residual when use_r, else p). With `find`
+// (base <= t), the lane holding the first id whose prefix mass, counted from
+// `base`, exceeds t writes it to *found.
 template <class Ev>
-__device__ uint64_t chunk_walk(const Ev& ev, const typename Ev::Row& rp,
-                               const typename Ev::Row& rq, bool hasq, bool use_r, int64_t c0,
-                               int64_t c1, uint32_t bp, uint32_t bq, uint64_t base, bool find,
-                               uint64_t t, WalkSmem& sm) {
-  const int32_t sp = Ev::rstar(rp), sq = hasq ? Ev::rstar(rq) : 0;
+__device__ uint64_t wave_walk(const Ev& ev, const typename Ev::Row& rp, const typename Ev::Row& rq,
+                              bool use_r, int64_t i0, int64_t i1, uint32_t bp, uint32_t bq,
+                              uint64_t base, bool find, uint64_t t, int64_t* found) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int32_t sp = Ev::rstar(rp), sq = use_r ? Ev::rstar(rq) : 0;
   uint64_t run = base;
-  for (int64_t r0 = c0; r0 < c1; r0 += SM_ROUND) {
-    const int64_t idx = r0 + (int64_t)threadIdx.x * 8;
+  for (int64_t r0 = i0; r0 < i1; r0 += kDrawSub) {
+    const int64_t idx = r0 + (int64_t)lane * 8;
     float p[8], q[8];
     uint32_t mp = 0, mq = 0;
-    if (idx < c1) {
-      mp = ev.load8(rp, idx, c1, p);
-      if (use_r) mq = ev.load8(rq, idx, c1, q);
-    } else {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) { p[u] = 0.0f; q[u] = 0.0f; }
+    for (int u = 0; u < 8; ++u) { p[u] = 0.0f; q[u] = 0.0f; }
+    if (idx < i1) {
+      mp = ev.load8(rp, idx, i1, p);
+      if (use_r) mq = ev.load8(rq, idx, i1, q);
     }
     uint32_t rk_p = bp, rk_q = bq;
-    if (Ev::kGroups) {  // member ranks: block scan of packed (p count, q count)
-      uint32_t tot;
-      const uint32_t ex = block_excl_u32((uint32_t)__popc(mp) | ((uint32_t)__popc(mq) << 16),
-                                         sm.s32, &tot);
-      rk_p += ex & 0xFFFFu;
-      rk_q += ex >> 16;
+    if constexpr (Ev::kGroups) {  // member ranks: wave scan of packed (p count, q count)
+      const uint32_t cnt = (uint32_t)__popc(mp) | ((uint32_t)__popc(mq) << 16);
+      const uint32_t incl = wave_incl_scan_u32(cnt, lane);
+      const uint32_t tot = rdlane(incl, kWave - 1);
+      rk_p += (incl - cnt) & 0xFFFFu;
+      rk_q += (incl - cnt) >> 16;
       bp += tot & 0xFFFFu;
       bq += tot >> 16;
     }
@@ -337,10 +338,11 @@ __device__ uint64_t chunk_walk(const Ev& ev, const typename Ev::Row& rp,
       }
       mine += w[u];
     }
-    uint64_t tot;
-    const uint64_t ex = block_excl_u64(mine, sm.s64, &tot);
+    const uint64_t incl = wave_incl_scan_u64(mine, lane);
+    const uint64_t tot = ((uint64_t)rdlane((uint32_t)(incl >> 32), kWave - 1) << 32) |
+                         rdlane((uint32_t)incl, kWave - 1);
     if (find) {
-      const uint64_t st = run + ex;
+      const uint64_t st = run + incl - mine;
       if (st <= t && st + mine > t) {
         uint64_t acc = st;
         int64_t f = -1;
@@ -349,7 +351,7 @@ __device__ uint64_t chunk_walk(const Ev& ev, const typename Ev::Row& rp,
           acc += w[u];
           if (f < 0 && acc > t) f = idx + u;
         }
-        sm.found = f;
+        *found = f;
       }
     }
     run += tot;
@@ -357,89 +359,352 @@ __device__ uint64_t chunk_walk(const Ev& ev, const typename Ev::Row& rp,
   return run - base;
 }
 
-// ---------------------------------------------------------------- select
-struct SelectArgs {
-  const SampleJob* jobs;
+// ---------------------------------------------------------------- the draw
+struct DrawArgs {
+  AcceptArgs acc;      // acc.stats == null: the draws are given in `jobs`
+  SampleJob* jobs;
   int64_t V;
-  int64_t chunk;
-  int32_t nchunk;
-  const ChunkRec* recs;
-  int64_t* y;
+  int64_t rec_ids;     // ids per record (a multiple of kDrawSub)
+  int32_t nrec;        // records per job
+  int32_t gw;          // consecutive records per wave
+  int32_t nblk;        // blocks per job
+  ChunkRec* recs;      // [jobs, nrec]
+  uint32_t* counters;  // [jobs], zero on entry (cleared by the kernel before)
+  int64_t* y;          // null: records only
 };
 
 template <class Ev>
-__global__ void __launch_bounds__(SM_NT) select_kernel(Ev ev, SelectArgs a) {
-  __shared__ float tbl_p[kTbl];
-  __shared__ float tbl_q[kTbl];
-  __shared__ WalkSmem sm;
-  __shared__ uint64_t s_r[kMaxChunks];
-  __shared__ int32_t s_part[2];
-  __shared__ int64_t s_pick[4];
-  const int64_t j = blockIdx.x;
-  const SampleJob job = a.jobs[j];
+__global__ void __launch_bounds__(SM_NT) draw_kernel(Ev ev, DrawArgs a) {
+  __shared__ float tbl_p[Ev::kLdsTbl];
+  __shared__ float tbl_q[Ev::kLdsTbl];
+  __shared__ float lst_p[SM_NW][kDrawSub];  // per-wave lists of ids with p mass
+  __shared__ float lst_q[SM_NW][kDrawSub];
+  __shared__ unsigned long long acc[SM_NW][6];  // per-wave record sums (16-bit rows)
+  __shared__ SampleJob s_job;
+  __shared__ uint64_t s64[SM_NW];
+  __shared__ int32_t s_last;
+  __shared__ int32_t s_part[2];    // records where p's / q's kept group members run out
+  __shared__ uint32_t s_pbase[4];  // their member ranks (bp, bq) at the record start
+  __shared__ uint64_t s_rm[2];     // and their residual masses
+  __shared__ int64_t s_pick[3];
+  __shared__ int64_t s_found;
+  const int64_t j = (int64_t)blockIdx.x / a.nblk;
+  const int bi = (int)((int64_t)blockIdx.x % a.nblk);
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+
+  // ---- 1. the draw: from the accept chain (wave 0) or given
+  if (threadIdx.x < kWave) {
+    if (a.acc.stats) {
+      SampleJob jb;
+      uint32_t fl;
+      const int64_t n = accept_chain_wave(a.acc, j, &jb, &fl);
+      if (lane == 0) {
+        if (bi == 0) {
+          a.jobs[j] = jb;
+          if (a.acc.n_acc) a.acc.n_acc[j] = n;
+          if (a.acc.flags) a.acc.flags[j] = (uint8_t)fl;
+        }
+        s_job = jb;
+      }
+    } else if (lane == 0) {
+      s_job = a.jobs[j];
+    }
+  }
+  __syncthreads();
+  const SampleJob job = s_job;
   const bool hasq = job.qrow >= 0;
   ev.stage(job.prow, tbl_p);
   if (hasq) ev.stage(job.qrow, tbl_q);
-  if (threadIdx.x < 2) s_part[threadIdx.x] = -1;
-  if (threadIdx.x == 0) s_pick[0] = -1;
   __syncthreads();
   typename Ev::Row rp, rq;
   ev.bind(rp, job.prow, tbl_p);
   if (hasq) ev.bind(rq, job.qrow, tbl_q);
-  const int32_t sp = Ev::rstar(rp), sq = hasq ? Ev::rstar(rq) : 0;
-  float vp = 0.0f, vq = 0.0f;
-  if constexpr (Ev::kGroups) {
-    vp = rp.vg;
-    if (hasq) vq = rq.vg;
-  }
 
-  // ---- chunk c (thread c): member ranks at its start, exact p mass, and the
-  // residual mass when both rows' kept members are all-or-nothing inside it
-  const int c = threadIdx.x;
-  ChunkRec rec = {};
-  if (c < a.nchunk) rec = a.recs[j * a.nchunk + c];
-  uint64_t tot_n;
-  const uint64_t ex_n = block_excl_u64((uint64_t)rec.np | ((uint64_t)rec.nq << 32), sm.s64, &tot_n);
-  const uint32_t bp = (uint32_t)ex_n, bq = (uint32_t)(ex_n >> 32);
-  const uint32_t kp = (uint32_t)min<int64_t>(max<int64_t>((int64_t)sp - bp, 0), rec.np);
-  const uint32_t kq = (uint32_t)min<int64_t>(max<int64_t>((int64_t)sq - bq, 0), rec.nq);
-  const uint64_t pmass = rec.p2 + (uint64_t)kp * fixed62(vp);
-  uint64_t rmass = 0;
-  if (hasq && c < a.nchunk) {
-    const bool pall = kp == rec.np, pnone = kp == 0, qall = kq == rec.nq, qnone = kq == 0;
-    if ((pall || pnone) && (qall || qnone)) {
-      rmass = rec.r0 + (qall ? rec.ra : rec.rb);
-      if (pall && rec.np) {
-        rmass += rec.rp;
-        rmass += (uint64_t)rec.ndbl * fixed62(fmaxf(vp - (qall ? vq : 0.0f), 0.0f));
+  // ---- 2. records: wave w reduces records [r_beg, r_end) in 512-id rounds,
+  // software-pipelined two rounds deep (buffers A / B keep fixed roles, so no
+  // register rotation waits on a load in flight).
+  {
+    const int r_beg = (bi * SM_NW + w) * a.gw;
+    const int r_end = min(a.nrec, r_beg + a.gw);
+    if (r_beg < r_end) {
+      const int64_t x_beg = (int64_t)r_beg * a.rec_ids;
+      const int64_t x_end = min(a.V, (int64_t)r_end * a.rec_ids);
+      const int64_t nround = (x_end - x_beg + kDrawSub - 1) / kDrawSub;
+      const int64_t rpr = a.rec_ids / kDrawSub;  // rounds per record
+      const int64_t lane_off = (int64_t)lane * 8;
+      uint64_t p2 = 0, r0 = 0, ra = 0, rb = 0, rpm = 0;
+      uint32_t np = 0, nq = 0, ndbl = 0;
+      // one round: evaluate, compact the ids that may carry p mass into this
+      // wave's LDS list (sign bits mark group members), reduce one per lane;
+      // a round that ends a record publishes it
+      auto round = [&](const typename Ev::Raw& cp, const typename Ev::Raw& cq, int64_t ro) {
+        const int64_t s0 = x_beg + ro * kDrawSub;
+        const int64_t rec = s0 / a.rec_ids;
+        const int64_t e1 = min(a.V, (rec + 1) * a.rec_ids);
+        const int64_t cur = s0 + lane_off;
+        float p[8], q[8];
+        const uint32_t ep = ev.eval(rp, cur, e1, cp, p);
+        const uint32_t mp = ep & 0xFFu, lp = (ep >> 8) & 0xFFu;
+        uint32_t mq = 0;
+        if (hasq) {
+          mq = ev.eval(rq, cur, e1, cq, q) & 0xFFu;
+        } else {
+#pragma unroll
+          for (int t = 0; t < 8; ++t) q[t] = 0.0f;
+        }
+        np += __popc(mp);
+        nq += __popc(mq);
+        const uint32_t c = __popc(lp);
+        const uint32_t incl = wave_incl_scan_u32(c, lane);
+        const uint32_t n = rdlane(incl, kWave - 1);
+        uint32_t o = incl - c;
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+          if ((lp >> t) & 1u) {
+            lst_p[w][o] = __uint_as_float(__float_as_uint(p[t]) | (((mp >> t) & 1u) << 31));
+            lst_q[w][o] = __uint_as_float(__float_as_uint(q[t]) | (((mq >> t) & 1u) << 31));
+            ++o;
+          }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_wave_barrier();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        for (uint32_t i = lane; i < n; i += kWave) {
+          const uint32_t bp = __float_as_uint(lst_p[w][i]), bq = __float_as_uint(lst_q[w][i]);
+          const bool ip = (bp >> 31) != 0, iq = (bq >> 31) != 0;
+          const float pv = __uint_as_float(bp & 0x7FFFFFFFu);
+          const float qv = __uint_as_float(bq & 0x7FFFFFFFu);
+          const uint64_t wr = fixed62(fmaxf(pv - qv, 0.0f));
+          const uint64_t fp = fixed62(pv);
+          p2 += ip ? 0ull : fp;
+          r0 += (!ip && !iq) ? wr : 0ull;
+          ra += (!ip && iq) ? wr : 0ull;
+          rb += (!ip && iq) ? fp : 0ull;
+          rpm += (ip && !iq) ? wr : 0ull;
+          ndbl += (ip && iq) ? 1u : 0u;
+        }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_wave_barrier();  // list reads done before the next round's writes
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if ((ro + 1) % rpr == 0 || ro + 1 == nround) {
+          ChunkRec rc;
+          rc.p2 = wave_sum_u64(p2);
+          rc.r0 = wave_sum_u64(r0);
+          rc.ra = wave_sum_u64(ra);
+          rc.rb = wave_sum_u64(rb);
+          rc.rp = wave_sum_u64(rpm);
+          rc.np = wave_sum_u32(np);
+          rc.nq = wave_sum_u32(nq);
+          rc.ndbl = wave_sum_u32(ndbl);
+          rc.pad = 0;
+          rc.pad2 = 0;
+          if (lane == 0) store_rec(a.recs + j * a.nrec + rec, rc);
+          p2 = r0 = ra = rb = rpm = 0;
+          np = nq = ndbl = 0;
+        }
+      };
+      // 16-bit rows, lean: keys from packed codes, group-member counts from
+      // ballots (scalar popcounts), the ids that may carry p mass (p's kept
+      // keys, ~2% under a nucleus) compacted by ballot into this wave's LDS list
+      // as packed (p code, q code) and evaluated one per lane, sums
+      // accumulated with LDS atomics (no per-record wave reductions).
+      uint32_t np_s = 0, nq_s = 0;
+      if constexpr (Ev::kGroups) {
+        if (lane < 6) acc[w][lane] = 0ull;
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_wave_barrier();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
       }
-    } else {
-      if (!(pall || pnone)) s_part[0] = c;
-      if (!(qall || qnone)) s_part[1] = c;
+      auto round16 = [&](const typename Ev::Raw& cp, const typename Ev::Raw& cq, int64_t ro) {
+        if constexpr (Ev::kGroups) {
+          const int64_t s0 = x_beg + ro * kDrawSub;
+          const int64_t rec = s0 / a.rec_ids;
+          const int64_t e1 = min(a.V, (rec + 1) * a.rec_ids);
+          const int nvalid = (int)max<int64_t>(0, min<int64_t>(8, e1 - (s0 + lane_off)));
+          const int32_t klo_p = rp.st.klo, glo_p = rp.st.glo, ghi_p = rp.st.ghi;
+          const int32_t klo_q = hasq ? rq.st.klo : 0x7FFFFFFF;
+          const int32_t glo_q = hasq ? rq.st.glo : 1, ghi_q = hasq ? rq.st.ghi : 0;
+          const uint32_t pw[4] = {cp.x, cp.y, cp.z, cp.w};
+          const uint32_t qw[4] = {cq.x, cq.y, cq.z, cq.w};
+          uint32_t kp2[4], kq2[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            kp2[i] = keys2_of_codes2(pw[i]);
+            kq2[i] = keys2_of_codes2(qw[i]);
+          }
+          uint32_t* lst = reinterpret_cast<uint32_t*>(&lst_p[w][0]);
+          uint32_t off = 0;
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            const int sh = 16 * (t & 1);
+            const int32_t kp = (int32_t)((kp2[t >> 1] >> sh) & 0xFFFFu);
+            const int32_t kq = (int32_t)((kq2[t >> 1] >> sh) & 0xFFFFu);
+            const bool valid = t < nvalid;
+            const bool lv = valid && kp >= klo_p;
+            const uint64_t bl = __ballot(lv);
+            np_s += (uint32_t)__popcll(__ballot(valid && kp >= glo_p && kp <= ghi_p));
+            nq_s += (uint32_t)__popcll(__ballot(valid && kq >= glo_q && kq <= ghi_q));
+            if (lv) {
+              const uint32_t pos =
+                  off + __builtin_amdgcn_mbcnt_hi((uint32_t)(bl >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)bl, 0u));
+              lst[pos] = ((pw[t >> 1] >> sh) & 0xFFFFu) | (((qw[t >> 1] >> sh) & 0xFFFFu) << 16);
+            }
+            off += (uint32_t)__popcll(bl);
+          }
+          __atomic_signal_fence(__ATOMIC_SEQ_CST);
+          __builtin_amdgcn_wave_barrier();
+          __atomic_signal_fence(__ATOMIC_SEQ_CST);
+          auto tval = [&](const RowStat& st, const float* tb, int32_t key, uint32_t code) -> float {
+            const int32_t tt = st.kmax - key;
+            if (tt < st.ntbl) return tb[tt];
+            return val16_exp<Ev::kFmt>(code, ev.T, st.m, st.zf, st.totf);
+          };
+          for (uint32_t i = lane; i < off; i += kWave) {
+            const uint32_t e = lst[i];
+            const uint32_t cpd = e & 0xFFFFu, cqd = e >> 16;
+            const int32_t kp = (int32_t)key_of_code16(cpd), kq = (int32_t)key_of_code16(cqd);
+            const bool ip = kp >= glo_p && kp <= ghi_p;
+            const bool iq = kq >= glo_q && kq <= ghi_q;
+            const float pv = ip ? rp.vg : tval(rp.st, tbl_p, kp, cpd);
+            float qv = 0.0f;
+            if (hasq) qv = iq ? rq.vg : (kq >= klo_q ? tval(rq.st, tbl_q, kq, cqd) : 0.0f);
+            const uint64_t wr = fixed62(fmaxf(pv - qv, 0.0f));
+            const uint64_t fp = fixed62(pv);
+            atomicAdd(&acc[w][0], ip ? 0ull : fp);
+            atomicAdd(&acc[w][1], (!ip && !iq) ? wr : 0ull);
+            atomicAdd(&acc[w][2], (!ip && iq) ? wr : 0ull);
+            atomicAdd(&acc[w][3], (!ip && iq) ? fp : 0ull);
+            atomicAdd(&acc[w][4], (ip && !iq) ? wr : 0ull);
+            atomicAdd(&acc[w][5], (ip && iq) ? 1ull : 0ull);
+          }
+          __atomic_signal_fence(__ATOMIC_SEQ_CST);
+          __builtin_amdgcn_wave_barrier();  // list / sums settled before reuse
+          __atomic_signal_fence(__ATOMIC_SEQ_CST);
+          if ((ro + 1) % rpr == 0 || ro + 1 == nround) {
+            if (lane == 0) {
+              ChunkRec rc;
+              rc.p2 = acc[w][0];
+              rc.r0 = acc[w][1];
+              rc.ra = acc[w][2];
+              rc.rb = acc[w][3];
+              rc.rp = acc[w][4];
+              rc.ndbl = (uint32_t)acc[w][5];
+              rc.np = np_s;
+              rc.nq = nq_s;
+              rc.pad = 0;
+              rc.pad2 = 0;
+              store_rec(a.recs + j * a.nrec + rec, rc);
+              for (int i = 0; i < 6; ++i) acc[w][i] = 0ull;
+            }
+            np_s = nq_s = 0;
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_wave_barrier();
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+          }
+        } else {
+          round(cp, cq, ro);
+        }
+      };
+      typename Ev::Raw ap = {}, aq = {}, bp_ = {}, bq_ = {};
+      ap = ev.fetch(rp, x_beg + lane_off, x_end);
+      if (hasq) aq = ev.fetch(rq, x_beg + lane_off, x_end);
+      if (nround > 1) {
+        bp_ = ev.fetch(rp, x_beg + kDrawSub + lane_off, x_end);
+        if (hasq) bq_ = ev.fetch(rq, x_beg + kDrawSub + lane_off, x_end);
+      }
+      for (int64_t ro = 0; ro < nround; ro += 2) {
+        round16(ap, aq, ro);
+        if (ro + 2 < nround) {
+          const int64_t x = x_beg + (ro + 2) * kDrawSub + lane_off;
+          ap = ev.fetch(rp, x, x_end);
+          if (hasq) aq = ev.fetch(rq, x, x_end);
+        }
+        if (ro + 1 < nround) {
+          round16(bp_, bq_, ro + 1);
+          if (ro + 3 < nround) {
+            const int64_t x = x_beg + (ro + 3) * kDrawSub + lane_off;
+            bp_ = ev.fetch(rp, x, x_end);
+            if (hasq) bq_ = ev.fetch(rq, x, x_end);
+          }
+        }
+      }
+    }
+  }
+  if (!a.y) return;
+
+  // ---- 3. the block that completes the job's records draws. Each wave waits
+  // for its record stores (vmcnt(0)) before the block's counter increment, so
+  // the block that sees the last increment sees every record (agent-scope
+  // fences would write back the whole L2 in every block).
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // gfx9 encoding: vmcnt(0), expcnt / lgkmcnt untouched
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(&a.counters[j], 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == (uint32_t)(a.nblk - 1) ? 1 : 0;
+  }
+  if (threadIdx.x < 2) s_part[threadIdx.x] = -1;
+  if (threadIdx.x == 0) { s_pick[0] = -1; s_found = -1; }
+  __syncthreads();
+  if (!s_last) return;
+
+  const int32_t sp = Ev::rstar(rp), sq = hasq ? Ev::rstar(rq) : 0;
+  const float vp = rp.vg, vq = hasq ? rq.vg : 0.0f;
+  // thread t owns records [t*per, (t+1)*per): member ranks at their starts,
+  // exact masses where both groups' kept members are all-or-nothing
+  const int per = (a.nrec + SM_NT - 1) / SM_NT;
+  const int rb0 = min(a.nrec, (int)threadIdx.x * per), rb1 = min(a.nrec, rb0 + per);
+  const ChunkRec* jrecs = a.recs + j * a.nrec;
+  uint64_t cnt = 0;
+  for (int r = rb0; r < rb1; ++r) {
+    const ChunkRec rec = load_rec(jrecs + r);
+    cnt += (uint64_t)rec.np | ((uint64_t)rec.nq << 32);
+  }
+  uint64_t tot_n;
+  const uint64_t ex_n = block_excl_u64(cnt, s64, &tot_n);
+  uint64_t sum_r = 0, sum_p = 0;
+  {
+    uint32_t bp = (uint32_t)ex_n, bq = (uint32_t)(ex_n >> 32);
+    for (int r = rb0; r < rb1; ++r) {
+      const ChunkRec rec = load_rec(jrecs + r);
+      uint64_t pm, rm;
+      if (!rec_masses(rec, bp, bq, sp, sq, vp, vq, hasq, &pm, &rm)) {
+        // at most one record where p's kept members run out, one for q's
+        const int64_t kp = min<int64_t>(max<int64_t>((int64_t)sp - bp, 0), rec.np);
+        const int slot = (kp != 0 && kp != (int64_t)rec.np) ? 0 : 1;
+        s_part[slot] = r;
+        s_pbase[2 * slot] = bp;
+        s_pbase[2 * slot + 1] = bq;
+      }
+      sum_r += rm;
+      sum_p += pm;
+      bp += rec.np;
+      bq += rec.nq;
     }
   }
   __syncthreads();
-  // ---- rescan the (at most two) chunks where a group's kept members run out
-  if (hasq) {
-    const int pa = s_part[0], pb = s_part[1];
-    for (int i = 0; i < 2; ++i) {
-      const int cc = i == 0 ? pa : pb;
-      if (cc < 0 || (i == 1 && cc == pa)) continue;
-      if (c == cc) s_pick[1] = ((int64_t)bq << 32) | bp;
-      __syncthreads();
-      const int64_t packed = s_pick[1];
-      const int64_t c0 = (int64_t)cc * a.chunk;
-      const uint64_t m = chunk_walk(ev, rp, rq, true, true, c0, min(a.V, c0 + a.chunk),
-                                    (uint32_t)(packed & 0xFFFFFFFF), (uint32_t)(packed >> 32),
-                                    0, false, 0, sm);
-      if (c == cc) rmass = m;
-      __syncthreads();
+  // the (at most two) records where a group's kept members run out: one wave each
+  const int pa = s_part[0], pb = s_part[1];
+  if (w < 2) {
+    const int rr = w == 0 ? pa : pb;
+    if (rr >= 0 && !(w == 1 && rr == pa)) {
+      const int64_t i0 = (int64_t)rr * a.rec_ids, i1 = min(a.V, i0 + a.rec_ids);
+      const uint64_t m = wave_walk(ev, rp, rq, true, i0, i1, s_pbase[2 * w], s_pbase[2 * w + 1], 0,
+                                   false, 0, &s_found);
+      if (lane == 0) s_rm[w] = m;
     }
   }
-  // ---- totals, degenerate-residual rule, the chunk holding the target
+  __syncthreads();
+  for (int i = 0; i < 2; ++i) {
+    const int rr = i == 0 ? pa : pb;
+    if (rr >= rb0 && rr < rb1 && !(i == 1 && rr == pa)) sum_r += s_rm[i];
+  }
+  // totals, degenerate-residual rule (sampling.py:85-88), the record holding the target
   uint64_t tot_r, tot_p;
-  const uint64_t ex_r = block_excl_u64(rmass, sm.s64, &tot_r);
-  const uint64_t ex_p = block_excl_u64(pmass, sm.s64, &tot_p);
+  const uint64_t ex_r = block_excl_u64(sum_r, s64, &tot_r);
+  const uint64_t ex_p = block_excl_u64(sum_p, s64, &tot_p);
   const bool use_r = hasq && rn32_u64(tot_r) > 1e-9f;
   const uint64_t tot = use_r ? tot_r : tot_p;
   if (tot == 0) {
@@ -447,27 +712,43 @@ __global__ void __launch_bounds__(SM_NT) select_kernel(Ev ev, SelectArgs a) {
     return;
   }
   const uint64_t t = uniform_threshold(job.u, tot);
-  const uint64_t ex = use_r ? ex_r : ex_p, mine = use_r ? rmass : pmass;
-  if (c < a.nchunk && ex <= t && ex + mine > t) {
-    s_pick[0] = c;
-    s_pick[1] = ((int64_t)bq << 32) | bp;
-    s_pick[2] = (int64_t)ex;
+  {
+    uint64_t run = use_r ? ex_r : ex_p;
+    const uint64_t mine = use_r ? sum_r : sum_p;
+    if (rb0 < rb1 && run <= t && run + mine > t) {  // exactly one thread
+      uint32_t bp = (uint32_t)ex_n, bq = (uint32_t)(ex_n >> 32);
+      for (int r = rb0; r < rb1; ++r) {
+        const ChunkRec rec = load_rec(jrecs + r);
+        uint64_t pm, rm;
+        if (!rec_masses(rec, bp, bq, sp, sq, vp, vq, hasq, &pm, &rm))
+          rm = r == pa ? s_rm[0] : s_rm[1];
+        const uint64_t m = use_r ? rm : pm;
+        if (run + m > t) {
+          s_pick[0] = r;
+          s_pick[1] = ((int64_t)bq << 32) | bp;
+          s_pick[2] = (int64_t)run;
+          break;
+        }
+        run += m;
+        bp += rec.np;
+        bq += rec.nq;
+      }
+    }
   }
   __syncthreads();
-  const int64_t cstar = s_pick[0];
-  if (cstar < 0) {  // unreachable: masses sum to tot > t
+  const int64_t rec_star = s_pick[0];
+  if (rec_star < 0) {  // unreachable: record masses sum to tot > t
     if (threadIdx.x == 0) a.y[j] = -1;
     return;
   }
-  const int64_t packed = s_pick[1];
-  const uint64_t base = (uint64_t)s_pick[2];
-  if (threadIdx.x == 0) sm.found = -1;
+  if (w == 0) {
+    const int64_t packed = s_pick[1];
+    const int64_t i0 = rec_star * a.rec_ids, i1 = min(a.V, i0 + a.rec_ids);
+    wave_walk(ev, rp, rq, use_r, i0, i1, (uint32_t)(packed & 0xFFFFFFFF),
+              (uint32_t)(packed >> 32), (uint64_t)s_pick[2], true, t, &s_found);
+  }
   __syncthreads();
-  const int64_t c0 = cstar * a.chunk;
-  chunk_walk(ev, rp, rq, hasq, use_r, c0, min(a.V, c0 + a.chunk), (uint32_t)(packed & 0xFFFFFFFF),
-             (uint32_t)(packed >> 32), base, true, t, sm);
-  __syncthreads();
-  if (threadIdx.x == 0) a.y[j] = sm.found;
+  if (threadIdx.x == 0) a.y[j] = s_found;
 }
 
 // ---------------------------------------------------------------- to_probs output
@@ -519,6 +800,12 @@ __global__ void __launch_bounds__(SM_NT) materialize16_kernel(Eval16<FMT> ev, Ma
   __syncthreads();
   typename Eval16<FMT>::Row r;
   ev.bind(r, row, tbl);
+  if (r.st.flags & kRowUnsupported) {  // outside the row kernel's windows: mark, don't guess
+    float* o = a.out + row * a.ld_out;
+    for (int64_t i = cidx * a.chunk + threadIdx.x; i < min(a.V, (cidx + 1) * a.chunk); i += SM_NT)
+      o[i] = __builtin_nanf("");
+    return;
+  }
   const bool part = partial_group(r.st);
   uint32_t rank = 0;
   if (part) {  // members in earlier chunks
@@ -557,33 +844,30 @@ __global__ void __launch_bounds__(SM_NT) materialize16_kernel(Eval16<FMT> ev, Ma
 // ---------------------------------------------------------------- residual_probs output
 
 __global__ void __launch_bounds__(SM_NT) residual_norm_kernel(ResidualNormArgs a) {
-  __shared__ float s_tot;
-  __shared__ int s_use_r;
-  const int64_t row = (int64_t)blockIdx.x / a.nchunk;
-  const int64_t cidx = (int64_t)blockIdx.x % a.nchunk;
-  if (threadIdx.x == 0) {
-    // dense fp32 rows have no tie groups: residual mass is r0, p mass p2
-    uint64_t totR = 0, totP = 0;
-    for (int c = 0; c < a.nchunk; ++c) {
-      totR += a.recs[row * a.nchunk + c].r0;
-      totP += a.recs[row * a.nchunk + c].p2;
-    }
-    const float fr = rn32_u64(totR);
-    const bool use_r = fr > 1e-9f;
-    s_use_r = use_r;
-    s_tot = fmaxf(use_r ? fr : rn32_u64(totP), 1e-12f);
+  __shared__ uint64_t s64[SM_NW];
+  const int64_t row = (int64_t)blockIdx.x / a.nrec;
+  const int64_t cidx = (int64_t)blockIdx.x % a.nrec;
+  // dense fp32 rows have no tie groups: residual mass is r0, p mass p2
+  uint64_t r = 0, p = 0;
+  for (int c = threadIdx.x; c < a.nrec; c += SM_NT) {
+    const ChunkRec rec = load_rec(a.recs + row * a.nrec + c);
+    r += rec.r0;
+    p += rec.p2;
   }
-  __syncthreads();
-  const float tot = s_tot;
-  const bool use_r = s_use_r != 0;
-  const int64_t c0 = cidx * a.chunk;
-  const int64_t c1 = min(a.V, c0 + a.chunk);
-  const float* p = a.p + row * a.ld;
-  const float* q = a.q + row * a.ld;
+  uint64_t totR, totP;
+  block_excl_u64(r, s64, &totR);
+  block_excl_u64(p, s64, &totP);
+  const float fr = rn32_u64(totR);
+  const bool use_r = fr > 1e-9f;
+  const float tot = fmaxf(use_r ? fr : rn32_u64(totP), 1e-12f);
+  const int64_t c0 = cidx * a.rec_ids;
+  const int64_t c1 = min(a.V, c0 + a.rec_ids);
+  const float* pp = a.p + row * a.ld;
+  const float* qq = a.q + row * a.ld;
   float* o = a.out + row * a.ld_out;
   for (int64_t idx = c0 + threadIdx.x; idx < c1; idx += SM_NT) {
-    const float r = use_r ? fmaxf(p[idx] - q[idx], 0.0f) : p[idx];
-    o[idx] = r / tot;
+    const float v = use_r ? fmaxf(pp[idx] - qq[idx], 0.0f) : pp[idx];
+    o[idx] = v / tot;
   }
 }
 
@@ -598,58 +882,54 @@ __global__ void gather_kernel(const float* probs, int64_t rows, int64_t V, int64
 
 // ---------------------------------------------------------------- launch helpers
 template <class Ev>
-static hipError_t launch_chunks(const Ev& ev, const AcceptArgs* acc, SampleJob* jobs,
-                                int64_t njobs, int64_t V, int64_t chunk, int nchunk,
-                                ChunkRec* recs, hipStream_t s) {
-  ChunkArgs ca = {};
-  if (acc) ca.acc = *acc;
-  ca.jobs = jobs;
-  ca.V = V;
-  ca.chunk = chunk;
-  ca.nchunk = nchunk;
-  ca.recs = recs;
-  hipLaunchKernelGGL((chunk_kernel<Ev>), dim3((unsigned)(nchunk * njobs)), dim3(SM_NT), 0, s, ev,
-                     ca);
-  return hipGetLastError();
-}
-
-template <class Ev>
 static hipError_t launch_draw(const Ev& ev, const AcceptArgs* acc, SampleJob* jobs,
-                              int64_t njobs, int64_t V, int64_t chunk, int nchunk,
-                              ChunkRec* recs, int64_t* y, hipStream_t s) {
-  if (nchunk > kMaxChunks || nchunk > SM_NT) return hipErrorInvalidValue;
-  hipError_t e = launch_chunks(ev, acc, jobs, njobs, V, chunk, nchunk, recs, s);
-  if (e != hipSuccess) return e;
-  SelectArgs sa{jobs, V, chunk, nchunk, recs, y};
-  hipLaunchKernelGGL((select_kernel<Ev>), dim3((unsigned)njobs), dim3(SM_NT), 0, s, ev, sa);
+                              int64_t njobs, int64_t V, ChunkRec* recs, uint32_t* counters,
+                              int64_t* y, hipStream_t s) {
+  DrawArgs da = {};
+  if (acc) da.acc = *acc;
+  da.jobs = jobs;
+  da.V = V;
+  int nrec;
+  draw_layout(V, &da.rec_ids, &nrec);
+  da.nrec = nrec;
+  // records per wave: enough waves to cover the CUs a few times over
+  const int64_t waves_wanted = 4096;
+  int64_t gw = (njobs * nrec + waves_wanted - 1) / waves_wanted;
+  gw = gw < 1 ? 1 : (gw > 16 ? 16 : gw);
+  da.gw = (int32_t)gw;
+  da.nblk = (int32_t)((nrec + SM_NW * gw - 1) / (SM_NW * gw));
+  da.recs = recs;
+  da.counters = counters;
+  da.y = y;
+  hipLaunchKernelGGL((draw_kernel<Ev>), dim3((unsigned)(da.nblk * njobs)), dim3(SM_NT), 0, s, ev,
+                     da);
   return hipGetLastError();
 }
 
 hipError_t launch_draw16(int fmt, const RowSource16& src, const RowStat* stats,
                          const float* tables, float T, const AcceptArgs* acc, SampleJob* jobs,
-                         int64_t njobs, int64_t V, int64_t chunk, int nchunk, ChunkRec* recs,
-                         int64_t* y, hipStream_t s) {
+                         int64_t njobs, int64_t V, ChunkRec* recs, uint32_t* counters, int64_t* y,
+                         hipStream_t s) {
   if (!src.vec) return hipErrorInvalidValue;
   if (fmt == SDX_BF16) {
     Eval16<SDX_BF16> ev{src.base, src.ld, src.base2, src.ld2, src.split, stats, tables, T};
-    return launch_draw(ev, acc, jobs, njobs, V, chunk, nchunk, recs, y, s);
+    return launch_draw(ev, acc, jobs, njobs, V, recs, counters, y, s);
   }
   Eval16<SDX_F16> ev{src.base, src.ld, src.base2, src.ld2, src.split, stats, tables, T};
-  return launch_draw(ev, acc, jobs, njobs, V, chunk, nchunk, recs, y, s);
+  return launch_draw(ev, acc, jobs, njobs, V, recs, counters, y, s);
 }
 
 hipError_t launch_draw_probs(const RowSourceF32& src, const AcceptArgs* acc, SampleJob* jobs,
-                             int64_t njobs, int64_t V, int64_t chunk, int nchunk, ChunkRec* recs,
+                             int64_t njobs, int64_t V, ChunkRec* recs, uint32_t* counters,
                              int64_t* y, hipStream_t s) {
   EvalProb ev{src.base, src.ld, src.base2, src.ld2, src.split, src.vec};
-  return launch_draw(ev, acc, jobs, njobs, V, chunk, nchunk, recs, y, s);
+  return launch_draw(ev, acc, jobs, njobs, V, recs, counters, y, s);
 }
 
 hipError_t launch_chunk_mass_probs(const RowSourceF32& src, SampleJob* jobs, int64_t njobs,
-                                   int64_t V, int64_t chunk, int nchunk, ChunkRec* recs,
-                                   hipStream_t s) {
+                                   int64_t V, ChunkRec* recs, hipStream_t s) {
   EvalProb ev{src.base, src.ld, src.base2, src.ld2, src.split, src.vec};
-  return launch_chunks(ev, nullptr, jobs, njobs, V, chunk, nchunk, recs, s);
+  return launch_draw(ev, nullptr, jobs, njobs, V, recs, nullptr, nullptr, s);
 }
 
 hipError_t launch_materialize16(int fmt, const RowSource16& src, const RowStat* stats,
@@ -672,8 +952,7 @@ hipError_t launch_materialize16(int fmt, const RowSource16& src, const RowStat* 
 }
 
 hipError_t launch_residual_norm(const ResidualNormArgs& a, int64_t rows, hipStream_t s) {
-  hipLaunchKernelGGL(residual_norm_kernel, dim3((unsigned)(a.nchunk * rows)), dim3(SM_NT), 0,
-                     s, a);
+  hipLaunchKernelGGL(residual_norm_kernel, dim3((unsigned)(a.nrec * rows)), dim3(SM_NT), 0, s, a);
   return hipGetLastError();
 }
 

@@ -143,7 +143,9 @@ def rejection_sample(target_logits, draft_logits, draft_ids, u_accept, u_final, 
     (the residual/bonus draw), active [B] bool (the engine's ~done; None = all).
     Returns (n_acc [B] int64, y [B] int64, flags [B] uint8): row b emits
     draft_ids[b, :n_acc[b]] then y[b] and drops k - n_acc[b] cached positions.
-    flags bit 0 marks rows whose accept decision was within 1e-5 of flipping.
+    flags bit 0 marks rows whose accept decision was within 1e-5 of flipping;
+    bit 1 rows with +inf/NaN logits and bit 2 rows outside the kernels'
+    histogram windows (both: results of that row unspecified).
     With temperature <= 0 the draft logits are not read (may be None).
     """
     T, tp, tk = _switch_args(temperature, top_p, top_k)

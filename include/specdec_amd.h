@@ -45,7 +45,11 @@ enum sdx_status {
 /* Per-row flag bits written by the verify entry points. */
 enum sdx_flag {
   SDX_FLAG_ACCEPT_NEAR_TIE = 1, /* an evaluated accept test had |u - min(p/q,1)| < 1e-5 */
-  SDX_FLAG_NONFINITE = 2        /* a logit row held +inf or NaN: results unspecified */
+  SDX_FLAG_NONFINITE = 2,       /* a logit row held +inf or NaN: results unspecified */
+  SDX_FLAG_UNSUPPORTED = 4      /* a row's probability mass spans more distinct logit values
+                                   than the row kernels' histogram windows cover (only with
+                                   |logit| >= 2^18 at temperatures above ~2500, or fp16 rows
+                                   spanning over 36 binades of mass): results unspecified */
 };
 
 const char* sdx_last_error(void);
