@@ -70,7 +70,7 @@ constexpr int64_t kMaxVocab16 = 16 * 20 * 512;  // register capacity of the row 
 // Workspace of the transform + draw pipeline over `rows` rows and `njobs` draws.
 size_t transform_ws(Carve& c, int64_t rows, int64_t V, int dtype, int64_t njobs,
                     sdx::RowStat** stats, float** tables, float** dense, sdx::SampleJob** jobs,
-                    sdx::ChunkRec** recs, uint32_t** counters) {
+                    sdx::ChunkRec** recs, uint32_t** counters, uint64_t** rank_acc = nullptr) {
   int64_t rec_ids;
   int nrec;
   sdx::draw_layout(V, &rec_ids, &nrec);
@@ -80,6 +80,7 @@ size_t transform_ws(Carve& c, int64_t rows, int64_t V, int dtype, int64_t njobs,
   *jobs = njobs ? c.take<sdx::SampleJob>(njobs) : nullptr;
   *recs = njobs ? c.take<sdx::ChunkRec>((size_t)njobs * nrec) : nullptr;
   *counters = njobs ? c.take<uint32_t>((size_t)njobs) : nullptr;
+  if (rank_acc) *rank_acc = njobs ? c.take<uint64_t>((size_t)rows) : nullptr;
   return c.used;
 }
 
@@ -272,8 +273,9 @@ int sdx_gather_prob(const float* probs, int64_t rows, int64_t vocab, int64_t ld,
 size_t sdx_verify_workspace(int64_t batch, int32_t k, int64_t vocab, int dtype) {
   Carve c{nullptr};
   sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; sdx::ChunkRec* rc; uint32_t* ct;
+  uint64_t* ra;
   const int64_t rows = batch * (2 * (int64_t)k + 1);
-  transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jb, &rc, &ct);
+  transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jb, &rc, &ct, &ra);
   c.take<int64_t>(batch * ((int64_t)k + 1));  // greedy argmax
   return c.used;
 }
@@ -327,9 +329,10 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
   Carve c{(uint8_t*)workspace};
   sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jobs; sdx::ChunkRec* recs;
   uint32_t* counters;
+  uint64_t* rank_acc;
   const int64_t ntgt = batch * ((int64_t)k + 1), ndrf = batch * (int64_t)k;
   const int64_t rows = ntgt + ndrf;
-  transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jobs, &recs, &counters);
+  transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jobs, &recs, &counters, &rank_acc);
   int64_t* am = c.take<int64_t>(ntgt);
   if (sw.greedy) {
     // one-hot p: only the target argmax matters (see sdx_verify_greedy)
@@ -364,7 +367,10 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
     a.use_p = sw.use_p; a.use_k = sw.use_k; a.greedy = 0;
     a.stats = st; a.tables = tb;
     a.zero = counters; a.nzero = batch;
+    a.rank_acc = dtype == SDX_BF16 ? rank_acc : nullptr;
     if (int e = row_stats16(dtype, a, rows, s)) return e;
+    if (dtype == SDX_BF16)
+      if (int e = hip_status(sdx::launch_rank_bf16(a, rows, s), "rank_bf16")) return e;
   }
   if (stats_only) return SDX_OK;
   sdx::AcceptArgs aa{st, batch, k, u_accept, u_final, active, jobs, n_acc, flags};

@@ -21,6 +21,7 @@ struct RowStatArgs {
   float* tables;  // [rows, kTbl]
   uint32_t* zero;  // words [0, nzero) cleared (block `row` clears word `row`), or null
   int64_t nzero;
+  uint64_t* rank_acc;  // [rows] rank accumulators, cleared by the row kernel, or null
 };
 
 struct F32Args {
@@ -104,6 +105,8 @@ int rowstat16_nslot(int64_t V);
 hipError_t launch_rowstat16(int fmt, const RowStatArgs& a, int64_t rows, hipStream_t s);
 // sdx_rowstream.hip
 hipError_t launch_rowstream_bf16(const RowStatArgs& a, int64_t rows, hipStream_t s);
+// sdx_rank.hip: pgather of drafted tokens inside a partial tie group (after rowstream)
+hipError_t launch_rank_bf16(const RowStatArgs& a, int64_t rows, hipStream_t s);
 // sdx_f32.hip
 constexpr int64_t kF32MaxVocab = 8192;
 hipError_t launch_to_probs_f32(const F32Args& a, int64_t rows, hipStream_t s);

@@ -252,6 +252,7 @@ rowstream_bf16_kernel(RowStatArgs a) {
   RowStat* st_out = a.stats + row;
   float* tbl_out = a.tables + row * kTbl;
   if (tid == 0 && row < a.nzero) a.zero[row] = 0u;
+  if (tid == 0 && a.rank_acc) a.rank_acc[row] = 0ull;
 
   for (int b = tid; b < SK_NB; b += SK_NT) hist[b] = 0u;
   __syncthreads();
@@ -593,22 +594,16 @@ rowstream_bf16_kernel(RowStatArgs a) {
     tbl_out[t] = v;
   }
 
-  // ---- 7. probability of the drafted token (rank it if it sits in the tie group)
+  // ---- 7. probability of the drafted token. Inside a partial tie group it
+  // depends on the token's member rank (members with lower ids): the rank
+  // kernel counts it, spread over many blocks, and sets pgather.
   float pg = 0.0f;
   if (gid >= 0 && gid < V) {
     const int32_t kk = (int32_t)key_of_code16(ptr[gid]);
     bool kept = kk >= klo;
     if (kept && kk >= glo && kk <= ghi) {
-      if (rstar <= 0) {
-        kept = false;
-      } else if (rstar < gcount) {  // members before gid, in id order
-        uint32_t cnt = 0;
-        for (int64_t i = tid; i < gid; i += SK_NT) {
-          const int32_t k2 = (int32_t)key_of_code16(ptr[i]);
-          cnt += (k2 >= glo && k2 <= ghi) ? 1u : 0u;
-        }
-        kept = blk_sum_u32(cnt, sm) < (uint32_t)rstar;
-      }
+      if (rstar <= 0) kept = false;
+      else if (rstar < gcount) { kept = false; rflags |= kRowRank; }
     }
     if (kept) pg = exp_det(sk_d((uint32_t)kk, T, m)) / zf / totf;
   }
