@@ -386,6 +386,7 @@ __global__ void __launch_bounds__(SM_NT) draw_kernel(Ev ev, DrawArgs a) {
   __shared__ int32_t s_part[2];    // records where p's / q's kept group members run out
   __shared__ uint32_t s_pbase[4];  // their member ranks (bp, bq) at the record start
   __shared__ uint64_t s_rm[2];     // and their residual masses
+  __shared__ uint64_t s_rm2[SM_NW];
   __shared__ int64_t s_pick[3];
   __shared__ int64_t s_found;
   const int64_t j = (int64_t)blockIdx.x / a.nblk;
@@ -652,14 +653,25 @@ __global__ void __launch_bounds__(SM_NT) draw_kernel(Ev ev, DrawArgs a) {
 
   const int32_t sp = Ev::rstar(rp), sq = hasq ? Ev::rstar(rq) : 0;
   const float vp = rp.vg, vq = hasq ? rq.vg : 0.0f;
-  // thread t owns records [t*per, (t+1)*per): member ranks at their starts,
-  // exact masses where both groups' kept members are all-or-nothing
+  // thread t owns records [rb0, rb1): member ranks at their starts, exact
+  // masses where both groups' kept members are all-or-nothing. Up to two
+  // records per thread (vocabularies up to 262,144) stay in registers.
   const int per = (a.nrec + SM_NT - 1) / SM_NT;
   const int rb0 = min(a.nrec, (int)threadIdx.x * per), rb1 = min(a.nrec, rb0 + per);
   const ChunkRec* jrecs = a.recs + j * a.nrec;
+  ChunkRec cache[2];
+  if (per <= 2) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      if (rb0 + i < rb1) cache[i] = load_rec(jrecs + rb0 + i);
+  }
+  auto rec_at = [&](int r) -> ChunkRec {
+    if (per <= 2) return r == rb0 ? cache[0] : cache[1];
+    return load_rec(jrecs + r);
+  };
   uint64_t cnt = 0;
   for (int r = rb0; r < rb1; ++r) {
-    const ChunkRec rec = load_rec(jrecs + r);
+    const ChunkRec rec = rec_at(r);
     cnt += (uint64_t)rec.np | ((uint64_t)rec.nq << 32);
   }
   uint64_t tot_n;
@@ -668,7 +680,7 @@ __global__ void __launch_bounds__(SM_NT) draw_kernel(Ev ev, DrawArgs a) {
   {
     uint32_t bp = (uint32_t)ex_n, bq = (uint32_t)(ex_n >> 32);
     for (int r = rb0; r < rb1; ++r) {
-      const ChunkRec rec = load_rec(jrecs + r);
+      const ChunkRec rec = rec_at(r);
       uint64_t pm, rm;
       if (!rec_masses(rec, bp, bq, sp, sq, vp, vq, hasq, &pm, &rm)) {
         // at most one record where p's kept members run out, one for q's
@@ -687,7 +699,7 @@ __global__ void __launch_bounds__(SM_NT) draw_kernel(Ev ev, DrawArgs a) {
   __syncthreads();
   // the (at most two) records where a group's kept members run out: one wave each
   const int pa = s_part[0], pb = s_part[1];
-  if (w < 2) {
+  if ((pa >= 0 || pb >= 0) && w < 2) {
     const int rr = w == 0 ? pa : pb;
     if (rr >= 0 && !(w == 1 && rr == pa)) {
       const int64_t i0 = (int64_t)rr * a.rec_ids, i1 = min(a.V, i0 + a.rec_ids);
@@ -696,15 +708,32 @@ __global__ void __launch_bounds__(SM_NT) draw_kernel(Ev ev, DrawArgs a) {
       if (lane == 0) s_rm[w] = m;
     }
   }
-  __syncthreads();
+  if (pa >= 0 || pb >= 0) __syncthreads();
   for (int i = 0; i < 2; ++i) {
     const int rr = i == 0 ? pa : pb;
     if (rr >= rb0 && rr < rb1 && !(i == 1 && rr == pa)) sum_r += s_rm[i];
   }
-  // totals, degenerate-residual rule (sampling.py:85-88), the record holding the target
-  uint64_t tot_r, tot_p;
-  const uint64_t ex_r = block_excl_u64(sum_r, s64, &tot_r);
-  const uint64_t ex_p = block_excl_u64(sum_p, s64, &tot_p);
+  // totals (one paired scan), degenerate-residual rule (sampling.py:85-88),
+  // the record holding the target
+  uint64_t ex_r, ex_p, tot_r, tot_p;
+  {
+    const uint64_t ir = wave_incl_scan_u64(sum_r, lane), ip = wave_incl_scan_u64(sum_p, lane);
+    if (lane == kWave - 1) { s64[w] = ir; s_rm2[w] = ip; }
+    __syncthreads();
+    uint64_t orr = 0, opp = 0;
+    tot_r = 0;
+    tot_p = 0;
+#pragma unroll
+    for (int i = 0; i < SM_NW; ++i) {
+      const uint64_t xr = s64[i], xp = s_rm2[i];
+      orr += i < w ? xr : 0ull;
+      opp += i < w ? xp : 0ull;
+      tot_r += xr;
+      tot_p += xp;
+    }
+    ex_r = orr + ir - sum_r;
+    ex_p = opp + ip - sum_p;
+  }
   const bool use_r = hasq && rn32_u64(tot_r) > 1e-9f;
   const uint64_t tot = use_r ? tot_r : tot_p;
   if (tot == 0) {
@@ -718,7 +747,7 @@ __global__ void __launch_bounds__(SM_NT) draw_kernel(Ev ev, DrawArgs a) {
     if (rb0 < rb1 && run <= t && run + mine > t) {  // exactly one thread
       uint32_t bp = (uint32_t)ex_n, bq = (uint32_t)(ex_n >> 32);
       for (int r = rb0; r < rb1; ++r) {
-        const ChunkRec rec = load_rec(jrecs + r);
+        const ChunkRec rec = rec_at(r);
         uint64_t pm, rm;
         if (!rec_masses(rec, bp, bq, sp, sq, vp, vq, hasq, &pm, &rm))
           rm = r == pa ? s_rm[0] : s_rm[1];
