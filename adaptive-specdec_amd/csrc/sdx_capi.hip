@@ -316,8 +316,8 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
                        float temperature, float top_p, int32_t top_k, int64_t* n_acc, int64_t* y,
                        uint8_t* flags, void* workspace, size_t workspace_bytes,
                        sdx_stream_t stream, bool stats_only) {
-  if (!target_logits || !draft_ids || !u_accept || !u_final || batch < 0 || k < 1 ||
-      !dtype_ok(dtype))
+  if (!target_logits || (!draft_ids && !stats_only) || !u_accept || !u_final || batch < 0 ||
+      k < 1 || !dtype_ok(dtype))
     return fail(SDX_EINVAL, "sdx_verify: bad arguments");
   if (int e = check_vocab(dtype, vocab)) return e;
   if (batch == 0) return SDX_OK;

@@ -257,11 +257,13 @@ class Verifier:
         _lib.check(rc, "Verifier")
         return self.n_acc, self.y, self.flags
 
-    def stats(self, target, draft, draft_ids):
-        """Phase 1 only (fused to_probs statistics of all rows), for timing."""
+    def stats(self, target, draft, draft_ids=None):
+        """Phase 1 only (fused to_probs statistics of all rows), for timing.
+        Without draft_ids: the row statistics alone (no gathered probabilities)."""
         if self.greedy:
             raise ValueError("greedy verify has no statistics phase")
+        ids = _lib.ptr(draft_ids) if draft_ids is not None else None
         rc = self.L.sdx_verify_stats(_lib.ptr(target), _lib.ptr(draft), self.dt, self.B, self.k,
-                                     self.V, _lib.ptr(draft_ids), self.T, self.tp, self.tk,
+                                     self.V, ids, self.T, self.tp, self.tk,
                                      _lib.ptr(self.ws), self.ws.numel(), _lib.stream_of(target))
         _lib.check(rc, "Verifier.stats")

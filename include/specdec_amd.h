@@ -104,7 +104,8 @@ int sdx_verify(const void* target_logits, const void* draft_logits, int dtype,
 /* Phase 1 of sdx_verify alone: the fused to_probs statistics of every target and draft
  * row (normaliser, top-k/top-p boundary, drafted-token probabilities) into the workspace,
  * without the accept test or the final draw. Lets a caller time or overlap the
- * vocabulary pass; temperature must be > 0. Same workspace as sdx_verify. */
+ * vocabulary pass; temperature must be > 0. Same workspace as sdx_verify.
+ * draft_ids may be NULL: then only the row statistics (no gathered probabilities). */
 int sdx_verify_stats(const void* target_logits, const void* draft_logits, int dtype,
                      int64_t batch, int32_t k, int64_t vocab, const int64_t* draft_ids,
                      float temperature, float top_p, int32_t top_k, void* workspace,
