@@ -6,30 +6,40 @@
 // reduced to counts per value in an LDS histogram. The histogram uses a fixed
 // value window, not one anchored at the row maximum, so the LDS atomics start
 // as soon as the first 16-byte loads land and overlap the rest of the row:
-//   bin 0               x <= -2^18, -inf, -NaN       (exp_det == 0, checked)
-//   bins 1..6400        -2^18 < x <= -2^-32          (one bin per bf16 value)
-//   bin 6401            |x| < 2^-32, +-0, denormals  (all share exp(-m), checked)
-//   bins 6402..12801    2^-32 <= x < 2^18            (one bin per bf16 value)
-//   bin 12802           x >= 2^18, +inf, +NaN        (row leaves the fixed window)
-// The bins are in value order. 52 KiB of LDS per 512-thread workgroup fits
-// three workgroups per CU, so the 576 rows of a B=64, k=4 verify all stream at
-// once and share HBM evenly; the row maximum is tracked in registers.
+//   bin 0               x <= -2^16, -inf, -NaN       (exp_det == 0, checked)
+//   bins 1..5120        -2^16 < x <= -2^-24          (one bin per bf16 value)
+//   bin 5121            |x| < 2^-24, +-0, denormals  (all share exp(-m), checked)
+//   bins 5122..10241    2^-24 <= x < 2^16            (one bin per bf16 value)
+//   bin 10242           x >= 2^16, +inf, +NaN        (row leaves the fixed window)
+// The bins are in value order, and a bin follows from the raw code with
+// packed 16-bit arithmetic on two codes at once (magnitude clamped into the
+// window, mirrored for negative codes), about ten vector instructions per two
+// logits; the running maximum is tracked on the bins. 40 KiB of LDS per
+// 512-thread workgroup fits three workgroups per CU, so the 576 rows of a
+// B=64, k=4 verify all stream at once and share HBM evenly.
 //
 // After the histogram, the whole block works on it: the exact fixed-point
 // normaliser over occupied bins (the top bins' exp values kept in LDS); the
 // top-k / top-p walk down from the maximum in rounds of one bin per thread,
 // with a block scan of exact cumulative mass and the reference's fp32 keep
 // test `cum - p < top_p`; the boundary tie group (occupied bins of equal
-// probability) and the number of its members kept, lowest ids first. The
-// index cut inside that group is left to the consumers, which count group
-// members in id order as they stream the rows they need; only a drafted token
-// inside its row's group is ranked here, by a rescan of the row prefix.
+// probability) and the number of its members kept, lowest ids first. Block
+// reductions cost one barrier each (partials go to alternating LDS slots).
+// The index cut inside the tie group is left to the consumers, which count
+// group members in id order as they stream the rows they need; a drafted
+// token inside its row's group is ranked by the rank kernel.
+//
+// x / T is evaluated as fl32(fl64(x) * fl64(1 / T)). For a 16-bit x (at most
+// 11 significant bits) and fp32 T this equals the correctly rounded fp32
+// quotient: the fp64 product is within 2^-52 (relative) of x / T, while x / T
+// is never an fp32 rounding midpoint and stays at least 2^-49 (relative) away
+// from every midpoint, its significand being a ratio of integers below 2^24.
 //
 // Elements in bin 0 that carry mass (huge negative logits at huge
 // temperatures) are summed by one more pass. Rows the fixed window cannot
-// represent (values >= 2^18, a maximum among the merged tiny values, tiny
+// represent (values >= 2^16, a maximum among the merged tiny values, tiny
 // values of different probability) are re-streamed into a histogram anchored
-// at the row maximum (keys [kmax - 12802, kmax]). A decision that needs the
+// at the row maximum (keys [kmax - 10242, kmax]). A decision that needs the
 // order of elements below either window marks the row unsupported.
 #include "sdx_launch.hpp"
 
@@ -37,30 +47,39 @@ namespace sdx {
 
 constexpr int SK_NT = 512;
 constexpr int SK_NW = SK_NT / kWave;
-constexpr uint32_t SK_NEG_LO = 0x3780u;   // key of -(2^18 - ulp)
-constexpr uint32_t SK_ZERO_LO = 0x5080u;  // first key of the merged tiny-magnitude bin
-constexpr uint32_t SK_ZERO_HI = 0xAF7Fu;
-constexpr uint32_t SK_POS_LO = 0xAF80u;   // key of 2^-32
-constexpr int SK_WIN = 6400;
-constexpr int SK_BIN_ZERO = 6401;
-constexpr int SK_BIN_EXC = 12802;
-constexpr int SK_TRASH = 12803;           // padding ids past the row end
-constexpr int SK_NB = 12804;
+constexpr uint32_t SK_MAG_LO = 0x3380u;   // magnitude code of 2^-24
+constexpr int SK_WIN = 5120;              // window values per sign
+constexpr uint32_t SK_NEG_LO = 0x3880u;   // key of -(2^16 - ulp)
+constexpr uint32_t SK_ZERO_LO = 0x4C80u;  // first key of the merged tiny-magnitude bin
+constexpr uint32_t SK_ZERO_HI = 0xB37Fu;  // its last key
+constexpr uint32_t SK_POS_LO = 0xB380u;   // key of 2^-24
+constexpr int SK_BIN_ZERO = SK_WIN + 1;
+constexpr int SK_BIN_EXC = 2 * SK_WIN + 2;
+constexpr int SK_NB = 2 * SK_WIN + 4;     // bins, the last one (SK_NB - 1) unused
+constexpr int SK_ETOP = 1024;             // exp values cached for the top bins
 
 __device__ __forceinline__ int sk_bin_of_key(uint32_t k) {
-  const uint32_t c1 = min(k > 0x377Fu ? k - 0x377Fu : 0u, 6401u);
-  const uint32_t c2 = min(k > 0xAF7Fu ? k - 0xAF7Fu : 0u, 6401u);
+  const uint32_t c1 = min(k > SK_NEG_LO - 1 ? k - (SK_NEG_LO - 1) : 0u, (uint32_t)SK_WIN + 1);
+  const uint32_t c2 = min(k > SK_ZERO_HI ? k - SK_ZERO_HI : 0u, (uint32_t)SK_WIN + 1);
   return (int)(c1 + c2);
 }
-// Two packed keys -> two packed bins (v_pk_sub_u16 with clamp, v_pk_min_u16, v_pk_add_u16).
+// Two packed bf16 codes -> two packed byte offsets 4 * bin (each < 2^16):
+// t = clamp(|code| - (SK_MAG_LO - 1), 0, SK_WIN + 1) is the magnitude's place
+// in the window; bin = SK_WIN + 1 + t for a positive code, SK_WIN + 1 - t for
+// a negative one, formed as 4 * (t ^ s) + (4 * (SK_WIN + 1) - 4 * s) with
+// s = 0 or 0xFFFF (the sign spread over the half), all modulo 2^16.
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t sk_bins2(uint32_t keys2) {
-  const us2 k = __builtin_bit_cast(us2, keys2);
-  const us2 c1 = __builtin_elementwise_min(__builtin_elementwise_sub_sat(k, (us2){0x377F, 0x377F}),
-                                           (us2){6401, 6401});
-  const us2 c2 = __builtin_elementwise_min(__builtin_elementwise_sub_sat(k, (us2){0xAF7F, 0xAF7F}),
-                                           (us2){6401, 6401});
-  return __builtin_bit_cast(uint32_t, c1 + c2);
+typedef short ss2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t sk_off2(uint32_t w) {
+  const us2 c = __builtin_bit_cast(us2, w);
+  const us2 mag = c & (us2){0x7FFF, 0x7FFF};
+  const us2 t = __builtin_elementwise_min(
+      __builtin_elementwise_sub_sat(mag, (us2){SK_MAG_LO - 1, SK_MAG_LO - 1}),
+      (us2){SK_WIN + 1, SK_WIN + 1});
+  const us2 s = __builtin_bit_cast(us2, __builtin_bit_cast(ss2, c) >> (ss2){15, 15});
+  const us2 x = t ^ s;
+  const us2 cs = s * (us2){0xFFFC, 0xFFFC} + (us2){4 * (SK_WIN + 1), 4 * (SK_WIN + 1)};
+  return __builtin_bit_cast(uint32_t, x * (us2){4, 4} + cs);
 }
 __device__ __forceinline__ uint32_t max2(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(us2, a),
@@ -73,11 +92,13 @@ struct BinMap {
   bool anchored;
   uint32_t lo;
   uint32_t zrep;  // fixed window: a key of the merged tiny bin standing for all of it
+  uint32_t zlo;   // the merged tiny bin's lowest key: SK_ZERO_LO, or its smallest key
+                  // present when only its members (not its edges) share one exp value
   __device__ uint32_t key_lo(int b) const {
     if (anchored) return b <= 0 ? 0u : lo + (uint32_t)(b - 1);
     if (b <= 0) return 0u;
     if (b <= SK_WIN) return SK_NEG_LO + (uint32_t)(b - 1);
-    if (b == SK_BIN_ZERO) return SK_ZERO_LO;
+    if (b == SK_BIN_ZERO) return zlo;
     return SK_POS_LO + (uint32_t)(b - SK_BIN_ZERO - 1);
   }
   __device__ uint32_t key_hi(int b) const {
@@ -94,74 +115,120 @@ struct BinMap {
   }
 };
 
-__device__ __forceinline__ float sk_d(uint32_t key, float T, float m) {
-  return decode16<SDX_BF16>(code_of_key16(key)) / T - m;
+// fl32(x / T) as fl32(fl64(x) * fl64(1/T)) (equal for 16-bit x, see above)
+__device__ __forceinline__ float sk_s(uint32_t key, double invT) {
+  return (float)((double)decode16<SDX_BF16>(code_of_key16(key)) * invT);
+}
+__device__ __forceinline__ float sk_d(uint32_t key, double invT, float m) {
+  return sk_s(key, invT) - m;
 }
 
 // ---------------------------------------------------------------- block helpers
 // All of them contain barriers: call them from every thread of the block.
-struct SkSmem {
-  uint64_t u64[SK_NW];
-  uint32_t u32[2 * SK_NW];
+// Partials go to LDS slot set `rs`, which then flips: a set is written again
+// only after the next helper's barrier, which every thread passes after
+// reading it, so each helper needs one barrier.
+struct SkRed {
+  uint64_t v[2][4][SK_NW];
 };
-__device__ __forceinline__ uint64_t blk_incl_u64(uint64_t v, SkSmem& sm, uint64_t* total) {
+enum : int { kOpNone = 0, kOpSum64 = 1, kOpMin32 = 2, kOpMax32 = 3, kOpSum32 = 4 };
+template <int O>
+__device__ __forceinline__ uint64_t sk_wave_op(uint64_t v) {
+  if constexpr (O == kOpSum64) return wave_sum_u64(v);
+  else if constexpr (O == kOpMin32) return (uint64_t)(~wave_max_u32(~(uint32_t)v));
+  else if constexpr (O == kOpMax32) return (uint64_t)wave_max_u32((uint32_t)v);
+  else if constexpr (O == kOpSum32) return (uint64_t)wave_sum_u32((uint32_t)v);
+  else return 0;
+}
+template <int O>
+__device__ __forceinline__ uint64_t sk_comb(uint64_t a, uint64_t b) {
+  if constexpr (O == kOpMin32) return min(a, b);
+  else if constexpr (O == kOpMax32) return max(a, b);
+  else return a + b;
+}
+template <int O>
+__device__ __forceinline__ uint64_t sk_ident() {
+  return O == kOpMin32 ? 0xFFFFFFFFull : 0ull;
+}
+struct Red4 {
+  uint64_t v[4];
+};
+template <int O0, int O1 = kOpNone, int O2 = kOpNone, int O3 = kOpNone>
+__device__ __forceinline__ Red4 blk_red(uint64_t a0, uint64_t a1, uint64_t a2, uint64_t a3,
+                                        SkRed& red, int& rs) {
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  const uint64_t x0 = sk_wave_op<O0>(a0), x1 = sk_wave_op<O1>(a1);
+  const uint64_t x2 = sk_wave_op<O2>(a2), x3 = sk_wave_op<O3>(a3);
+  if (lane == 0) {
+    red.v[rs][0][w] = x0;
+    if (O1) red.v[rs][1][w] = x1;
+    if (O2) red.v[rs][2][w] = x2;
+    if (O3) red.v[rs][3][w] = x3;
+  }
+  __syncthreads();
+  Red4 r = {{sk_ident<O0>(), sk_ident<O1>(), sk_ident<O2>(), sk_ident<O3>()}};
+#pragma unroll
+  for (int i = 0; i < SK_NW; ++i) {
+    r.v[0] = sk_comb<O0>(r.v[0], red.v[rs][0][i]);
+    if (O1) r.v[1] = sk_comb<O1>(r.v[1], red.v[rs][1][i]);
+    if (O2) r.v[2] = sk_comb<O2>(r.v[2], red.v[rs][2][i]);
+    if (O3) r.v[3] = sk_comb<O3>(r.v[3], red.v[rs][3][i]);
+  }
+  rs ^= 1;
+  return r;
+}
+__device__ __forceinline__ uint32_t blk_min_u32(uint32_t v, SkRed& red, int& rs) {
+  return (uint32_t)blk_red<kOpMin32>(v, 0, 0, 0, red, rs).v[0];
+}
+__device__ __forceinline__ uint32_t blk_max_u32(uint32_t v, SkRed& red, int& rs) {
+  return (uint32_t)blk_red<kOpMax32>(v, 0, 0, 0, red, rs).v[0];
+}
+__device__ __forceinline__ uint32_t blk_sum_u32(uint32_t v, SkRed& red, int& rs) {
+  return (uint32_t)blk_red<kOpSum32>(v, 0, 0, 0, red, rs).v[0];
+}
+__device__ __forceinline__ uint64_t blk_sum_u64(uint64_t v, SkRed& red, int& rs) {
+  return blk_red<kOpSum64>(v, 0, 0, 0, red, rs).v[0];
+}
+// Inclusive block scan, one barrier; *total gets the block sum.
+__device__ __forceinline__ uint64_t blk_incl_u64(uint64_t v, SkRed& red, int& rs, uint64_t* total) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const uint64_t incl = wave_incl_scan_u64(v, lane);
-  if (lane == kWave - 1) sm.u64[w] = incl;
+  if (lane == kWave - 1) red.v[rs][0][w] = incl;
   __syncthreads();
   uint64_t off = 0, tot = 0;
 #pragma unroll
   for (int i = 0; i < SK_NW; ++i) {
-    const uint64_t x = sm.u64[i];
+    const uint64_t x = red.v[rs][0][i];
     off += i < w ? x : 0ull;
     tot += x;
   }
-  __syncthreads();
+  rs ^= 1;
   *total = tot;
   return off + incl;
 }
-__device__ __forceinline__ uint32_t blk_incl_u32(uint32_t v, SkSmem& sm, uint32_t* total) {
+__device__ __forceinline__ uint32_t blk_incl_u32(uint32_t v, SkRed& red, int& rs, uint32_t* total) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const uint32_t incl = wave_incl_scan_u32(v, lane);
-  if (lane == kWave - 1) sm.u32[w] = incl;
+  if (lane == kWave - 1) red.v[rs][0][w] = incl;
   __syncthreads();
   uint32_t off = 0, tot = 0;
 #pragma unroll
   for (int i = 0; i < SK_NW; ++i) {
-    const uint32_t x = sm.u32[i];
+    const uint32_t x = (uint32_t)red.v[rs][0][i];
     off += i < w ? x : 0u;
     tot += x;
   }
-  __syncthreads();
+  rs ^= 1;
   *total = tot;
   return off + incl;
 }
-__device__ __forceinline__ uint64_t blk_sum_u64(uint64_t v, SkSmem& sm) {
-  uint64_t t;
-  blk_incl_u64(v, sm, &t);
-  return t;
-}
-__device__ __forceinline__ uint32_t blk_sum_u32(uint32_t v, SkSmem& sm) {
-  uint32_t t;
-  blk_incl_u32(v, sm, &t);
-  return t;
-}
-__device__ __forceinline__ uint32_t blk_min_u32(uint32_t v, SkSmem& sm) {
-  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o, kWave));
-  if (lane == 0) sm.u32[SK_NW + w] = v;
-  __syncthreads();
-  uint32_t r = 0xFFFFFFFFu;
-#pragma unroll
-  for (int i = 0; i < SK_NW; ++i) r = min(r, sm.u32[SK_NW + i]);
-  __syncthreads();
-  return r;
-}
-__device__ __forceinline__ uint32_t blk_max_u32(uint32_t v, SkSmem& sm) {
-  return ~blk_min_u32(~v, sm);
-}
 
+// Whole block: the largest key of the row (padding / -NaN code 0xFFFF has key 0).
+__device__ uint32_t exact_kmax(const uint16_t* __restrict__ ptr, int64_t V, SkRed& red, int& rs) {
+  uint32_t mx = 0;
+  for (int64_t i = threadIdx.x; i < V; i += SK_NT) mx = max(mx, key_of_code16(ptr[i]));
+  return blk_max_u32(mx, red, rs);
+}
 // Whole block: counts the row's elements into `hist` under an anchored map.
 __device__ void restream_anchored(const uint16_t* __restrict__ ptr, int64_t V, const BinMap& bm,
                                   uint32_t* hist) {
@@ -187,52 +254,60 @@ struct Extremes {
   uint32_t below_max, zkey_min, ze_min, ze_max;
 };
 __device__ Extremes key_extremes(const uint16_t* __restrict__ ptr, int64_t V, uint32_t lo,
-                                 uint32_t zlo, uint32_t zhi, float T, float m, SkSmem& sm) {
+                                 uint32_t zlo, uint32_t zhi, double invT, float m, SkRed& red,
+                                 int& rs) {
   uint32_t b = 0, z0 = 0xFFFFu, e0 = 0xFFFFFFFFu, e1 = 0;
   for (int64_t i = threadIdx.x; i < V; i += SK_NT) {
     const uint32_t k = key_of_code16(ptr[i]);
     if (k < lo) b = max(b, k);
     if (k >= zlo && k <= zhi) {
-      const uint32_t e = __float_as_uint(exp_det(sk_d(k, T, m)));
+      const uint32_t e = __float_as_uint(exp_det(sk_d(k, invT, m)));
       z0 = min(z0, k);
       e0 = min(e0, e);
       e1 = max(e1, e);
     }
   }
+  const Red4 r = blk_red<kOpMax32, kOpMin32, kOpMin32, kOpMax32>(b, z0, e0, e1, red, rs);
   Extremes x;
-  x.below_max = blk_max_u32(b, sm);
-  x.zkey_min = blk_min_u32(z0, sm);
-  x.ze_min = blk_min_u32(e0, sm);
-  x.ze_max = blk_max_u32(e1, sm);
+  x.below_max = (uint32_t)r.v[0];
+  x.zkey_min = (uint32_t)r.v[1];
+  x.ze_min = (uint32_t)r.v[2];
+  x.ze_max = (uint32_t)r.v[3];
   return x;
 }
 // Whole block: sum over elements with key < lo of fixed62(exp_det(x/T - m) / div),
 // exact in 128 bits (split as sum lo32 + 2^32 sum hi32, each below 2^63).
-__device__ U128 below_sum(const uint16_t* __restrict__ ptr, int64_t V, uint32_t lo, float T,
-                          float m, float div, SkSmem& sm) {
+__device__ U128 below_sum(const uint16_t* __restrict__ ptr, int64_t V, uint32_t lo, double invT,
+                          float m, float div, SkRed& red, int& rs) {
   uint64_t slo = 0, shi = 0;
   for (int64_t i = threadIdx.x; i < V; i += SK_NT) {
     const uint32_t k = key_of_code16(ptr[i]);
     if (k < lo) {
-      const float e = exp_det(sk_d(k, T, m));
+      const float e = exp_det(sk_d(k, invT, m));
       const uint64_t f = fixed62(div == 1.0f ? e : e / div);
       slo += (uint32_t)f;
       shi += (uint32_t)(f >> 32);
     }
   }
-  slo = blk_sum_u64(slo, sm);
-  shi = blk_sum_u64(shi, sm);
-  return u128_add(U128{slo, 0}, U128{shi << 32, shi >> 32});
+  const Red4 r = blk_red<kOpSum64, kOpSum64>(slo, shi, 0, 0, red, rs);
+  return u128_add(U128{r.v[0], 0}, U128{r.v[1] << 32, r.v[1] >> 32});
 }
+
+// All LDS of the kernel in one object, histogram first (LDS address 0, so the
+// streaming atomics address it by byte offset alone).
+struct SkLds {
+  uint32_t hist[SK_NB];
+  float etop[SK_ETOP];  // exp values of the top SK_ETOP bins (bmax - i); occupied ones only
+  SkRed red;
+  int32_t i32[12];
+  uint64_t x64[2];
+};
 
 __global__ void __launch_bounds__(SK_NT) __attribute__((amdgpu_waves_per_eu(6)))
 rowstream_bf16_kernel(RowStatArgs a) {
-  __shared__ uint32_t hist[SK_NB];
-  __shared__ float etop[SK_NT];  // exp values of the top SK_NT bins (0 if unoccupied)
-  __shared__ SkSmem sm;
-  __shared__ int32_t s_i32[12];
-  __shared__ uint64_t s_x64[2];
-  __shared__ float s_f[2];
+  __shared__ SkLds L;
+  uint32_t* const hist = L.hist;
+  int rs = 0;
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int64_t row = blockIdx.x;
@@ -257,59 +332,75 @@ rowstream_bf16_kernel(RowStatArgs a) {
   for (int b = tid; b < SK_NB; b += SK_NT) hist[b] = 0u;
   __syncthreads();
 
-  // ---- 1. stream the row: 16-byte loads, packed keys -> packed bins, LDS atomics
-  uint32_t kmx2 = 0;  // packed running maximum of keys
+  // ---- 1. stream the row: 16-byte loads two stages deep, packed codes ->
+  // packed bin offsets, LDS atomics; the running maximum on the offsets
+  uint32_t omx = 0;
   {
-    constexpr int U = 4;  // 16-byte loads in flight per lane
-    const int64_t stride = (int64_t)SK_NT * 8;
-    for (int64_t i0 = (int64_t)tid * 8; i0 < V; i0 += stride * U) {
-      uint4 v[U];
+    // raw buffer loads: per-lane offset tid * 16 stays in a register, the
+    // iteration offset is scalar; loads past the row read zeros (unused)
+    constexpr int U = 4;
+    constexpr uint32_t kStep = (uint32_t)SK_NT * U;
+    const uint32_t n4 = (uint32_t)(V >> 3);  // whole 8-element groups (V < 2^31)
+    const uint32_t iters = (n4 + kStep - 1) / kStep;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)ptr, (short)0, (int)(n4 * 16u), 0x00020000);
+    const uint32_t voff = (uint32_t)tid * 16u;
+    char* const hb = reinterpret_cast<char*>(hist);
+    auto load = [&](uint4 (&d)[U], uint32_t it) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int64_t e0 = i0 + u * stride;
-        if (e0 + 8 <= V) {
-          v[u] = *reinterpret_cast<const uint4*>(ptr + e0);
-        } else if (e0 < V) {  // the row's last partial group, element by element
-          uint32_t w[4] = {0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu};
-#pragma unroll
-          for (int t = 0; t < 8; ++t)
-            if (e0 + t < V)
-              w[t >> 1] = (w[t >> 1] & ~(0xFFFFu << (16 * (t & 1)))) |
-                          ((uint32_t)ptr[e0 + t] << (16 * (t & 1)));
-          v[u] = make_uint4(w[0], w[1], w[2], w[3]);
-        }
+        const auto x = __builtin_amdgcn_raw_buffer_load_b128(
+            rsrc, (int)voff, (int)((it * kStep + (uint32_t)u * SK_NT) * 16u), 0);
+        d[u] = make_uint4(x[0], x[1], x[2], x[3]);
       }
+    };
+    auto proc = [&](const uint4& v) {
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int64_t e0 = i0 + u * stride;
-        if (e0 < V) {
-          const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-          uint32_t bins[4];
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t o = sk_off2(w[t]);
+        omx = max2(omx, o);
+        atomicAdd(reinterpret_cast<uint32_t*>(hb + (o & 0xFFFFu)), 1u);
+        atomicAdd(reinterpret_cast<uint32_t*>(hb + (o >> 16)), 1u);
+      }
+    };
+    auto proc_all = [&](const uint4 (&d)[U]) {
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const uint32_t k2 = keys2_of_codes2(w[t]);  // padding code 0xFFFF -> key 0
-            kmx2 = max2(kmx2, k2);
-            bins[t] = sk_bins2(k2);
-          }
-          if (e0 + 8 <= V) {
+      for (int u = 0; u < U; ++u) proc(d[u]);
+    };
+    auto proc_last = [&](const uint4 (&d)[U], uint32_t it) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              atomicAdd(&hist[bins[t] & 0xFFFFu], 1u);
-              atomicAdd(&hist[bins[t] >> 16], 1u);
-            }
-          } else {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-              const uint32_t bb = (t & 1) ? (bins[t >> 1] >> 16) : (bins[t >> 1] & 0xFFFFu);
-              atomicAdd(&hist[e0 + t < V ? bb : (uint32_t)SK_TRASH], 1u);
-            }
-          }
-        }
+      for (int u = 0; u < U; ++u)
+        if (it * kStep + (uint32_t)u * SK_NT + (uint32_t)tid < n4) proc(d[u]);
+    };
+    if (iters > 0) {
+      uint4 A[U], B[U];
+      load(A, 0);
+      for (uint32_t it = 0;; it += 2) {  // uniform control flow
+        if (it + 1 >= iters) { proc_last(A, it); break; }
+        load(B, it + 1);
+        proc_all(A);
+        if (it + 2 >= iters) { proc_last(B, it + 1); break; }
+        load(A, it + 2);
+        proc_all(B);
       }
     }
+    const int64_t t0 = (int64_t)n4 * 8;  // the last V % 8 elements, one per thread
+    if (tid < V - t0) {
+      const uint32_t o = 4u * (uint32_t)sk_bin_of_key(key_of_code16(ptr[t0 + tid]));
+      omx = max2(omx, o);
+      atomicAdd(reinterpret_cast<uint32_t*>(hb + o), 1u);
+    }
   }
-  // (the reduction's barriers also complete the histogram)
-  const uint32_t kmax = blk_max_u32(max(kmx2 & 0xFFFFu, kmx2 >> 16), sm);
+  // (the reduction's barrier also completes the histogram)
+  const int bmx = (int)(blk_max_u32(max(omx & 0xFFFFu, omx >> 16), L.red, rs) >> 2);
+  uint32_t kmax;
+  if (bmx >= 1 && bmx <= 2 * SK_WIN + 1 && bmx != SK_BIN_ZERO) {
+    kmax = bmx <= SK_WIN ? SK_NEG_LO + (uint32_t)(bmx - 1)
+                         : SK_POS_LO + (uint32_t)(bmx - SK_BIN_ZERO - 1);
+  } else {  // the maximum is not a single window value: find it (uniform branch)
+    kmax = exact_kmax(ptr, V, L.red, rs);
+  }
 
   if (kmax >= kPosInfKey<SDX_BF16> || kmax == 0) {  // +inf / NaN: flag, outputs unspecified
     if (tid == 0) {
@@ -321,14 +412,15 @@ rowstream_bf16_kernel(RowStatArgs a) {
     return;
   }
   const float T = a.T;
-  const float m = decode16<SDX_BF16>(code_of_key16(kmax)) / T;
+  const double invT = 1.0 / (double)T;
+  const float m = sk_s(kmax, invT);
 
   // ---- 2. fixed window valid for this row? else re-stream anchored at kmax.
   // Bin 0 ("below the window") may carry mass: then Z adds it by one more pass
   // and a decision that needs it marks the row unsupported. The quick checks
   // use the bins' edge keys; when they fail, one pass finds the actual extreme
   // keys (rare: huge negative logits at huge temperatures, tiny logits).
-  BinMap bm{false, 0u, 0x8000u};
+  BinMap bm{false, 0u, 0x8000u, SK_ZERO_LO};
   uint32_t rflags = 0;
   uint32_t below_lo = SK_NEG_LO;  // keys below it are below the window
   bool below_mass = false;        // ... and some of them have exp_det > 0
@@ -336,21 +428,22 @@ rowstream_bf16_kernel(RowStatArgs a) {
   {
     const int b0 = sk_bin_of_key(kmax);
     bool ok = b0 >= 1 && b0 != SK_BIN_EXC;
-    const bool maybe_below = ok && hist[0] != 0 && exp_det(sk_d(SK_NEG_LO - 1, T, m)) > 0.0f;
+    const bool maybe_below = ok && hist[0] != 0 && exp_det(sk_d(SK_NEG_LO - 1, invT, m)) > 0.0f;
     // the merged tiny bin needs one exp value for all its members: d equal at its
     // edges (fp32 division and subtraction are monotone), else checked per member
-    const float dz = sk_d(0x8000u, T, m);
+    const float dz = sk_d(0x8000u, invT, m);
     const bool check_zero = ok && hist[SK_BIN_ZERO] != 0 &&
-                            !(sk_d(SK_ZERO_LO, T, m) == dz && sk_d(SK_ZERO_HI, T, m) == dz);
+                            !(sk_d(SK_ZERO_LO, invT, m) == dz && sk_d(SK_ZERO_HI, invT, m) == dz);
     if (maybe_below || check_zero) {  // uniform across the block
-      const Extremes x = key_extremes(ptr, V, SK_NEG_LO, SK_ZERO_LO, SK_ZERO_HI, T, m, sm);
+      const Extremes x =
+          key_extremes(ptr, V, SK_NEG_LO, SK_ZERO_LO, SK_ZERO_HI, invT, m, L.red, rs);
       if (maybe_below) {
         below_top = x.below_max;
-        below_mass = exp_det(sk_d(below_top, T, m)) > 0.0f;
+        below_mass = exp_det(sk_d(below_top, invT, m)) > 0.0f;
       }
       if (check_zero) {
-        if (x.ze_min == x.ze_max) bm.zrep = x.zkey_min;
-        else ok = false;
+        if (x.ze_min == x.ze_max) bm.zrep = bm.zlo = x.zkey_min;  // consumers read the
+        else ok = false;                                            // group's p at its lo key
       }
     }
     if (!ok) {  // uniform across the block
@@ -363,44 +456,41 @@ rowstream_bf16_kernel(RowStatArgs a) {
       __syncthreads();
       restream_anchored(ptr, V, bm, hist);
       __syncthreads();
-      if (bm.lo > 0 && hist[0] != 0 && exp_det(sk_d(bm.lo - 1, T, m)) > 0.0f) {
-        below_top = key_extremes(ptr, V, bm.lo, 1u, 0u, T, m, sm).below_max;
-        below_mass = exp_det(sk_d(below_top, T, m)) > 0.0f;
+      if (bm.lo > 0 && hist[0] != 0 && exp_det(sk_d(bm.lo - 1, invT, m)) > 0.0f) {
+        below_top = key_extremes(ptr, V, bm.lo, 1u, 0u, invT, m, L.red, rs).below_max;
+        below_mass = exp_det(sk_d(below_top, invT, m)) > 0.0f;
       }
     }
     if (below_mass) rflags |= kRowBelowWindow;
   }
   const int bmax = bm.bin(kmax);
-  auto e_of_bin = [&](int b) -> float { return exp_det(sk_d(bm.key_rep(b), T, m)); };
+  auto e_of_bin = [&](int b) -> float { return exp_det(sk_d(bm.key_rep(b), invT, m)); };
 
   // ---- 3. exact normaliser: sum c * fixed62(e) as sum c * lo32 + 2^32 sum c * hi32
   // (sum c <= V < 2^31 keeps both below 2^63). Thread t takes bins bmax - t - j*SK_NT,
-  // so the first round covers the top bins and leaves their exp values in etop.
+  // so the first rounds cover the top bins and leave their exp values in etop.
+  float zf;
   {
     uint64_t slo = 0, shi = 0;
     for (int b = bmax - tid, j = 0; b >= 1; b -= SK_NT, ++j) {
       const uint32_t c = hist[b];
-      const float e = c ? e_of_bin(b) : 0.0f;
-      if (j == 0) etop[tid] = e;
       if (c) {
+        const float e = e_of_bin(b);
+        if (j * SK_NT < SK_ETOP) L.etop[tid + j * SK_NT] = e;
         const uint64_t f = fixed62(e);
         slo += (uint64_t)c * (uint32_t)f;
         shi += (uint64_t)c * (uint32_t)(f >> 32);
       }
     }
-    if (bmax - tid < 1) etop[tid] = 0.0f;
-    slo = blk_sum_u64(slo, sm);
-    shi = blk_sum_u64(shi, sm);
-    U128 z = u128_add(U128{slo, 0}, U128{shi << 32, shi >> 32});
-    if (below_mass) z = u128_add(z, below_sum(ptr, V, below_lo, T, m, 1.0f, sm));
-    if (tid == 0) s_f[0] = rn32_u128(z);
-    __syncthreads();
+    const Red4 zr = blk_red<kOpSum64, kOpSum64>(slo, shi, 0, 0, L.red, rs);
+    U128 z = u128_add(U128{zr.v[0], 0}, U128{zr.v[1] << 32, zr.v[1] >> 32});
+    if (below_mass) z = u128_add(z, below_sum(ptr, V, below_lo, invT, m, 1.0f, L.red, rs));
+    zf = rn32_u128(z);  // every thread, same value
   }
-  const float zf = s_f[0];
   auto p_of_bin = [&](int b) -> float {
     if (b < 1) return 0.0f;
     const int i = bmax - b;
-    return (i < SK_NT ? etop[i] : e_of_bin(b)) / zf;
+    return (i < SK_ETOP ? L.etop[i] : e_of_bin(b)) / zf;
   };
 
   // ---- 4. top-k threshold: rounds of one bin per thread, descending from bmax
@@ -413,9 +503,9 @@ rowstream_bf16_kernel(RowStatArgs a) {
       const int b = top - tid;
       const uint32_t c = b >= 1 ? hist[b] : 0u;
       uint32_t tot;
-      const uint32_t incl = blk_incl_u32(c, sm, &tot);
+      const uint32_t incl = blk_incl_u32(c, L.red, rs, &tot);
       const bool hit = c != 0 && before + incl >= (uint32_t)a.top_k;
-      const uint32_t th = blk_min_u32(hit ? (uint32_t)tid : 0xFFFFFFFFu, sm);
+      const uint32_t th = blk_min_u32(hit ? (uint32_t)tid : 0xFFFFFFFFu, L.red, rs);
       if (th != 0xFFFFFFFFu) { kb = top - (int)th; break; }
       before += tot;
     }
@@ -440,13 +530,12 @@ rowstream_bf16_kernel(RowStatArgs a) {
         if (nxt < 1 || p_of_bin(nxt) != p_kth) break;
         lowb = nxt;
       }
-      if (tid == 0) s_i32[0] = lowb;
+      if (tid == 0) L.i32[0] = lowb;
     }
     __syncthreads();
-    klo_bin = s_i32[0];
-    __syncthreads();
+    klo_bin = L.i32[0];
     // ties at the k-th that continue below the window cannot be ordered here
-    if (k_cut && below_mass && exp_det(sk_d(below_top, T, m)) / zf == p_of_bin(kb))
+    if (k_cut && below_mass && exp_det(sk_d(below_top, invT, m)) / zf == p_of_bin(kb))
       rflags |= kRowUnsupported;
   }
 
@@ -458,45 +547,42 @@ rowstream_bf16_kernel(RowStatArgs a) {
     const float tp = a.top_p;
     uint64_t S = 0;
     int bb = -1;
+    float pb = 0.0f;
+    int gtop0 = 0, gbot0 = 0;
+    uint32_t above0 = 0, gcnt0 = 0;
     for (int top = bmax; top >= klo_bin; top -= SK_NT) {
       const int b = top - tid;
       const uint32_t c = b >= klo_bin ? hist[b] : 0u;
       const float p = c ? p_of_bin(b) : 0.0f;
       const uint64_t mi = (uint64_t)c * fixed62(p);
       uint64_t tot;
-      const uint64_t incl = blk_incl_u64(mi, sm, &tot);
+      const uint64_t incl = blk_incl_u64(mi, L.red, rs, &tot);
+      // keep fails from the boundary bin on (cum grows, p shrinks, fp32 ops monotone)
       const bool fail = c != 0 && !((rn32_u64(S + incl) - p) < tp);
-      const uint32_t tf = blk_min_u32(fail ? (uint32_t)tid : 0xFFFFFFFFu, sm);
-      if (tf != 0xFFFFFFFFu) {  // the boundary bin is in this round
-        if (tid == (int)tf) {
-          s_x64[0] = S + incl - mi;  // mass before the boundary bin
-          s_i32[1] = (int32_t)c;
-          s_f[1] = p;
-        }
+      const uint32_t tf = blk_min_u32(fail ? (uint32_t)tid : 0xFFFFFFFFu, L.red, rs);
+      if (tf != 0xFFFFFFFFu) {  // the boundary bin is in this round (uniform)
         bb = top - (int)tf;
-        __syncthreads();
+        pb = p_of_bin(bb);
+        if (tid == (int)tf) L.x64[0] = S + incl - mi;  // mass before the boundary bin
         // group bins of this round: occupied, of the boundary's probability
-        const bool in_g = c != 0 && p == s_f[1];
-        const uint32_t gmax = blk_max_u32(in_g ? (uint32_t)b : 0u, sm);
-        const uint32_t gmin = blk_min_u32(in_g ? (uint32_t)b : 0xFFFFFFFFu, sm);
-        const uint32_t above = blk_sum_u32(in_g && b > bb ? c : 0u, sm);
-        const uint32_t gsum = blk_sum_u32(in_g ? c : 0u, sm);
-        if (tid == 0) {
-          s_i32[2] = (int32_t)gmax; s_i32[3] = (int32_t)gmin;
-          s_i32[4] = (int32_t)above; s_i32[5] = (int32_t)gsum;
-          }
+        const bool in_g = c != 0 && p == pb;
+        const Red4 gr = blk_red<kOpMax32, kOpMin32, kOpSum32, kOpSum32>(
+            in_g ? (uint32_t)b : 0u, in_g ? (uint32_t)b : 0xFFFFFFFFu,
+            in_g && b > bb ? c : 0u, in_g ? c : 0u, L.red, rs);
+        gtop0 = (int)gr.v[0];
+        gbot0 = (int)gr.v[1];
+        above0 = (uint32_t)gr.v[2];
+        gcnt0 = (uint32_t)gr.v[3];
         break;
       }
       S += tot;
     }
-    __syncthreads();
-    if (bb >= 1) {
-      const uint64_t Sb0 = s_x64[0];
-      const uint32_t cb = (uint32_t)s_i32[1];
-      const float pb = s_f[1];
+    if (bb >= 1) {  // uniform
       if (tid < kWave) {  // wave 0: the group beyond this round (rare), then the kept count
-        int gtop = s_i32[2], gbot = s_i32[3];
-        uint32_t above = (uint32_t)s_i32[4], gcnt = (uint32_t)s_i32[5];
+        const uint64_t Sb0 = L.x64[0];  // written before the group reduction's barrier
+        const uint32_t cb = hist[bb];
+        int gtop = gtop0, gbot = gbot0;
+        uint32_t above = above0, gcnt = gcnt0;
         {  // occupied bins above the round's group bins: the first one differs unless
            // the group continues into earlier rounds
           for (;;) {
@@ -543,21 +629,21 @@ rowstream_bf16_kernel(RowStatArgs a) {
         uint32_t rr = lo_r;
         if (Sb0 == (uint64_t)above * P && above == 0 && rr == 0) rr = 1;  // keep[..., 0] = True
         if (tid == 0) {
-          s_i32[7] = gtop; s_i32[8] = gbot; s_i32[9] = (int32_t)(above + rr);
-          s_i32[10] = (int32_t)gcnt;
-          s_x64[1] = Sb0 + (uint64_t)rr * P;
+          L.i32[7] = gtop; L.i32[8] = gbot; L.i32[9] = (int32_t)(above + rr);
+          L.i32[10] = (int32_t)gcnt;
+          L.x64[1] = Sb0 + (uint64_t)rr * P;
         }
       }
       __syncthreads();
-      ghi_b = s_i32[7];
-      glo_b = s_i32[8];
-      rstar = s_i32[9];
-      gcount = s_i32[10];
-      kept_mass = s_x64[1];
+      ghi_b = L.i32[7];
+      glo_b = L.i32[8];
+      rstar = L.i32[9];
+      gcount = L.i32[10];
+      kept_mass = L.x64[1];
       klo_bin = glo_b;
       has_group = true;
       // a tie group that continues below the window cannot be ordered here
-      if (below_mass && exp_det(sk_d(below_top, T, m)) / zf == pb) rflags |= kRowUnsupported;
+      if (below_mass && exp_det(sk_d(below_top, invT, m)) / zf == pb) rflags |= kRowUnsupported;
     } else {
       kept_mass = S;
       if (below_mass && !k_cut) rflags |= kRowUnsupported;  // nucleus reaches below the window
@@ -571,8 +657,9 @@ rowstream_bf16_kernel(RowStatArgs a) {
       const uint32_t c = hist[b];
       if (c) acc += (uint64_t)c * fixed62(p_of_bin(b));
     }
-    kept_mass = blk_sum_u64(acc, sm);
-    if (below_mass && keep_below) kept_mass += below_sum(ptr, V, below_lo, T, m, zf, sm).lo;
+    kept_mass = blk_sum_u64(acc, L.red, rs);
+    if (below_mass && keep_below)
+      kept_mass += below_sum(ptr, V, below_lo, invT, m, zf, L.red, rs).lo;
   }
   const float totf = fmaxf(rn32_u64(kept_mass), 1e-12f);
   const int32_t klo = keep_below ? 0 : (int32_t)bm.key_lo(klo_bin);
@@ -589,7 +676,7 @@ rowstream_bf16_kernel(RowStatArgs a) {
     if (b >= 1) {
       v = hist[b] != 0 ? p_of_bin(b) / totf : 0.0f;
     } else {  // below the window: exact per key (zero in the fixed window)
-      v = exp_det(sk_d(kk, T, m)) / zf / totf;
+      v = exp_det(sk_d(kk, invT, m)) / zf / totf;
     }
     tbl_out[t] = v;
   }
@@ -605,7 +692,7 @@ rowstream_bf16_kernel(RowStatArgs a) {
       if (rstar <= 0) kept = false;
       else if (rstar < gcount) { kept = false; rflags |= kRowRank; }
     }
-    if (kept) pg = exp_det(sk_d((uint32_t)kk, T, m)) / zf / totf;
+    if (kept) pg = exp_det(sk_d((uint32_t)kk, invT, m)) / zf / totf;
   }
   if (tid == 0) {
     RowStat st;

@@ -171,25 +171,26 @@ def test_g1_config1_on_gpu():
 
 def _window_edge_rows(V):
     """bf16 rows at and beyond the edges of the streaming kernel's fixed value
-    window (|x| in [2^-32, 2^18)), which it re-streams into a window anchored
-    at the row maximum, mixed with ordinary rows."""
+    window (|x| in [2^-24, 2^16)), which it re-streams into a window anchored
+    at the row maximum, mixed with ordinary rows. Rows 0, 2 and 8 hold values
+    with |x| >= 2^16."""
     g = np.random.default_rng(17)
     base = (g.standard_normal((10, V)) * 3).astype(np.float32)
     rows = [base[0].copy() for _ in range(10)]
-    rows[0][[3, 77]] = [3.0e6, 2.5e6]                     # >= 2^18: leaves the window
+    rows[0][[3, 77]] = [3.0e6, 2.5e6]                     # >= 2^16: leaves the window
     rows[1] = (g.standard_normal(V) * 1e-13).astype(np.float32)   # max among tiny values
     rows[1][[10, 11]] = [0.0, -0.0]
-    rows[2][::7] = -3.0e6                                 # <= -2^18: bin 0, zero mass
+    rows[2][::7] = -3.0e6                                 # <= -2^16: bin 0, zero mass
     rows[3][::5] = 1e-20                                  # tiny values share exp(-m)
     rows[3][1::5] = -1e-30
     rows[4][:] = -np.inf
     rows[4][[1, 2, 3]] = [-1e-14, -2e-14, -2e-14]         # max inside the merged tiny bin
     rows[5] = base[5]                                     # ordinary
-    rows[6][::3] = -2.5e5                                 # just inside the window
-    rows[7][[0, V - 1]] = [2.6e5, 2.6e5]                  # top of the window, tie at both ends
-    rows[8][[5, 6]] = [2.63e5, 2.62e5]                    # 2^18 and just below it
-    rows[9][::4] = 3e-10                                  # just above 2^-32
-    rows[9][1::4] = -2e-10                                # just below it
+    rows[6][::3] = -6.0e4                                 # just inside the window
+    rows[7][[0, V - 1]] = [6.5e4, 6.5e4]                  # top of the window, tie at both ends
+    rows[8][[5, 6]] = [6.6e4, 6.5e4]                      # 2^16 and just below it
+    rows[9][::4] = 7e-8                                   # just above 2^-24
+    rows[9][1::4] = -5e-8                                 # just below it
     return np.stack(rows)
 
 
@@ -201,12 +202,12 @@ def test_to_probs_bf16_window_edges(T, tp, tk):
     got = _np(S.to_probs(x, T, tp, tk))
     ref = O.to_probs(_np(x), T, tp, tk)
     # rows the kernels cannot represent come back as NaN (the C API also flags
-    # them in verify); only absurd temperatures with |x| >= 2^18 produce them
+    # them in verify); only absurd temperatures on rows with |x| >= 2^16 produce them
     bad = np.isnan(got).any(axis=1)
     assert not np.isnan(got[~bad]).any()
     if T < 1e3:
         assert not bad.any()
-    assert bad.sum() <= 2
+    assert set(np.flatnonzero(bad)) <= {0, 2, 8}
     _assert_probs_equal(got[~bad], ref[~bad])
 
 

@@ -94,3 +94,31 @@ def test_uniform_threshold_exact():
     assert uniform_threshold(np.float32(0.0), 10 ** 18) == 0
     with pytest.raises(ValueError):
         uniform_threshold(np.float32(1.0), 5)
+
+
+def _all_codes16(fmt):
+    c = np.arange(65536, dtype=np.uint32)
+    if fmt == "bf16":
+        return (c << 16).view(np.float32)
+    return c.astype(np.uint16).view(np.float16).astype(np.float32)
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "f16"])
+def test_scaled_logit_by_fp64_reciprocal_equals_fp32_division(fmt):
+    """The kernels evaluate x / T as fl32(fl64(x) * fl64(1/T)). For every
+    16-bit x and fp32 T this must equal numpy's correctly rounded fp32
+    division (the reference's `logits / temperature`): checked here over all
+    65,536 codes for a spread of temperatures, including ones whose inverse
+    is not exact and huge / tiny ones that overflow or underflow the quotient."""
+    x = _all_codes16(fmt)
+    rs = np.random.RandomState(7)
+    temps = [0.8, 0.7, 0.1, 1.0 / 3.0, 3.0, 1.5, 1e-3, 4e6, 1e-30, 3e38, 0.95, 2.0 ** -20,
+             1.0 + 2.0 ** -23, 1.0 - 2.0 ** -24]
+    temps += list(rs.uniform(0.05, 4.0, 40)) + list(np.exp(rs.uniform(-60, 60, 20)))
+    with np.errstate(all="ignore"):
+        for T in temps:
+            T32 = np.float32(T)
+            want = x / T32
+            got = (x.astype(np.float64) * (1.0 / np.float64(T32))).astype(np.float32)
+            same = (want == got) | (np.isnan(want) & np.isnan(got))
+            assert same.all(), (fmt, T, x[~same][:4], want[~same][:4], got[~same][:4])
