@@ -22,6 +22,8 @@ struct RowStatArgs {
   uint32_t* zero;  // words [0, nzero) cleared (block `row` clears word `row`), or null
   int64_t nzero;
   uint64_t* rank_acc;  // [rows] rank accumulators, cleared by the row kernel, or null
+  int64_t late_block;  // bf16 streaming kernel: blocks from here stream at raised wave
+                       // priority (set by launch_rowstream_bf16)
 };
 
 struct F32Args {

@@ -334,6 +334,10 @@ rowstream_bf16_kernel(RowStatArgs a) {
 
   // ---- 1. stream the row: 16-byte loads two stages deep, packed codes ->
   // packed bin offsets, LDS atomics; the running maximum on the offsets
+  // Blocks dealt after two per CU share a CU with two older workgroups, whose
+  // waves win instruction arbitration; raising this block's wave priority while
+  // it streams lets all three stream side by side instead of this one last.
+  if ((int64_t)blockIdx.x >= a.late_block) __builtin_amdgcn_s_setprio(3);
   uint32_t omx = 0;
   {
     // raw buffer loads: per-lane offset tid * 16 stays in a register, the
@@ -392,6 +396,7 @@ rowstream_bf16_kernel(RowStatArgs a) {
       atomicAdd(reinterpret_cast<uint32_t*>(hb + o), 1u);
     }
   }
+  __builtin_amdgcn_s_setprio(0);
   // (the reduction's barrier also completes the histogram)
   const int bmx = (int)(blk_max_u32(max(omx & 0xFFFFu, omx >> 16), L.red, rs) >> 2);
   uint32_t kmax;
@@ -487,10 +492,13 @@ rowstream_bf16_kernel(RowStatArgs a) {
     if (below_mass) z = u128_add(z, below_sum(ptr, V, below_lo, invT, m, 1.0f, L.red, rs));
     zf = rn32_u128(z);  // every thread, same value
   }
+  // e / zf as fl32(fl64(e) * fl64(1 / zf)): the correctly rounded quotient
+  // for fp32 operands (same argument as for x / T above)
+  const double invz = 1.0 / (double)zf;
   auto p_of_bin = [&](int b) -> float {
     if (b < 1) return 0.0f;
     const int i = bmax - b;
-    return (i < SK_ETOP ? L.etop[i] : e_of_bin(b)) / zf;
+    return (float)((double)(i < SK_ETOP ? L.etop[i] : e_of_bin(b)) * invz);
   };
 
   // ---- 4. top-k threshold: rounds of one bin per thread, descending from bmax
@@ -662,6 +670,7 @@ rowstream_bf16_kernel(RowStatArgs a) {
       kept_mass += below_sum(ptr, V, below_lo, invT, m, zf, L.red, rs).lo;
   }
   const float totf = fmaxf(rn32_u64(kept_mass), 1e-12f);
+  const double invtot = 1.0 / (double)totf;
   const int32_t klo = keep_below ? 0 : (int32_t)bm.key_lo(klo_bin);
   const int32_t glo = has_group ? (int32_t)bm.key_lo(glo_b) : klo;
   const int32_t ghi = has_group ? (int32_t)bm.key_hi(ghi_b) : klo - 1;
@@ -674,7 +683,7 @@ rowstream_bf16_kernel(RowStatArgs a) {
     const int b = bm.bin(kk);
     float v;
     if (b >= 1) {
-      v = hist[b] != 0 ? p_of_bin(b) / totf : 0.0f;
+      v = hist[b] != 0 ? (float)((double)p_of_bin(b) * invtot) : 0.0f;
     } else {  // below the window: exact per key (zero in the fixed window)
       v = exp_det(sk_d(kk, invT, m)) / zf / totf;
     }
@@ -714,7 +723,24 @@ rowstream_bf16_kernel(RowStatArgs a) {
   }
 }
 
-hipError_t launch_rowstream_bf16(const RowStatArgs& a, int64_t rows, hipStream_t s) {
+// Compute units of the current device (cached per device; 0 if unknown).
+static int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+hipError_t launch_rowstream_bf16(const RowStatArgs& args, int64_t rows, hipStream_t s) {
+  RowStatArgs a = args;
+  const int cus = device_cus();
+  a.late_block = cus > 0 ? 2 * (int64_t)cus : INT64_MAX;
   hipLaunchKernelGGL(rowstream_bf16_kernel, dim3((unsigned)rows), dim3(SK_NT), 0, s, a);
   return hipGetLastError();
 }

@@ -122,3 +122,19 @@ def test_scaled_logit_by_fp64_reciprocal_equals_fp32_division(fmt):
             got = (x.astype(np.float64) * (1.0 / np.float64(T32))).astype(np.float32)
             same = (want == got) | (np.isnan(want) & np.isnan(got))
             assert same.all(), (fmt, T, x[~same][:4], want[~same][:4], got[~same][:4])
+
+
+def test_fp32_quotient_by_fp64_reciprocal():
+    """The kernels evaluate p = e / z (and p / totf) as fl32(fl64(e) * fl64(1/z)):
+    equal to the correctly rounded fp32 quotient for fp32 operands (the exact
+    quotient of two 24-bit significands is never within 2^-52 of an fp32
+    rounding midpoint). Checked on random, denormal and edge operands."""
+    rs = np.random.RandomState(11)
+    e = np.concatenate([rs.uniform(0, 1, 400000), np.exp(rs.uniform(-104, 0, 400000)),
+                        [1.0, 2.0 ** -149, 2.0 ** -126, 0.5, 1.0 - 2.0 ** -24]]).astype(np.float32)
+    z = np.concatenate([rs.uniform(1, 3, 400000), np.exp(rs.uniform(0, 12, 400000)),
+                        [1.0, 3.0, 1.0 + 2.0 ** -23, 7.0, 151936.0]]).astype(np.float32)
+    with np.errstate(all="ignore"):
+        want = e / z
+        got = (e.astype(np.float64) * (1.0 / z.astype(np.float64))).astype(np.float32)
+    assert np.array_equal(want, got)
