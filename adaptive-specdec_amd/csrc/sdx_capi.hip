@@ -369,11 +369,14 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
     a.zero = counters; a.nzero = batch;
     a.rank_acc = dtype == SDX_BF16 ? rank_acc : nullptr;
     if (int e = row_stats16(dtype, a, rows, s)) return e;
-    if (dtype == SDX_BF16)
+    // bf16: drafted tokens the row kernel could not rank (a tie group of several
+    // values) are ranked by the draw's accept chain; the statistics-only call
+    // (and drafts too long for the one-wave chain) complete them with the rank kernel
+    if (dtype == SDX_BF16 && (stats_only || 2 * (int64_t)k + 1 > 64))
       if (int e = hip_status(sdx::launch_rank_bf16(a, rows, s), "rank_bf16")) return e;
   }
   if (stats_only) return SDX_OK;
-  sdx::AcceptArgs aa{st, batch, k, u_accept, u_final, active, jobs, n_acc, flags};
+  sdx::AcceptArgs aa{st, batch, k, u_accept, u_final, active, jobs, n_acc, flags, draft_ids};
   if (dtype == SDX_F32) {
     sdx::RowSourceF32 src{dn, vocab, dn, vocab, rows, (vocab % 4) == 0};
     return hip_status(sdx::launch_draw_probs(src, &aa, jobs, batch, vocab, recs,

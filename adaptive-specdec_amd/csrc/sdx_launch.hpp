@@ -60,6 +60,7 @@ struct AcceptArgs {
   SampleJob* jobs;        // [batch]
   int64_t* n_acc;
   uint8_t* flags;
+  const int64_t* draft_ids;  // [batch, k] (16-bit rows: ranks of flagged drafted tokens)
 };
 
 // Partial sums of one draw over one chunk of ids, before the member ranks of

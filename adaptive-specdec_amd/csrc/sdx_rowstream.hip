@@ -27,7 +27,8 @@
 // reductions cost one barrier each (partials go to alternating LDS slots).
 // The index cut inside the tie group is left to the consumers, which count
 // group members in id order as they stream the rows they need; a drafted
-// token inside its row's group is ranked by the rank kernel.
+// token inside its row's group is ranked here when the group is its own value
+// alone, else by the accept chain of the draw (or the rank kernel).
 //
 // x / T is evaluated as fl32(fl64(x) * fl64(1 / T)). For a 16-bit x (at most
 // 11 significant bits) and fp32 T this equals the correctly rounded fp32
@@ -339,6 +340,14 @@ rowstream_bf16_kernel(RowStatArgs a) {
   // it streams lets all three stream side by side instead of this one last.
   if ((int64_t)blockIdx.x >= a.late_block) __builtin_amdgcn_s_setprio(3);
   uint32_t omx = 0;
+  // The drafted token's member rank, when its tie group turns out to be its own
+  // value alone: equal codes before it. The histogram is read at a barrier
+  // just before the stream iteration holding the token (every earlier element
+  // is counted there); that iteration's elements before it are counted by hand.
+  const bool has_g = gid >= 0 && gid < V;
+  const uint32_t cg = has_g ? (uint32_t)ptr[gid] : 0u;
+  const int bin_g = sk_bin_of_key(key_of_code16(cg));
+  uint32_t snap = 0, pre = 0;  // pre: per thread, equal codes in the held iteration
   {
     // raw buffer loads: per-lane offset tid * 16 stays in a register, the
     // iteration offset is scalar; loads past the row read zeros (unused)
@@ -350,6 +359,22 @@ rowstream_bf16_kernel(RowStatArgs a) {
         __builtin_amdgcn_make_buffer_rsrc((void*)ptr, (short)0, (int)(n4 * 16u), 0x00020000);
     const uint32_t voff = (uint32_t)tid * 16u;
     char* const hb = reinterpret_cast<char*>(hist);
+    const uint32_t it_g = has_g ? (uint32_t)((gid >> 3) / kStep) : 0xFFFFFFFFu;
+    auto at_token = [&](const uint4 (&d)[U], uint32_t it) {  // before processing iteration it
+      if (it != it_g) return;  // uniform
+      __syncthreads();
+      snap = hist[bin_g];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t e0 = ((int64_t)it * kStep + (uint32_t)u * SK_NT + (uint32_t)tid) * 8;
+        const uint32_t wd[4] = {d[u].x, d[u].y, d[u].z, d[u].w};
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const uint32_t c = (t & 1) ? wd[t >> 1] >> 16 : wd[t >> 1] & 0xFFFFu;
+          pre += (e0 + t < gid && c == cg) ? 1u : 0u;
+        }
+      }
+    };
     auto load = [&](uint4 (&d)[U], uint32_t it) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -381,19 +406,27 @@ rowstream_bf16_kernel(RowStatArgs a) {
       uint4 A[U], B[U];
       load(A, 0);
       for (uint32_t it = 0;; it += 2) {  // uniform control flow
+        at_token(A, it);
         if (it + 1 >= iters) { proc_last(A, it); break; }
         load(B, it + 1);
         proc_all(A);
+        at_token(B, it + 1);
         if (it + 2 >= iters) { proc_last(B, it + 1); break; }
         load(A, it + 2);
         proc_all(B);
       }
     }
+    if (has_g && it_g >= iters) {  // the token among the last V % 8 elements
+      __syncthreads();
+      snap = hist[bin_g];
+    }
     const int64_t t0 = (int64_t)n4 * 8;  // the last V % 8 elements, one per thread
     if (tid < V - t0) {
-      const uint32_t o = 4u * (uint32_t)sk_bin_of_key(key_of_code16(ptr[t0 + tid]));
+      const uint32_t c = ptr[t0 + tid];
+      const uint32_t o = 4u * (uint32_t)sk_bin_of_key(key_of_code16(c));
       omx = max2(omx, o);
       atomicAdd(reinterpret_cast<uint32_t*>(hb + o), 1u);
+      if (has_g && it_g >= iters && t0 + tid < gid && c == cg) ++pre;
     }
   }
   __builtin_amdgcn_s_setprio(0);
@@ -475,6 +508,7 @@ rowstream_bf16_kernel(RowStatArgs a) {
   // (sum c <= V < 2^31 keeps both below 2^63). Thread t takes bins bmax - t - j*SK_NT,
   // so the first rounds cover the top bins and leave their exp values in etop.
   float zf;
+  uint32_t pre_all = 0;  // equal codes before the drafted token (when has_g)
   {
     uint64_t slo = 0, shi = 0;
     for (int b = bmax - tid, j = 0; b >= 1; b -= SK_NT, ++j) {
@@ -487,7 +521,8 @@ rowstream_bf16_kernel(RowStatArgs a) {
         shi += (uint64_t)c * (uint32_t)(f >> 32);
       }
     }
-    const Red4 zr = blk_red<kOpSum64, kOpSum64>(slo, shi, 0, 0, L.red, rs);
+    const Red4 zr = blk_red<kOpSum64, kOpSum64, kOpSum32>(slo, shi, pre, 0, L.red, rs);
+    pre_all = (uint32_t)zr.v[2];
     U128 z = u128_add(U128{zr.v[0], 0}, U128{zr.v[1] << 32, zr.v[1] >> 32});
     if (below_mass) z = u128_add(z, below_sum(ptr, V, below_lo, invT, m, 1.0f, L.red, rs));
     zf = rn32_u128(z);  // every thread, same value
@@ -694,12 +729,19 @@ rowstream_bf16_kernel(RowStatArgs a) {
   // depends on the token's member rank (members with lower ids): the rank
   // kernel counts it, spread over many blocks, and sets pgather.
   float pg = 0.0f;
-  if (gid >= 0 && gid < V) {
-    const int32_t kk = (int32_t)key_of_code16(ptr[gid]);
+  if (has_g) {
+    const int32_t kk = (int32_t)key_of_code16(cg);
     bool kept = kk >= klo;
     if (kept && kk >= glo && kk <= ghi) {
-      if (rstar <= 0) kept = false;
-      else if (rstar < gcount) { kept = false; rflags |= kRowRank; }
+      if (rstar <= 0) {
+        kept = false;
+      } else if (rstar < gcount) {
+        // a single-value group whose bin holds that value alone: its member rank
+        // is the count of equal codes before the token; otherwise the draw ranks it
+        const bool one = glo == ghi && bin_g >= 1 && bin_g <= 2 * SK_WIN + 1 && bin_g != SK_BIN_ZERO;
+        if (one) kept = (int32_t)(snap + pre_all) < rstar;
+        else { kept = false; rflags |= kRowRank; }
+      }
     }
     if (kept) pg = exp_det(sk_d((uint32_t)kk, invT, m)) / zf / totf;
   }

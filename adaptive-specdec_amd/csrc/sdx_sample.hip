@@ -819,8 +819,9 @@ struct Draw16Args {
 // RowStats of its 2k+1 rows (2k+1 <= 64): lane i holds row i (target
 // positions 0..k, then the k draft rows). The draw's RowStats go to st[0] (p)
 // and st[1] (q, for a residual draw).
-__device__ inline int64_t chain16_wave(const AcceptArgs& a, int64_t b, SampleJob* job,
-                                       uint32_t* fl_out, RowStat* st) {
+template <int FMT>
+__device__ inline int64_t chain16_wave(const AcceptArgs& a, const Eval16<FMT>& ev, int64_t b,
+                                       SampleJob* job, uint32_t* fl_out, RowStat* st) {
   const int lane = threadIdx.x & (kWave - 1);
   const int k = a.k;
   const int64_t trow0 = b * (k + 1), drow0 = a.batch * (k + 1) + b * k;
@@ -834,6 +835,30 @@ __device__ inline int64_t chain16_wave(const AcceptArgs& a, int64_t b, SampleJob
   const float u = lane < k ? a.u_accept[b * k + lane] : 2.0f;
   const float uf = a.u_final[b];
   const bool alive = a.active ? a.active[b] != 0 : true;
+  // drafted tokens the row kernel left unranked (their tie group spans several
+  // values; rare): the wave counts the group members before the token
+  uint64_t todo = __ballot(lane < nr && lane != k && (w3.x & kRowRank) != 0);
+  while (todo) {  // uniform
+    const int l = __ffsll((unsigned long long)todo) - 1;
+    todo &= todo - 1;
+    const int i = l < k ? l : l - k - 1;  // draft position of that row
+    const int64_t row = l <= k ? trow0 + l : drow0 + i;
+    const uint16_t* ptr = row < ev.split ? ev.base + row * ev.ld : ev.base2 + (row - ev.split) * ev.ld2;
+    const int64_t gid = a.draft_ids[b * k + i];
+    const int32_t glo = (int32_t)rdlane(w1.z, l), ghi = (int32_t)rdlane(w1.w, l);
+    uint32_t cnt = 0;
+    for (int64_t e = lane; e < gid; e += kWave) {
+      const int32_t kk = (int32_t)key_of_code16(ptr[e]);
+      cnt += (kk >= glo && kk <= ghi) ? 1u : 0u;
+    }
+    cnt = wave_sum_u32(cnt);
+    const int32_t rstar = (int32_t)rdlane(w2.x, l);
+    float v = 0.0f;
+    if ((int32_t)cnt < rstar)
+      v = val16_exp<FMT>(ptr[gid], ev.T, __uint_as_float(rdlane(w0.x, l)),
+                         __uint_as_float(rdlane(w0.y, l)), __uint_as_float(rdlane(w0.z, l)));
+    if (lane == l) w0.w = __float_as_uint(v);
+  }
   const float pg = __uint_as_float(w0.w);                          // RowStat::pgather
   const float qx = __shfl(pg, min(lane + k + 1, kWave - 1), kWave);  // its draft row's
   bool ok = true, near = false;
@@ -1137,7 +1162,7 @@ draw16_kernel(Draw16Args<FMT> a) {
     uint32_t fl;
     int64_t n;
     if (2 * a.acc.k + 1 <= kWave) {
-      n = chain16_wave(a.acc, j, &jb, &fl, s_st);
+      n = chain16_wave<FMT>(a.acc, ev, j, &jb, &fl, s_st);
     } else {  // long drafts: the generic chain, then the two RowStats word by word
       n = accept_chain_wave(a.acc, j, &jb, &fl);
       if (lane < 32) {

@@ -275,3 +275,35 @@ def test_rejection_sample_large_tie_groups(T, tp):
     assert np.array_equal(n.cpu().numpy(), rn)
     assert np.array_equal(y.cpu().numpy(), ry)
     assert np.array_equal(f.cpu().numpy(), rf)
+
+
+def _tiny_tie_rows(n, V, rng):
+    """Rows of ten logits 3.0 and the rest tiny values (|x| < 2^-24, many bf16
+    codes) that share one probability: one boundary tie group of many values."""
+    x = (rng.standard_normal((n, V)) * 1e-9).astype(np.float32)
+    x[:, ::7] = 0.0
+    x[:, 1::11] = -0.0
+    x[:, :10] = 3.0
+    return x
+
+
+@pytest.mark.parametrize("T,tp", [(1.0, 0.5), (1.0, 0.8)])
+def test_rejection_sample_multivalue_tie_group_ranks(T, tp):
+    """Drafted tokens inside a partial boundary tie group spanning many values
+    (the merged tiny-value bin): their member ranks come from the accept chain."""
+    B, k, V = 4, 2, 4096
+    rng = np.random.default_rng(9)
+    tgt_np = _tiny_tie_rows(B * (k + 1), V, rng).reshape(B, k + 1, V)
+    drf_np = _tiny_tie_rows(B * k, V, rng).reshape(B, k, V)
+    tgt = torch.tensor(tgt_np, device=DEV).to(torch.bfloat16)
+    drf = torch.tensor(drf_np, device=DEV).to(torch.bfloat16)
+    ids = torch.tensor(rng.integers(10, V, (B, k)), device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(12)
+    ua = uniforms((B, k), g, DEV) * 0.5
+    uf = uniforms((B,), g, DEV)
+    n, y, f = S.rejection_sample(tgt, drf, ids, ua, uf, temperature=T, top_p=tp)
+    rn, ry, rf = O.rejection_sample(_np(tgt), _np(drf), ids.cpu().numpy(), _np(ua), _np(uf),
+                                    T, tp, 0)
+    assert np.array_equal(n.cpu().numpy(), rn)
+    assert np.array_equal(y.cpu().numpy(), ry)
+    assert np.array_equal(f.cpu().numpy(), rf)
