@@ -277,6 +277,8 @@ size_t sdx_verify_workspace(int64_t batch, int32_t k, int64_t vocab, int dtype) 
   const int64_t rows = batch * (2 * (int64_t)k + 1);
   transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jb, &rc, &ct, &ra);
   c.take<int64_t>(batch * ((int64_t)k + 1));  // greedy argmax
+  // rows split over blocks (counters that stay zero between calls, part histograms)
+  c.take<uint8_t>(dtype == SDX_BF16 ? sdx::rowstream_split_bytes(rows, vocab) : 0);
   return c.used;
 }
 
@@ -334,6 +336,8 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
   const int64_t rows = ntgt + ndrf;
   transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jobs, &recs, &counters, &rank_acc);
   int64_t* am = c.take<int64_t>(ntgt);
+  const size_t split_bytes = dtype == SDX_BF16 ? sdx::rowstream_split_bytes(rows, vocab) : 0;
+  uint8_t* split_ws = c.take<uint8_t>(split_bytes);
   if (sw.greedy) {
     // one-hot p: only the target argmax matters (see sdx_verify_greedy)
     const bool vec = aligned16(target_logits) && (vocab % (dtype == SDX_F32 ? 4 : 8)) == 0;
@@ -368,6 +372,8 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
     a.stats = st; a.tables = tb;
     a.zero = counters; a.nzero = batch;
     a.rank_acc = dtype == SDX_BF16 ? rank_acc : nullptr;
+    a.split_ws = split_ws;
+    a.split_bytes = split_bytes;
     if (int e = row_stats16(dtype, a, rows, s)) return e;
     // bf16: drafted tokens the row kernel could not rank (a tie group of several
     // values) are ranked by the draw's accept chain; the statistics-only call

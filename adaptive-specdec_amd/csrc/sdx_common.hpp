@@ -81,6 +81,34 @@ __device__ __forceinline__ float exp_det(float d) {
   return (float)ldexp(p, (int)k);
 }
 
+// exp_det without the early exit: the same value, 0 below -104 (and for NaN)
+// by a final select, so that independent evaluations can interleave.
+__device__ __forceinline__ float exp_det_sel(float d) {
+#pragma clang fp contract(off)
+  const double kInvLn2 = 0x1.71547652b82fep+0;
+  const double kLn2Hi = 0x1.62e42fee00000p-1;
+  const double kLn2Lo = 0x1.a39ef35793c76p-33;
+  const double dd = (double)fmaxf(d, -105.0f);
+  const double k = rint(dd * kInvLn2);
+  const double r = (dd - k * kLn2Hi) - k * kLn2Lo;
+  double p = 0x1.6124613a86d09p-33;
+  p = p * r + 0x1.1eed8eff8d898p-29;
+  p = p * r + 0x1.ae64567f544e4p-26;
+  p = p * r + 0x1.27e4fb7789f5cp-22;
+  p = p * r + 0x1.71de3a556c734p-19;
+  p = p * r + 0x1.a01a01a01a01ap-16;
+  p = p * r + 0x1.a01a01a01a01ap-13;
+  p = p * r + 0x1.6c16c16c16c17p-10;
+  p = p * r + 0x1.1111111111111p-7;
+  p = p * r + 0x1.5555555555555p-5;
+  p = p * r + 0x1.5555555555555p-3;
+  p = p * r + 0x1.0000000000000p-1;
+  p = p * r + 0x1.0000000000000p+0;
+  p = p * r + 0x1.0000000000000p+0;
+  const float e = (float)ldexp(p, (int)k);
+  return d >= -104.0f ? e : 0.0f;
+}
+
 // ---------------------------------------------------------------- fixed point
 // floor(x * 2^62) for fp32 x in [0, 1] (branch-free: both shifts, one select).
 __device__ __forceinline__ uint64_t fixed62(float x) {

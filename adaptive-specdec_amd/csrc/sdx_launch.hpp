@@ -24,6 +24,16 @@ struct RowStatArgs {
   uint64_t* rank_acc;  // [rows] rank accumulators, cleared by the row kernel, or null
   int64_t late_block;  // bf16 streaming kernel: blocks from here stream at raised wave
                        // priority (set by launch_rowstream_bf16)
+  // bf16 streaming kernel, rows split over several blocks (set by launch_rowstream_bf16
+  // from split_ws / split_bytes): blocks [0, nwhole) take whole rows, the rows after
+  // nwhole are taken by nparts blocks each, the last of which to finish merges them
+  uint8_t* split_ws;   // caller region: arrival counters (zero between launches), then
+  size_t split_bytes;  // the parts' packed histograms; null / too small: no split
+  int64_t nwhole;
+  int32_t nparts;
+  int32_t xcd_group;  // a row's parts on blocks of one XCD (block index mod 8)
+  uint32_t* split_cnt;
+  uint8_t* split_parts;
 };
 
 struct F32Args {
@@ -108,6 +118,9 @@ int rowstat16_nslot(int64_t V);
 hipError_t launch_rowstat16(int fmt, const RowStatArgs& a, int64_t rows, hipStream_t s);
 // sdx_rowstream.hip
 hipError_t launch_rowstream_bf16(const RowStatArgs& a, int64_t rows, hipStream_t s);
+// bytes of RowStatArgs::split_ws that let launch_rowstream_bf16 split rows over
+// several blocks on the current device (0: it would not split)
+size_t rowstream_split_bytes(int64_t rows, int64_t V);
 // sdx_rank.hip: pgather of drafted tokens inside a partial tie group (after rowstream)
 hipError_t launch_rank_bf16(const RowStatArgs& a, int64_t rows, hipStream_t s);
 // sdx_f32.hip

@@ -58,6 +58,15 @@ constexpr int SK_BIN_ZERO = SK_WIN + 1;
 constexpr int SK_BIN_EXC = 2 * SK_WIN + 2;
 constexpr int SK_NB = 2 * SK_WIN + 4;     // bins, the last one (SK_NB - 1) unused
 constexpr int SK_ETOP = 1024;             // exp values cached for the top bins
+constexpr int SK_ZQ = 3 * kWave;          // per-wave queue of occupied bins (normaliser)
+// Rows split over several blocks: each part publishes its histogram as u16
+// counts, 8 bins per 16-byte chunk, then a header chunk (its largest bin
+// offset, its count of equal-bin elements before the drafted token).
+constexpr int SK_SPLIT_CHUNKS = (SK_NB + 7) / 8;
+constexpr uint32_t SK_SPLIT_BYTES = ((SK_SPLIT_CHUNKS + 1) * 16 + 63) / 64 * 64;
+constexpr int64_t SK_PART_MAX = 65535;          // logits per part (u16 counts)
+constexpr int64_t SK_PART_MIN_GROUPS = 1024;    // 8-logit groups per part, at least
+constexpr uint32_t SK_SC1 = 16;  // buffer-op cache policy: coherent across the device
 
 __device__ __forceinline__ int sk_bin_of_key(uint32_t k) {
   const uint32_t c1 = min(k > SK_NEG_LO - 1 ? k - (SK_NEG_LO - 1) : 0u, (uint32_t)SK_WIN + 1);
@@ -294,11 +303,92 @@ __device__ U128 below_sum(const uint16_t* __restrict__ ptr, int64_t V, uint32_t 
   return u128_add(U128{r.v[0], 0}, U128{r.v[1] << 32, r.v[1] >> 32});
 }
 
+// Rows split over P blocks. Every part publishes its histogram (u16 counts) and
+// header with device-coherent stores, waits for them, then counts itself in on
+// the row's arrival counter; the part that arrives last adds the other parts
+// into its LDS histogram, their largest offsets into *omx and their token
+// counts into *cp, resets the counter to zero and returns true. The others
+// return false (and leave the kernel).
+typedef uint32_t sk_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bool split_merge(uint32_t* __restrict__ cnt, uint8_t* parts, int P,
+                                            int64_t sidx, int part, uint32_t* hist,
+                                            uint32_t* omx, uint32_t* cp, int32_t* flag) {
+  const int tid = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      parts + sidx * P * (int64_t)SK_SPLIT_BYTES, (short)0, (int)(P * SK_SPLIT_BYTES), 0x00020000);
+  const uint32_t mine = (uint32_t)part * SK_SPLIT_BYTES;
+  for (int c = tid; c < SK_SPLIT_CHUNKS; c += SK_NT) {
+    const uint4 h0 = *reinterpret_cast<const uint4*>(hist + 8 * c);
+    const uint4 h1 = *reinterpret_cast<const uint4*>(hist + 8 * c + 4);
+    const sk_u32x4 w = {h0.x | (h0.y << 16), h0.z | (h0.w << 16), h1.x | (h1.y << 16),
+                        h1.z | (h1.w << 16)};
+    __builtin_amdgcn_raw_buffer_store_b128(w, rsrc, c * 16, (int)mine, SK_SC1);
+  }
+  if (tid == 0) {
+    const sk_u32x4 h = {*omx, *cp, 0u, 0u};
+    __builtin_amdgcn_raw_buffer_store_b128(h, rsrc, SK_SPLIT_CHUNKS * 16, (int)mine, SK_SC1);
+  }
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // gfx9 encoding: vmcnt(0) (stores done)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(cnt + sidx, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = prev == (uint32_t)(P - 1);
+    if (last) __hip_atomic_store(cnt + sidx, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    flag[0] = last ? 1 : 0;
+  }
+  __syncthreads();
+  if (!flag[0]) return false;
+  // thread t owns chunks t, t + SK_NT, t + 2 SK_NT (SK_SPLIT_CHUNKS <= 3 SK_NT)
+  static_assert(SK_SPLIT_CHUNKS <= 3 * SK_NT, "chunks per thread");
+  uint32_t acc[3][8];
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[k][t] = 0u;
+  uint32_t om = *omx, cc = *cp;
+  for (int o = 0; o < P; ++o) {  // uniform
+    if (o == part) continue;
+    const int so = o * (int)SK_SPLIT_BYTES;
+    sk_u32x4 x[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {  // clamped: every thread loads, unowned chunks unused
+      const int c = min(tid + k * SK_NT, SK_SPLIT_CHUNKS - 1);
+      x[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, c * 16, so, SK_SC1);
+    }
+    const sk_u32x4 h = __builtin_amdgcn_raw_buffer_load_b128(rsrc, SK_SPLIT_CHUNKS * 16, so, SK_SC1);
+    om = max(om, h[0]);
+    cc += h[1];
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[k][2 * j] += x[k][j] & 0xFFFFu;
+        acc[k][2 * j + 1] += x[k][j] >> 16;
+      }
+  }
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const int c = tid + k * SK_NT;
+    if (c < SK_SPLIT_CHUNKS) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) hist[8 * c + t] += acc[k][t];
+    }
+  }
+  __syncthreads();
+  *omx = om;
+  *cp = cc;
+  return true;
+}
+
 // All LDS of the kernel in one object, histogram first (LDS address 0, so the
 // streaming atomics address it by byte offset alone).
 struct SkLds {
-  uint32_t hist[SK_NB];
+  uint32_t hist[SK_SPLIT_CHUNKS * 8];  // SK_NB bins, zero padding to whole chunks
   float etop[SK_ETOP];  // exp values of the top SK_ETOP bins (bmax - i); occupied ones only
+  uint32_t zq[SK_NW][SK_ZQ];  // per-wave queues of occupied bins for the normaliser
   SkRed red;
   int32_t i32[12];
   uint64_t x64[2];
@@ -311,7 +401,23 @@ rowstream_bf16_kernel(RowStatArgs a) {
   int rs = 0;
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
-  const int64_t row = blockIdx.x;
+  // the row, and the part of it when rows after nwhole are split over nparts blocks
+  const int64_t blk = blockIdx.x;
+  const int P = a.nparts;
+  int64_t row = blk, sidx = -1;
+  int part = -1;
+  if (blk >= a.nwhole) {
+    const int64_t q = blk - a.nwhole;
+    if (a.xcd_group) {
+      const int64_t t = q >> 3;
+      sidx = (t / P) * 8 + (q & 7);
+      part = (int)(t % P);
+    } else {
+      sidx = q / P;
+      part = (int)(q % P);
+    }
+    row = a.nwhole + sidx;
+  }
   const int g = row < a.nrows[0] ? 0 : 1;
   const int64_t r = g ? row - a.nrows[0] : row;
   const uint16_t* __restrict__ ptr = a.base[g] + r * a.ld[g];
@@ -327,10 +433,10 @@ rowstream_bf16_kernel(RowStatArgs a) {
   const int64_t V = a.V;
   RowStat* st_out = a.stats + row;
   float* tbl_out = a.tables + row * kTbl;
-  if (tid == 0 && row < a.nzero) a.zero[row] = 0u;
-  if (tid == 0 && a.rank_acc) a.rank_acc[row] = 0ull;
+  if (tid == 0 && part <= 0 && row < a.nzero) a.zero[row] = 0u;
+  if (tid == 0 && part <= 0 && a.rank_acc) a.rank_acc[row] = 0ull;
 
-  for (int b = tid; b < SK_NB; b += SK_NT) hist[b] = 0u;
+  for (int b = tid; b < SK_SPLIT_CHUNKS * 8; b += SK_NT) hist[b] = 0u;
   __syncthreads();
 
   // ---- 1. stream the row: 16-byte loads two stages deep, packed codes ->
@@ -348,18 +454,30 @@ rowstream_bf16_kernel(RowStatArgs a) {
   const uint32_t cg = has_g ? (uint32_t)ptr[gid] : 0u;
   const int bin_g = sk_bin_of_key(key_of_code16(cg));
   uint32_t snap = 0, pre = 0;  // pre: per thread, equal codes in the held iteration
+  // this block's range: 8-element groups [g0, g1), then the last V % 8 elements
+  // when it holds the row's end
+  const uint32_t n4_all = (uint32_t)(V >> 3);  // whole 8-element groups (V < 2^31)
+  uint32_t g0 = 0, g1 = n4_all;
+  if (part >= 0) {
+    g0 = (uint32_t)((int64_t)n4_all * part / P);
+    g1 = (uint32_t)((int64_t)n4_all * (part + 1) / P);
+  }
+  const bool has_tail = g1 == n4_all;
+  const int64_t gid_l = gid - (int64_t)g0 * 8;  // the token's place in the range
+  const bool g_in_groups = has_g && gid_l >= 0 && gid_l < (int64_t)(g1 - g0) * 8;
+  const bool g_in_tail = has_g && has_tail && gid >= (int64_t)n4_all * 8;
   {
     // raw buffer loads: per-lane offset tid * 16 stays in a register, the
-    // iteration offset is scalar; loads past the row read zeros (unused)
+    // iteration offset is scalar; loads past the range read zeros (unused)
     constexpr int U = 4;
     constexpr uint32_t kStep = (uint32_t)SK_NT * U;
-    const uint32_t n4 = (uint32_t)(V >> 3);  // whole 8-element groups (V < 2^31)
+    const uint32_t n4 = g1 - g0;
     const uint32_t iters = (n4 + kStep - 1) / kStep;
-    const __amdgpu_buffer_rsrc_t rsrc =
-        __builtin_amdgcn_make_buffer_rsrc((void*)ptr, (short)0, (int)(n4 * 16u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(ptr + (int64_t)g0 * 8), (short)0, (int)(n4 * 16u), 0x00020000);
     const uint32_t voff = (uint32_t)tid * 16u;
     char* const hb = reinterpret_cast<char*>(hist);
-    const uint32_t it_g = has_g ? (uint32_t)((gid >> 3) / kStep) : 0xFFFFFFFFu;
+    const uint32_t it_g = g_in_groups ? (uint32_t)((gid_l >> 3) / kStep) : 0xFFFFFFFFu;
     auto at_token = [&](const uint4 (&d)[U], uint32_t it) {  // before processing iteration it
       if (it != it_g) return;  // uniform
       __syncthreads();
@@ -371,7 +489,7 @@ rowstream_bf16_kernel(RowStatArgs a) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
           const uint32_t c = (t & 1) ? wd[t >> 1] >> 16 : wd[t >> 1] & 0xFFFFu;
-          pre += (e0 + t < gid && c == cg) ? 1u : 0u;
+          pre += (e0 + t < gid_l && c == cg) ? 1u : 0u;
         }
       }
     };
@@ -416,22 +534,33 @@ rowstream_bf16_kernel(RowStatArgs a) {
         proc_all(B);
       }
     }
-    if (has_g && it_g >= iters) {  // the token among the last V % 8 elements
+    if (g_in_tail) {  // the token among the last V % 8 elements
       __syncthreads();
       snap = hist[bin_g];
     }
-    const int64_t t0 = (int64_t)n4 * 8;  // the last V % 8 elements, one per thread
-    if (tid < V - t0) {
+    const int64_t t0 = (int64_t)n4_all * 8;  // the last V % 8 elements, one per thread
+    if (has_tail && tid < V - t0) {
       const uint32_t c = ptr[t0 + tid];
       const uint32_t o = 4u * (uint32_t)sk_bin_of_key(key_of_code16(c));
       omx = max2(omx, o);
       atomicAdd(reinterpret_cast<uint32_t*>(hb + o), 1u);
-      if (has_g && it_g >= iters && t0 + tid < gid && c == cg) ++pre;
+      if (g_in_tail && t0 + tid < gid && c == cg) ++pre;
     }
   }
   __builtin_amdgcn_s_setprio(0);
   // (the reduction's barrier also completes the histogram)
-  const int bmx = (int)(blk_max_u32(max(omx & 0xFFFFu, omx >> 16), L.red, rs) >> 2);
+  uint32_t omx_b = blk_max_u32(max(omx & 0xFFFFu, omx >> 16), L.red, rs);
+  if (part >= 0) {  // uniform: publish this part; the last part of the row to finish goes on
+    // its count of equal-bin elements before the token
+    uint32_t cp = 0;
+    if (g_in_groups || g_in_tail) cp = snap + blk_sum_u32(pre, L.red, rs);
+    else if (has_g && gid >= (int64_t)g1 * 8) cp = hist[bin_g];
+    if (!split_merge(a.split_cnt, a.split_parts, P, sidx, part, hist, &omx_b, &cp, L.i32 + 11))
+      return;
+    snap = cp;  // every part's count, this one's included
+    pre = 0;
+  }
+  const int bmx = (int)(omx_b >> 2);
   uint32_t kmax;
   if (bmx >= 1 && bmx <= 2 * SK_WIN + 1 && bmx != SK_BIN_ZERO) {
     kmax = bmx <= SK_WIN ? SK_NEG_LO + (uint32_t)(bmx - 1)
@@ -505,21 +634,55 @@ rowstream_bf16_kernel(RowStatArgs a) {
   auto e_of_bin = [&](int b) -> float { return exp_det(sk_d(bm.key_rep(b), invT, m)); };
 
   // ---- 3. exact normaliser: sum c * fixed62(e) as sum c * lo32 + 2^32 sum c * hi32
-  // (sum c <= V < 2^31 keeps both below 2^63). Thread t takes bins bmax - t - j*SK_NT,
-  // so the first rounds cover the top bins and leave their exp values in etop.
+  // (sum c <= V < 2^31 keeps both below 2^63). Thread t reads bins bmax - t - j*SK_NT;
+  // each wave queues its occupied bins as (bin << 18 | count) in LDS and
+  // evaluates them 128 at a time, two independent exp evaluations per lane
+  // (sparse stretches of the window cost no idle lanes). The top SK_ETOP bins'
+  // exp values stay in etop.
   float zf;
   uint32_t pre_all = 0;  // equal codes before the drafted token (when has_g)
   {
     uint64_t slo = 0, shi = 0;
-    for (int b = bmax - tid, j = 0; b >= 1; b -= SK_NT, ++j) {
-      const uint32_t c = hist[b];
-      if (c) {
-        const float e = e_of_bin(b);
-        if (j * SK_NT < SK_ETOP) L.etop[tid + j * SK_NT] = e;
-        const uint64_t f = fixed62(e);
-        slo += (uint64_t)c * (uint32_t)f;
-        shi += (uint64_t)c * (uint32_t)(f >> 32);
+    uint32_t* const q = L.zq[tid / kWave];
+    uint32_t qn = 0;  // wave-uniform
+    auto zterm2 = [&](uint32_t e0, uint32_t e1) {
+      const uint32_t c0 = e0 & 0x3FFFFu, c1 = e1 & 0x3FFFFu;
+      const int b0 = (int)(e0 >> 18), b1 = (int)(e1 >> 18);
+      const float x0 = exp_det_sel(sk_d(bm.key_rep(b0), invT, m));
+      const float x1 = exp_det_sel(sk_d(bm.key_rep(b1), invT, m));
+      if (c0 != 0 && bmax - b0 < SK_ETOP) L.etop[bmax - b0] = x0;
+      if (c1 != 0 && bmax - b1 < SK_ETOP) L.etop[bmax - b1] = x1;
+      const uint64_t f0 = fixed62(x0), f1 = fixed62(x1);
+      slo += (uint64_t)c0 * (uint32_t)f0 + (uint64_t)c1 * (uint32_t)f1;
+      shi += (uint64_t)c0 * (uint32_t)(f0 >> 32) + (uint64_t)c1 * (uint32_t)(f1 >> 32);
+    };
+    const int nround = bmax >= 1 ? (bmax - 1) / SK_NT + 1 : 0;
+    for (int j0 = 0; j0 < nround; j0 += 4) {
+      uint32_t cc[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int b = bmax - tid - SK_NT * (j0 + u);
+        cc[u] = b >= 1 ? hist[b] : 0u;
       }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int b = bmax - tid - SK_NT * (j0 + u);
+        const uint64_t mk = __ballot(cc[u] != 0);
+        const uint32_t below = __builtin_amdgcn_mbcnt_hi(
+            (uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u));
+        if (cc[u] != 0) q[qn + below] = ((uint32_t)b << 18) | cc[u];
+        qn += (uint32_t)__popcll(mk);
+        if (qn >= 2 * kWave) {  // uniform
+          const uint32_t e0 = q[qn - 2 * kWave + lane], e1 = q[qn - kWave + lane];
+          qn -= 2 * kWave;
+          zterm2(e0, e1);
+        }
+      }
+    }
+    if (qn > 0) {  // uniform: the rest, under 128 entries (0: no bin)
+      const uint32_t e0 = (uint32_t)lane < qn ? q[lane] : 0u;
+      const uint32_t e1 = (uint32_t)lane + kWave < qn ? q[lane + kWave] : 0u;
+      zterm2(e0, e1);
     }
     const Red4 zr = blk_red<kOpSum64, kOpSum64, kOpSum32>(slo, shi, pre, 0, L.red, rs);
     pre_all = (uint32_t)zr.v[2];
@@ -779,11 +942,60 @@ static int device_cus() {
   return cus[dev];
 }
 
+// Rows beyond the last whole multiple of the CU count are split into parts so
+// that every CU streams about the same number of bytes (576 rows on 256 CUs:
+// 512 whole rows, 64 rows in 4 parts). Parts hold at least SK_PART_MIN_GROUPS
+// groups and at most SK_PART_MAX logits; 0 parts: no split.
+static int split_layout(int64_t rows, int64_t V, int cus, int64_t* nwhole) {
+  *nwhole = rows;
+  if (cus <= 0 || rows <= 0) return 0;
+  const int64_t whole = rows / cus * cus, rest = rows - whole;
+  if (rest == 0) return 0;
+  const int64_t n4 = V >> 3;
+  int64_t p = cus / rest;
+  if (p > 8) p = 8;
+  if (p > n4 / SK_PART_MIN_GROUPS) p = n4 / SK_PART_MIN_GROUPS;
+  while (p >= 2 && p <= 8 && ((n4 + p - 1) / p) * 8 + 7 > SK_PART_MAX) ++p;
+  if (p < 2 || p > 8 || n4 / p < SK_PART_MIN_GROUPS) return 0;
+  *nwhole = whole;
+  return (int)p;
+}
+static size_t split_need(int64_t rows, int64_t nwhole, int p) {
+  if (p < 2) return 0;
+  const int64_t rest = rows - nwhole;
+  return ((size_t)rest * 4 + 255) / 256 * 256 + (size_t)rest * p * SK_SPLIT_BYTES;
+}
+
+size_t rowstream_split_bytes(int64_t rows, int64_t V) {
+  int64_t nwhole;
+  const int p = split_layout(rows, V, device_cus(), &nwhole);
+  return split_need(rows, nwhole, p);
+}
+
 hipError_t launch_rowstream_bf16(const RowStatArgs& args, int64_t rows, hipStream_t s) {
   RowStatArgs a = args;
   const int cus = device_cus();
   a.late_block = cus > 0 ? 2 * (int64_t)cus : INT64_MAX;
-  hipLaunchKernelGGL(rowstream_bf16_kernel, dim3((unsigned)rows), dim3(SK_NT), 0, s, a);
+  int64_t nwhole;
+  int p = split_layout(rows, a.V, cus, &nwhole);
+  if (p >= 2 && (!a.split_ws || a.split_bytes < split_need(rows, nwhole, p))) p = 0;
+  int64_t grid = rows;
+  if (p >= 2) {
+    const int64_t rest = rows - nwhole;
+    a.nwhole = nwhole;
+    a.nparts = p;
+    a.xcd_group = (nwhole % 8 == 0 && rest % 8 == 0) ? 1 : 0;
+    a.split_cnt = reinterpret_cast<uint32_t*>(a.split_ws);
+    a.split_parts = a.split_ws + ((size_t)rest * 4 + 255) / 256 * 256;
+    grid = nwhole + rest * p;
+  } else {
+    a.nwhole = rows;
+    a.nparts = 1;
+    a.xcd_group = 0;
+    a.split_cnt = nullptr;
+    a.split_parts = nullptr;
+  }
+  hipLaunchKernelGGL(rowstream_bf16_kernel, dim3((unsigned)grid), dim3(SK_NT), 0, s, a);
   return hipGetLastError();
 }
 

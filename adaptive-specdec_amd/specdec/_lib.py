@@ -107,4 +107,5 @@ def stream_of(t):
 
 
 def workspace(nbytes, device):
-    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+    # zero-filled: the verify workspace carries counters that calls leave at zero
+    return torch.zeros(max(int(nbytes), 1), dtype=torch.uint8, device=device)

@@ -92,7 +92,11 @@ int sdx_gather_prob(const float* probs, int64_t rows, int64_t vocab, int64_t ld,
  * Outputs: n_acc [batch] accepted drafts, y [batch] the token emitted after them
  * (residual draw at position n_acc, or the bonus draw from p_{k+1} when n_acc == k),
  * flags [batch] (sdx_flag bits). Emitted tokens of row b: draft_ids[b, :n_acc[b]] then y[b];
- * KV rows to drop: k - n_acc[b] (engine.py:310). */
+ * KV rows to drop: k - n_acc[b] (engine.py:310).
+ * Workspace: sized by sdx_verify_workspace for the current device. Zero-fill it once
+ * before its first call: with bf16 logits it carries arrival counters of rows split
+ * over several blocks, which every call leaves at zero. Calls that share a workspace
+ * must not overlap. */
 size_t sdx_verify_workspace(int64_t batch, int32_t k, int64_t vocab, int dtype);
 int sdx_verify(const void* target_logits, const void* draft_logits, int dtype,
                int64_t batch, int32_t k, int64_t vocab,

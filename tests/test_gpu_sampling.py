@@ -75,7 +75,8 @@ def test_to_probs_nonaligned_vocab():
     _assert_probs_equal(got, ref)
 
 
-@pytest.mark.parametrize("B,k,V", [(16, 4, 1000), (4, 4, 151936), (8, 1, 512), (6, 8, 4096)])
+@pytest.mark.parametrize("B,k,V", [(16, 4, 1000), (4, 4, 151936), (8, 4, 151936), (8, 1, 512),
+                                   (6, 8, 4096)])
 @pytest.mark.parametrize("T,tp,tk", [(0.8, 0.95, 0), (1.0, 1.0, 0), (0.7, 0.9, 50)])
 def test_rejection_sample_bf16(B, k, V, T, tp, tk):
     inp = verify_inputs(B, k, V, seed=B * 100 + k, device=DEV, temperature=T, top_p=tp, top_k=tk)
@@ -87,6 +88,24 @@ def test_rejection_sample_bf16(B, k, V, T, tp, tk):
     assert np.array_equal(n.cpu().numpy(), rn)
     assert np.array_equal(y.cpu().numpy(), ry)
     assert np.array_equal(f.cpu().numpy(), rf)
+
+
+@pytest.mark.parametrize("seed", [1000, 1001])
+def test_rejection_sample_bf16_b64_k4_v151936(seed):
+    """The full B=64, k=4, V=151936 verify (576 rows: 512 whole, 64 split over
+    blocks on a 256-CU device), twice on one workspace."""
+    B, k, V, T, tp = 64, 4, 151936, 0.8, 0.95
+    inp = verify_inputs(B, k, V, seed=seed, device=DEV, temperature=T, top_p=tp)
+    v = S.Verifier(B, k, V, torch.bfloat16, temperature=T, top_p=tp)
+    rn, ry, rf = O.rejection_sample(_np(inp["target"]), _np(inp["draft"]),
+                                    inp["draft_ids"].cpu().numpy(), _np(inp["u_accept"]),
+                                    _np(inp["u_final"]), T, tp, 0)
+    for _ in range(2):
+        n, y, f = v(inp["target"], inp["draft"], inp["draft_ids"], inp["u_accept"],
+                    inp["u_final"])
+        assert np.array_equal(n.cpu().numpy(), rn)
+        assert np.array_equal(y.cpu().numpy(), ry)
+        assert np.array_equal(f.cpu().numpy(), rf)
 
 
 def test_rejection_sample_active_and_fp32():
