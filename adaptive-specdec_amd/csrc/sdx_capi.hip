@@ -505,4 +505,49 @@ int sdx_kv_append_paged(void* pool, int64_t layer_stride, int64_t side_stride, c
                     "kv_append_paged");
 }
 
+// ------------------------------------------------------------------ verify attention
+int sdx_verify_attention_paged(const void* q, int dtype, int64_t batch, const int64_t* cu_q,
+                               int32_t max_q, int32_t num_q_heads, int32_t num_kv_heads,
+                               int32_t head_dim, const void* k_pool, const void* v_pool,
+                               int64_t num_blocks, int32_t block_size, const int32_t* block_table,
+                               int64_t max_blocks, const int64_t* kv_len, const int32_t* row_order,
+                               float scale, void* out, int32_t* error, sdx_stream_t stream) {
+  if (!q || !cu_q || !k_pool || !v_pool || !block_table || !kv_len || !out || batch < 0 ||
+      max_q < 1 || num_q_heads < 1 || num_kv_heads < 1 || num_blocks < 1 || block_size < 1 ||
+      max_blocks < 1 || !(scale > 0.0f))
+    return fail(SDX_EINVAL, "sdx_verify_attention_paged: bad arguments");
+  if (dtype != SDX_BF16 || head_dim != 128)
+    return fail(SDX_EUNSUPPORTED, "sdx_verify_attention_paged: bf16 with head_dim 128 only");
+  if (num_q_heads % num_kv_heads != 0)
+    return fail(SDX_EINVAL, "sdx_verify_attention_paged: query heads must be a multiple of KV heads");
+  const int32_t group = num_q_heads / num_kv_heads;
+  if ((int64_t)max_q * group > 64)
+    return fail(SDX_EUNSUPPORTED,
+                "sdx_verify_attention_paged: max_q * (query heads per KV head) must be <= 64 "
+                "(got %d * %d)", max_q, group);
+  if (!aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool) || !aligned16(out))
+    return fail(SDX_EINVAL, "sdx_verify_attention_paged: tensors must be 16-byte aligned");
+  if (batch == 0) return SDX_OK;
+  sdx::AttnArgs a = {};
+  a.q = (const uint16_t*)q;
+  a.cu_q = cu_q;
+  a.k_pool = (const uint16_t*)k_pool;
+  a.v_pool = (const uint16_t*)v_pool;
+  a.block_table = block_table;
+  a.kv_len = kv_len;
+  a.row_order = row_order;
+  a.batch = batch;
+  a.out = (uint16_t*)out;
+  a.error = error;
+  a.max_blocks = max_blocks;
+  a.num_blocks = num_blocks;
+  a.hq = num_q_heads;
+  a.hkv = num_kv_heads;
+  a.group = group;
+  a.bs = block_size;
+  a.max_q = max_q;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  return hip_status(sdx::launch_verify_attn(a, batch, (hipStream_t)stream), "verify_attn");
+}
+
 }  // extern "C"

@@ -158,6 +158,22 @@ hipError_t launch_onehot(const int64_t* am, int64_t rows, int64_t V, float* out,
 hipError_t launch_greedy_accept(const int64_t* am, int64_t batch, int32_t k, const int64_t* ids,
                                 const float* u_accept, const uint8_t* active, int64_t* n_acc,
                                 int64_t* y, uint8_t* flags, hipStream_t s);
+// sdx_attn.hip: multi-query verify attention over paged KV (bf16, head_dim 128)
+struct AttnArgs {
+  const uint16_t* q;        // [T, hq, 128] bf16
+  const int64_t* cu_q;      // [B + 1] query-row offsets
+  const uint16_t* k_pool;   // [num_blocks, bs, hkv * 128] bf16
+  const uint16_t* v_pool;
+  const int32_t* block_table;  // [B, max_blocks]
+  const int64_t* kv_len;    // [B] keys per row, the new positions included
+  const int32_t* row_order;  // [B] rows in launch order, or null (0 .. B-1)
+  uint16_t* out;            // [T, hq, 128] bf16
+  int32_t* error;           // set when a row's shape or pages are out of range
+  int64_t max_blocks, num_blocks, batch;
+  int32_t hq, hkv, group, bs, max_q;
+  float scale_log2;         // softmax scale * log2(e)
+};
+hipError_t launch_verify_attn(const AttnArgs& a, int64_t batch, hipStream_t s);
 // sdx_kv.hip
 hipError_t launch_kv_advance(int64_t* lengths, int64_t batch, int64_t q, hipStream_t s);
 hipError_t launch_kv_rollback(int64_t* lengths, int64_t batch, const int64_t* n, int32_t* error,

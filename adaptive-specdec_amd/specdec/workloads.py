@@ -8,10 +8,14 @@
 * greedy:  the same logits, draft ids equal to the target argmax with a given
            probability per position (else a different id).
 * kv:      per-row lengths, a shuffled block table, staged K/V vectors.
+* attn:    adaptive-k verify attention: per-row k from the closed-form
+           controller at a per-row acceptance estimate, context lengths, a
+           shuffled block table over one layer's paged K/V, queries.
 """
 import torch
 
-__all__ = ["zipf_logits", "uniforms", "verify_inputs", "greedy_inputs", "kv_inputs"]
+__all__ = ["zipf_logits", "uniforms", "verify_inputs", "greedy_inputs", "kv_inputs",
+           "attn_inputs"]
 
 
 def uniforms(shape, generator, device):
@@ -78,4 +82,39 @@ def kv_inputs(layers, B, q, kv_heads, head_dim, block_size, len_lo, len_hi, seed
         "lengths": lengths.to(device), "block_table": block_table.to(device),
         "staged": staged.to(device), "keep": keep.to(device), "num_blocks": num_blocks,
         "max_blocks": max_blocks,
+    }
+
+
+def attn_inputs(B, seed, device, ctx_lo=1024, ctx_hi=8192, hq=32, hkv=8, d=128, block_size=16,
+                alpha_lo=0.4, alpha_hi=0.9, c=0.1, k_max=8, dtype=torch.bfloat16):
+    """Adaptive-k verify attention of one layer: row b drafts k_b = best_k(alpha_b, c)
+    tokens (alpha_b ~ U(alpha_lo, alpha_hi)), so q_b = k_b + 1 new positions after
+    a context of ctx_b ~ U[ctx_lo, ctx_hi] keys. K/V ~ N(0, 1) in a paged pool
+    [num_blocks, block_size, hkv * d] behind a shuffled block table; q ~ N(0, 1)."""
+    from .controller import best_k
+    g = torch.Generator(device="cpu").manual_seed(int(seed))
+    alphas = torch.rand(B, generator=g) * (alpha_hi - alpha_lo) + alpha_lo
+    k = torch.tensor([best_k(float(a), c, k_max) for a in alphas], dtype=torch.int64)
+    qb = k + 1
+    ctx = torch.randint(ctx_lo, ctx_hi + 1, (B,), generator=g)
+    kv_len = ctx + qb
+    pages = (kv_len + block_size - 1) // block_size
+    max_blocks = int(pages.max())
+    num_blocks = int(pages.sum())
+    perm = torch.randperm(num_blocks, generator=g).to(torch.int32)
+    bt = torch.full((B, max_blocks), -1, dtype=torch.int32)
+    o = 0
+    for b in range(B):
+        bt[b, :int(pages[b])] = perm[o:o + int(pages[b])]
+        o += int(pages[b])
+    cu_q = torch.zeros(B + 1, dtype=torch.int64)
+    cu_q[1:] = torch.cumsum(qb, 0)
+    gd = torch.Generator(device=device).manual_seed(int(seed) + 1)
+    k_pool = torch.randn((num_blocks, block_size, hkv * d), generator=gd, device=device).to(dtype)
+    v_pool = torch.randn((num_blocks, block_size, hkv * d), generator=gd, device=device).to(dtype)
+    q = torch.randn((int(cu_q[-1]), hq, d), generator=gd, device=device).to(dtype)
+    return {
+        "q": q, "cu_q": cu_q.to(device), "k_pool": k_pool, "v_pool": v_pool,
+        "block_table": bt.to(device), "kv_len": kv_len.to(device), "max_q": int(qb.max()),
+        "k": k, "ctx": ctx, "hq": hq, "hkv": hkv, "d": d,
     }

@@ -9,7 +9,7 @@ logits with a Zipf head, draft = target + N(0,1), draft ids drawn from q) are
 resident in HBM; three input sets (525 MB, more than the 256 MB MALL) rotate so
 no step reads another step's bytes from cache.
 
-    python bench.py [--steps K] [--warmup W] [--workload verify|greedy|kv]
+    python bench.py [--steps K] [--warmup W] [--workload verify|greedy|kv|attn]
 
 Prints one JSON line: verified tokens/s (sum over rows of n_acc + 1 per
 step), the roofline of the dominant kernel (row statistics: algorithmic
@@ -295,12 +295,53 @@ def bench_kv(args, torch):
             "cpu_baseline": None}
 
 
+def bench_attn(args, torch):
+    """Adaptive-k verify attention, one layer: B=128 rows with k_b = best_k(alpha_b, 0.1),
+    alpha_b ~ U(0.4, 0.9), contexts ~ U[1024, 8192], 32 query / 8 KV heads of 128,
+    paged bf16 KV (block 16). HBM roofline: every visible key and value read once."""
+    from specdec.attention import verify_attention_paged
+    from specdec.workloads import attn_inputs
+    dev = "cuda:0"
+    B = 128
+    inp = attn_inputs(B, seed=5, device=dev)
+    out = torch.empty_like(inp["q"])
+    call = lambda: verify_attention_paged(inp["q"], inp["cu_q"], inp["k_pool"], inp["v_pool"],  # noqa: E731
+                                          inp["block_table"], inp["kv_len"], inp["max_q"],
+                                          out=out)
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    g = capture(call, torch)
+    ms = timed_graphs([g], args.steps, torch)
+    kv_tokens = int(inp["kv_len"].sum().item())
+    d, hkv, hq = inp["d"], inp["hkv"], inp["hq"]
+    T = int(inp["cu_q"][-1].item())
+    alg = kv_tokens * hkv * d * 2 * 2 + 2 * T * hq * d * 2   # K + V once, q in, out
+    flops = 4 * d * sum(int(q) * hq * int(n) for q, n in
+                        zip((inp["k"] + 1).tolist(), inp["kv_len"].tolist()))
+    ach = alg / (ms / 1e3) / 1e9
+    return {"metric": "verify attention (1 layer, paged KV), GB/s", "value": round(ach, 1),
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "adaptive-k verify attention B=128, k_b=best_k(U(0.4,0.9), c=0.1), "
+                                   "ctx U[1024,8192], 32/8 heads x 128, paged bf16 block 16",
+                       "batch": B, "query_rows": T, "kv_tokens": kv_tokens,
+                       "mean_k": round(float(inp["k"].float().mean()), 3)},
+            "roofline": {"bound": "hbm", "kernel": "verify_attn_kernel",
+                         "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                         "algorithmic_bytes": alg, "avg_launch_us": round(ms * 1e3, 2),
+                         "mfma_tflops": round(flops / (ms / 1e3) / 1e12, 2)},
+            "cpu_baseline": None}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="verify", choices=["verify", "greedy", "kv"])
+    ap.add_argument("--workload", default="verify", choices=["verify", "greedy", "kv", "attn"])
     ap.add_argument("--sets", type=int, default=3)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=48)
@@ -317,7 +358,8 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no ROCm device visible", file=sys.stderr)
         sys.exit(1)
-    fn = {"verify": bench_verify, "greedy": bench_greedy, "kv": bench_kv}[args.workload]
+    fn = {"verify": bench_verify, "greedy": bench_greedy, "kv": bench_kv,
+          "attn": bench_attn}[args.workload]
     result = fn(args, torch)
     if args.calibrate_copy:
         # a device-to-device copy of known size: its FETCH_SIZE / WRITE_SIZE per

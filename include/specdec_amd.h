@@ -179,6 +179,29 @@ int sdx_kv_append_paged(void* pool, int64_t layer_stride, int64_t side_stride,
                         int64_t max_blocks, int32_t block_size, int64_t num_blocks,
                         const int64_t* lengths, int32_t* error, sdx_stream_t stream);
 
+/* ---- verify attention: the target's multi-query attention of one verify
+ * forward (bench/bench_engine.py:170-174 -> specdec/engine.py:273-275 through
+ * HF SDPA with the mask of specdec/kvcache.py:138-162), one layer.
+ * Row b has q_b = cu_q[b+1] - cu_q[b] <= max_q new positions (its k_b + 1
+ * verify positions), already appended to the paged cache; kv_len[b] counts
+ * the row's keys including them. Query j of row b sees keys
+ * s <= kv_len[b] - q_b + j. q / out: [cu_q[B], num_q_heads, head_dim] bf16;
+ * query head h reads KV head h / (num_q_heads / num_kv_heads). Pools: [num_blocks,
+ * block_size, num_kv_heads * head_dim] bf16 (the K and V sides of one layer of
+ * sdx_kv_append_paged's pool); block_table [batch, max_blocks] int32; cu_q and
+ * kv_len int64 on the device; row_order (nullable, int32 [batch]) gives the order
+ * in which rows are launched (longest kv_len first balances the tail; any
+ * permutation gives the same output). softmax(q k^T * scale) v in fp32, P rounded to
+ * bf16 for the P V product, output rounded to bf16. Rows whose shape or pages
+ * are out of range set *error (nullable) and are skipped. bf16, head_dim 128,
+ * max_q * (num_q_heads / num_kv_heads) <= 64. */
+int sdx_verify_attention_paged(const void* q, int dtype, int64_t batch, const int64_t* cu_q,
+                               int32_t max_q, int32_t num_q_heads, int32_t num_kv_heads,
+                               int32_t head_dim, const void* k_pool, const void* v_pool,
+                               int64_t num_blocks, int32_t block_size, const int32_t* block_table,
+                               int64_t max_blocks, const int64_t* kv_len, const int32_t* row_order,
+                               float scale, void* out, int32_t* error, sdx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,60 @@
+"""GPU parity of the MFMA verify attention (sdx_verify_attention_paged) against
+the float64 oracle (oracle/attention.py), at bf16 tolerance: q, K and V are
+bf16, the kernel accumulates in fp32 and rounds P (the softmax weights) and
+the output to bf16, so |gpu - oracle| <= 2e-2 + 2e-2 |oracle| elementwise."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as OA
+from specdec.attention import verify_attention_paged
+from specdec.workloads import attn_inputs
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _check(inp, hq, hkv, atol=2e-2, rtol=2e-2):
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = verify_attention_paged(inp["q"], inp["cu_q"], inp["k_pool"], inp["v_pool"],
+                                 inp["block_table"], inp["kv_len"], inp["max_q"], error=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    d = inp["q"].shape[-1]
+    ref = OA.verify_attention_paged(inp["q"].float().cpu().numpy(), inp["cu_q"].cpu().numpy(),
+                                    inp["k_pool"].float().cpu().numpy(),
+                                    inp["v_pool"].float().cpu().numpy(),
+                                    inp["block_table"].cpu().numpy(), inp["kv_len"].cpu().numpy(),
+                                    hq, hkv, 1.0 / np.sqrt(d))
+    got = out.float().cpu().numpy()
+    bad = np.abs(got - ref) > atol + rtol * np.abs(ref)
+    assert not bad.any(), (np.abs(got - ref).max(), np.argwhere(bad)[:5])
+    return np.abs(got - ref).max()
+
+
+@pytest.mark.parametrize("B,ctx_lo,ctx_hi,hq,hkv,k_max", [
+    (6, 0, 40, 32, 8, 8),       # short contexts: tails inside the first tiles
+    (5, 100, 300, 32, 8, 8),    # several tiles, ragged q_b from the controller
+    (3, 2000, 2600, 8, 1, 8),   # group 8: up to 72 > 64 rows -> k_max 7 below
+    (4, 37, 90, 16, 16, 3),     # no grouping (group 1)
+])
+def test_verify_attention_matches_oracle(B, ctx_lo, ctx_hi, hq, hkv, k_max):
+    if (k_max + 1) * (hq // hkv) > 64:
+        k_max = 64 // (hq // hkv) - 1
+    inp = attn_inputs(B, seed=B * 7 + ctx_lo, device=DEV, ctx_lo=ctx_lo, ctx_hi=ctx_hi, hq=hq,
+                      hkv=hkv, k_max=k_max, alpha_lo=0.85, alpha_hi=0.95)
+    _check(inp, hq, hkv)
+
+
+def test_verify_attention_rejects_bad_rows():
+    inp = attn_inputs(3, seed=5, device=DEV, ctx_lo=20, ctx_hi=40, hq=8, hkv=2, k_max=4)
+    bt = inp["block_table"].clone()
+    bt[1, 0] = 10 ** 6                      # a page id outside the pool
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    verify_attention_paged(inp["q"], inp["cu_q"], inp["k_pool"], inp["v_pool"], bt,
+                           inp["kv_len"], inp["max_q"], error=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 1
+    with pytest.raises(RuntimeError):       # max_q * group > 64
+        verify_attention_paged(inp["q"], inp["cu_q"], inp["k_pool"], inp["v_pool"],
+                               inp["block_table"], inp["kv_len"], 17)
