@@ -6,19 +6,23 @@
 // s <= lengths[b] + j) and grouped-query heads (query head h reads KV head
 // h / group, the repeat_kv of the HF Qwen3 attention).
 //
-// One workgroup per (batch row, KV head), rows taken in the caller's order
-// (longest context first balances the tail): its query rows are the q_b
-// positions x group heads that share the KV head (q_b * group <= 64, padded to
-// 16-row MFMA tiles; wave w owns rows 16w .. 16w + 15). The row's keys stream
-// through LDS in tiles of 32 tokens gathered through the block table (each
-// token's head slice is 256 contiguous bytes of its page), the next tile
-// prefetched into registers while the current one is used:
+// Split over the keys: one workgroup per (key chunk, batch row, KV head), so a
+// long row spreads over many CUs and the grid is balanced whatever the spread
+// of context lengths. A workgroup's query rows are the q_b positions x group
+// heads that share the KV head (q_b * group <= 64, padded to 16-row MFMA
+// tiles; wave w owns rows 16w .. 16w + 15). The chunk's token -> pool slot map
+// is built in LDS once from the block table (read alongside the row's shape);
+// its keys then stream through LDS
+// in tiles of 32 tokens (each token's head slice is 256 contiguous bytes of
+// its page), two tiles in flight in registers while one is used:
 //   S = Q K^T       16 x 32 per wave: 2 x 8 v_mfma_f32_16x16x16_bf16
 //   online softmax  per row in fp32 (max and sum across the 16-lane rows)
 //   O += P V        16 x 128 per wave: 8 x 2 MFMAs, P rounded to bf16
 // Q operands stay in registers; V is stored transposed in LDS so both MFMA
-// operands of P V are 8-byte reads.
-// The kernel is bound by the KV bytes it streams (about 22 flop per byte),
+// operands of P V are 8-byte reads. A row that fits one chunk writes its
+// output directly; otherwise each chunk writes (O unnormalised, max, sum) in
+// fp32 and a second kernel merges the chunks of the row.
+// The kernels are bound by the KV bytes streamed (about 22 flop per byte),
 // not by MFMA.
 #include "sdx_launch.hpp"
 
@@ -29,10 +33,12 @@ constexpr int VA_NW = VA_NT / kWave;
 constexpr int VA_D = 128;     // head dim
 constexpr int VA_TOK = 32;    // tokens per tile
 constexpr int VA_MAXM = 64;   // query rows per workgroup (q_b * group)
-constexpr int VA_KS = VA_D + 8;    // LDS row strides (bf16 elements), padded against
-                                   // bank conflicts of the 16-row operand reads
-constexpr int VA_VS = VA_TOK + 8;
-constexpr int VA_PS = VA_TOK + 8;
+// LDS row strides (bf16 elements): 2 mod 4 dwords, so the 8-byte MFMA operand
+// reads of 16 consecutive rows hit 32 distinct banks
+constexpr int VA_KS = VA_D + 4;
+constexpr int VA_VS = VA_TOK + 4;
+constexpr int VA_PS = VA_TOK + 4;
+constexpr int VA_CHMAX = 1024;  // most tokens per chunk (multiple of 2 tiles)
 
 typedef short va_s4 __attribute__((ext_vector_type(4)));
 typedef float va_f4 __attribute__((ext_vector_type(4)));
@@ -63,63 +69,120 @@ __device__ __forceinline__ float va_rowsum16(float v) {
   return v + va_ror<8>(v);
 }
 
+constexpr uint32_t VA_NOSLOT = 0xFFFFFFFFu;  // a token whose page id is outside the pool
+
+// the row checks both kernels make (uniform per workgroup): false for a row the
+// launch cannot serve
+__device__ __forceinline__ bool va_row(const AttnArgs& a, int64_t b, int64_t& q0, int64_t& qb,
+                                       int64_t& kvl) {
+  if (b < 0 || b >= a.batch) return false;
+  q0 = a.cu_q[b];
+  qb = a.cu_q[b + 1] - q0;
+  kvl = a.kv_len[b];
+  return qb >= 0 && qb <= a.max_q && kvl - qb >= 0 && (kvl + a.bs - 1) / a.bs <= a.max_blocks;
+}
+
 __global__ void __launch_bounds__(VA_NT) __attribute__((amdgpu_waves_per_eu(3)))
 verify_attn_kernel(AttnArgs a) {
-  __shared__ uint16_t sK[VA_TOK][VA_KS];
-  __shared__ uint16_t sVt[VA_D][VA_VS];
-  __shared__ uint16_t sP[VA_NW][16][VA_PS];
+  __shared__ __align__(16) uint16_t sK[VA_TOK][VA_KS];
+  __shared__ __align__(16) uint16_t sVt[VA_D][VA_VS];
+  __shared__ __align__(16) uint16_t sP[VA_NW][16][VA_PS];
+  __shared__ __align__(16) uint32_t sSlot[VA_CHMAX];  // chunk token -> head slice (256 B) of the pool
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
-  const int64_t b = a.row_order ? (int64_t)a.row_order[blockIdx.x / a.hkv] : blockIdx.x / a.hkv;
+  const int64_t rows = a.batch * a.hkv;
+  const int c = (int)(blockIdx.x / rows);
+  const int64_t slot = (blockIdx.x % rows) / a.hkv;
   const int kvh = (int)(blockIdx.x % a.hkv);
+  const int64_t b = a.row_order ? (int64_t)a.row_order[slot] : slot;
   if (b < 0 || b >= a.batch) {  // uniform: a row order outside [0, batch)
-    if (tid == 0 && a.error) *a.error = 1;
+    if (c == 0 && tid == 0 && a.error) *a.error = 1;
     return;
   }
-  const int64_t q0 = a.cu_q[b], qb = a.cu_q[b + 1] - q0;
-  const int64_t kvl = a.kv_len[b], base = kvl - qb;
-  if (qb < 0 || qb > a.max_q || base < 0 ||
-      (kvl + a.bs - 1) / a.bs > a.max_blocks) {  // uniform: a row the launch cannot serve
-    if (tid == 0 && a.error) *a.error = 1;
+  const int64_t c0 = (int64_t)c * a.chunk;
+  const int64_t p0 = c0 / a.bs;  // first page of the chunk
+  if (p0 >= a.max_blocks) return;  // past every row the block table can hold
+  // the row's shape and the chunk's page ids are fetched together: the ids of
+  // every page the chunk can touch go to LDS (in the V tile's space, unused yet)
+  const int64_t q0 = a.cu_q[b], qb = a.cu_q[b + 1] - q0, kvl = a.kv_len[b];
+  const int np = (int)min((int64_t)(a.chunk / a.bs + 2), a.max_blocks - p0);
+  int32_t* sPage = reinterpret_cast<int32_t*>(&sVt[0][0]);
+  for (int i = tid; i < np; i += VA_NT) sPage[i] = a.block_table[b * a.max_blocks + p0 + i];
+  const int64_t base = kvl - qb;
+  if (qb < 0 || qb > a.max_q || base < 0 || (kvl + a.bs - 1) / a.bs > a.max_blocks) {
+    if (c == 0 && tid == 0 && a.error) *a.error = 1;  // uniform: a row the launch cannot serve
     return;
   }
   const int M = (int)qb * a.group;
-  const int64_t rowB = (int64_t)a.hkv * VA_D * 2;  // bytes per token of a page row
+  if (c0 >= kvl || M == 0) return;  // no such chunk, or no queries
+  const int n = (int)min((int64_t)a.chunk, kvl - c0);
+  const bool whole = kvl <= a.chunk;  // the row is one chunk: write the output directly
+  __syncthreads();  // page ids in LDS
 
-  // ---- tile loads: thread t moves 16 bytes (8 dims) of tokens t / 16 and 16 + t / 16
-  const int ltok = tid / 16, lpart = tid % 16;
-  const int32_t* bt = a.block_table + b * a.max_blocks;
+  // ---- the chunk's slots: token t -> (page * bs + (c0 + t) % bs) * hkv + kvh
   int bad = 0;
-  auto gather = [&](int64_t t0, uint4 (&kv)[4]) {
+  for (int t = tid; t < n; t += VA_NT) {
+    const int64_t pos = c0 + t;
+    const int32_t page = sPage[pos / a.bs - p0];
+    const bool ok = page >= 0 && page < a.num_blocks;
+    bad |= !ok;
+    sSlot[t] = ok ? (uint32_t)((((int64_t)page * a.bs + pos % a.bs) * a.hkv) + kvh) : VA_NOSLOT;
+  }
+
+  // ---- tile loads. K: thread t moves 16 bytes (8 dims) of tokens t / 16 and
+  // 16 + t / 16. V: wave w moves tokens 8w .. 8w + 7, lane l dims 2l, 2l + 1 of
+  // each (a 256-byte row per load), so a lane can write V transposed in 8-byte
+  // runs of 4 tokens.
+  const int ltok = tid / 16, lpart = tid % 16;
+  // Loads are unconditional, so they stay in flight across the tile loop: a
+  // token past the chunk or with a page outside the pool reads slice 0 instead;
+  // its K only meets masked scores (or an error-flagged row) and its V is zeroed
+  // when staged.
+  auto gather = [&](int t0, uint4 (&kk)[2], uint32_t (&vv)[8], uint32_t& vok) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int64_t pos = t0 + ltok + 16 * h;
-      kv[2 * h] = make_uint4(0, 0, 0, 0);
-      kv[2 * h + 1] = make_uint4(0, 0, 0, 0);
-      if (pos < kvl) {
-        const int32_t page = bt[pos / a.bs];
-        if (page >= 0 && page < a.num_blocks) {
-          const int64_t off = (((int64_t)page * a.bs + pos % a.bs) * rowB + kvh * (VA_D * 2) +
-                               lpart * 16) / 2;
-          kv[2 * h] = *reinterpret_cast<const uint4*>(a.k_pool + off);
-          kv[2 * h + 1] = *reinterpret_cast<const uint4*>(a.v_pool + off);
-        } else {
-          bad = 1;
-        }
-      }
+      const int t = t0 + ltok + 16 * h;
+      const uint32_t sl = sSlot[min(t, n - 1)];
+      const bool ok = t < n && sl != VA_NOSLOT;
+      kk[h] = *reinterpret_cast<const uint4*>(a.k_pool + (size_t)(ok ? sl : 0u) * VA_D + lpart * 8);
+    }
+    const int tb = t0 + 8 * w;  // the wave's 8 tokens: slots read as two 16-byte words
+    const int tr = min(tb, VA_CHMAX - 8);
+    const uint4 s0 = *reinterpret_cast<const uint4*>(&sSlot[tr]);
+    const uint4 s1 = *reinterpret_cast<const uint4*>(&sSlot[tr + 4]);
+    const uint32_t sl[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    vok = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool ok = tb + e < n && sl[e] != VA_NOSLOT;
+      vok |= (uint32_t)ok << e;
+      vv[e] = *reinterpret_cast<const uint32_t*>(a.v_pool + (size_t)(ok ? sl[e] : 0u) * VA_D +
+                                                 2 * lane);
     }
   };
-  auto stage = [&](const uint4 (&kv)[4]) {
+  auto stage = [&](const uint4 (&kk)[2], const uint32_t (&vr)[8], uint32_t vok) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int tok = ltok + 16 * h;
-      *reinterpret_cast<uint4*>(&sK[tok][lpart * 8]) = kv[2 * h];
-      const uint32_t vw[4] = {kv[2 * h + 1].x, kv[2 * h + 1].y, kv[2 * h + 1].z,
-                              kv[2 * h + 1].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        sVt[lpart * 8 + e][tok] = (uint16_t)((e & 1) ? (vw[e >> 1] >> 16) : (vw[e >> 1] & 0xFFFFu));
+      uint2* dst = reinterpret_cast<uint2*>(&sK[ltok + 16 * h][lpart * 8]);  // rows are 8-byte aligned
+      dst[0] = make_uint2(kk[h].x, kk[h].y);
+      dst[1] = make_uint2(kk[h].z, kk[h].w);
     }
+    uint32_t vv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vv[e] = (vok >> e) & 1u ? vr[e] : 0u;
+    // dim 2l: the low halves of the 8 tokens, dim 2l + 1 the high halves
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      lo[e] = (vv[2 * e] & 0xFFFFu) | (vv[2 * e + 1] << 16);
+      hi[e] = (vv[2 * e] >> 16) | (vv[2 * e + 1] & 0xFFFF0000u);
+    }
+    uint2* d0 = reinterpret_cast<uint2*>(&sVt[2 * lane][8 * w]);
+    uint2* d1 = reinterpret_cast<uint2*>(&sVt[2 * lane + 1][8 * w]);
+    d0[0] = make_uint2(lo[0], lo[1]);
+    d0[1] = make_uint2(lo[2], lo[3]);
+    d1[0] = make_uint2(hi[0], hi[1]);
+    d1[1] = make_uint2(hi[2], hi[3]);
   };
 
   // ---- per-wave state: rows r0 + 4 * (lane / 16) + r, r < 4
@@ -128,15 +191,16 @@ verify_attn_kernel(AttnArgs a) {
   const int lr = 4 * (lane / 16), lc = lane % 16;
   va_f4 o[8];
 #pragma unroll
-  for (int n = 0; n < 8; ++n) o[n] = (va_f4){0.0f, 0.0f, 0.0f, 0.0f};
+  for (int j = 0; j < 8; ++j) o[j] = (va_f4){0.0f, 0.0f, 0.0f, 0.0f};
   float m_run[4], l_run[4];
-  int64_t lim[4];  // last visible key of the lane's rows (-1: padding row)
+  int lim[4];  // last visible key of the lane's rows, relative to the chunk (-1: none)
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     m_run[r] = -INFINITY;
     l_run[r] = 0.0f;
     const int i = r0 + lr + r;
-    lim[r] = i < M ? base + i / a.group : -1;
+    const int64_t l = i < M ? base + i / a.group - c0 : -1;
+    lim[r] = (int)max((int64_t)-1, min(l, (int64_t)a.chunk));
   }
 
   // the wave's query operands, in registers: lane holds row r0 + lc, dims
@@ -152,70 +216,83 @@ verify_attn_kernel(AttnArgs a) {
       qa[kc] = has ? *reinterpret_cast<const va_s4*>(src + kc * 16 + lr) : (va_s4){0, 0, 0, 0};
   }
 
-  uint4 kv[4];
-  gather(0, kv);
-  for (int64_t t0 = 0; t0 < kvl; t0 += VA_TOK) {
-    stage(kv);
-    __syncthreads();
-    if (t0 + VA_TOK < kvl) gather(t0 + VA_TOK, kv);  // next tile in flight meanwhile
-    if (active) {
-      // S = Q K^T for the wave's 16 rows x 32 tokens
-      va_f4 s[2];
+  // one tile: the wave's rows against the 32 keys from chunk token t0 in LDS
+  auto compute = [&](int t0) {
+    // S = Q K^T for the wave's 16 rows x 32 tokens
+    va_f4 s[2];
 #pragma unroll
-      for (int n = 0; n < 2; ++n) s[n] = (va_f4){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < 2; ++j) s[j] = (va_f4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int kc = 0; kc < VA_D / 16; ++kc) {
+    for (int kc = 0; kc < VA_D / 16; ++kc) {
 #pragma unroll
-        for (int n = 0; n < 2; ++n) {
-          const va_s4 kb = *reinterpret_cast<const va_s4*>(&sK[n * 16 + lc][kc * 16 + lr]);
-          s[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(qa[kc], kb, s[n], 0, 0, 0);
-        }
-      }
-      // online softmax in base 2; s[n][r] is row lr + r, token t0 + 16 n + lc
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float x[2];
-#pragma unroll
-        for (int n = 0; n < 2; ++n) {
-          const int64_t pos = t0 + 16 * n + lc;
-          x[n] = pos <= lim[r] ? s[n][r] * a.scale_log2 : -INFINITY;
-        }
-        const float tmax = va_rowmax16(fmaxf(x[0], x[1]));
-        const float mnew = fmaxf(m_run[r], tmax);
-        const float alpha = mnew == -INFINITY ? 1.0f : exp2f(m_run[r] - mnew);
-        float psum = 0.0f;
-#pragma unroll
-        for (int n = 0; n < 2; ++n) {
-          const float p = x[n] == -INFINITY ? 0.0f : exp2f(x[n] - mnew);
-          const uint16_t pb = va_bf16(p);
-          psum += __uint_as_float((uint32_t)pb << 16);  // the sum of what P V uses
-          sP[w][lr + r][16 * n + lc] = pb;
-        }
-        l_run[r] = l_run[r] * alpha + va_rowsum16(psum);
-        m_run[r] = mnew;
-#pragma unroll
-        for (int n = 0; n < 8; ++n) o[n][r] *= alpha;
-      }
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      __builtin_amdgcn_wave_barrier();  // P written by the whole wave before it is read
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      // O += P V: K = the tile's 32 tokens
-#pragma unroll
-      for (int kc = 0; kc < VA_TOK / 16; ++kc) {
-        const va_s4 pa = *reinterpret_cast<const va_s4*>(&sP[w][lc][kc * 16 + lr]);
-#pragma unroll
-        for (int n = 0; n < 8; ++n) {
-          const va_s4 vb = *reinterpret_cast<const va_s4*>(&sVt[n * 16 + lc][kc * 16 + lr]);
-          o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[n], 0, 0, 0);
-        }
+      for (int j = 0; j < 2; ++j) {
+        const va_s4 kb = *reinterpret_cast<const va_s4*>(&sK[j * 16 + lc][kc * 16 + lr]);
+        s[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(qa[kc], kb, s[j], 0, 0, 0);
       }
     }
+    // online softmax in base 2; s[j][r] is row lr + r, token t0 + 16 j + lc
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float x[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) x[j] = t0 + 16 * j + lc <= lim[r] ? s[j][r] * a.scale_log2 : -INFINITY;
+      const float tmax = va_rowmax16(fmaxf(x[0], x[1]));
+      const float mnew = fmaxf(m_run[r], tmax);
+      const float alpha = mnew == -INFINITY ? 1.0f : exp2f(m_run[r] - mnew);
+      float psum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float p = x[j] == -INFINITY ? 0.0f : exp2f(x[j] - mnew);
+        const uint16_t pb = va_bf16(p);
+        psum += __uint_as_float((uint32_t)pb << 16);  // the sum of what P V uses
+        sP[w][lr + r][16 * j + lc] = pb;
+      }
+      l_run[r] = l_run[r] * alpha + va_rowsum16(psum);
+      m_run[r] = mnew;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j][r] *= alpha;
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_wave_barrier();  // P written by the whole wave before it is read
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    // O += P V: K = the tile's 32 tokens
+#pragma unroll
+    for (int kc = 0; kc < VA_TOK / 16; ++kc) {
+      const va_s4 pa = *reinterpret_cast<const va_s4*>(&sP[w][lc][kc * 16 + lr]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const va_s4 vb = *reinterpret_cast<const va_s4*>(&sVt[j * 16 + lc][kc * 16 + lr]);
+        o[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[j], 0, 0, 0);
+      }
+    }
+  };
+
+  __syncthreads();  // the slot map is complete
+  // two tiles in flight while one is used: A holds tiles 0, 2, 4, ..., B 1, 3, 5, ...
+  uint4 kA[2], kB[2];
+  uint32_t vA[8], vB[8], okA, okB;
+  gather(0, kA, vA, okA);
+  gather(VA_TOK, kB, vB, okB);
+  // one exit, at the bottom: both register sets are then in flight in the same
+  // order on every entry to the loop, so each stage waits for its own set only
+  // (a second tile past the chunk's end is all masked, with V zeroed)
+  for (int t0 = 0;; t0 += 2 * VA_TOK) {
+    stage(kA, vA, okA);
+    __syncthreads();
+    gather(t0 + 2 * VA_TOK, kA, vA, okA);
+    if (active) compute(t0);
     __syncthreads();  // the tile's LDS is rewritten next
+    stage(kB, vB, okB);
+    __syncthreads();
+    gather(t0 + 3 * VA_TOK, kB, vB, okB);
+    if (active) compute(t0 + VA_TOK);
+    __syncthreads();
+    if (t0 + 2 * VA_TOK >= n) break;
   }
   if (bad && a.error) *a.error = 1;
+  if (!active) return;
 
-  // ---- out[q0 + j, kvh * group + g, :] = O / l
-  if (active) {
+  if (whole) {  // out[q0 + j, kvh * group + g, :] = O / l
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = r0 + lr + r;
@@ -224,14 +301,69 @@ verify_attn_kernel(AttnArgs a) {
         uint16_t* dst = a.out + ((q0 + j) * a.hq + kvh * a.group + g) * VA_D;
         const float inv = l_run[r] > 0.0f ? 1.0f / l_run[r] : 0.0f;
 #pragma unroll
-        for (int n = 0; n < 8; ++n) dst[n * 16 + lc] = va_bf16(o[n][r] * inv);
+        for (int jj = 0; jj < 8; ++jj) dst[jj * 16 + lc] = va_bf16(o[jj][r] * inv);
       }
+    }
+    return;
+  }
+  // the chunk's partial: O unnormalised and (max, sum) per query row, in the
+  // part of (row b, KV head, chunk c)
+  const int64_t part = ((b * a.hkv + kvh) * a.nchunk + c) * a.max_m;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int i = r0 + lr + r;
+    if (i < M) {
+      float* po = a.part_o + (part + i) * VA_D;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) po[jj * 16 + lc] = o[jj][r];
+      if (lc == 0) *reinterpret_cast<float2*>(a.part_ml + (part + i) * 2) = make_float2(m_run[r], l_run[r]);
     }
   }
 }
 
+// merge of the chunk partials of every row longer than one chunk: one workgroup
+// per (row, KV head); out = sum_c 2^(m_c - m) O_c / sum_c 2^(m_c - m) l_c with
+// m the rows's largest m_c
+__global__ void __launch_bounds__(VA_NT) verify_attn_merge_kernel(AttnArgs a) {
+  const int64_t b = blockIdx.x / a.hkv;
+  const int kvh = (int)(blockIdx.x % a.hkv);
+  int64_t q0, qb, kvl;
+  if (!va_row(a, b, q0, qb, kvl) || kvl <= a.chunk) return;
+  const int nch = (int)((kvl + a.chunk - 1) / a.chunk);
+  const int M = (int)qb * a.group;
+  const int64_t part0 = (b * a.hkv + kvh) * a.nchunk * a.max_m;
+  for (int e = threadIdx.x; e < M * VA_D; e += VA_NT) {
+    const int i = e / VA_D, d = e % VA_D;
+    float mx = -INFINITY;
+    for (int ch = 0; ch < nch; ++ch) mx = fmaxf(mx, a.part_ml[(part0 + (int64_t)ch * a.max_m + i) * 2]);
+    float num = 0.0f, den = 0.0f;
+    for (int ch = 0; ch < nch; ++ch) {
+      const int64_t p = part0 + (int64_t)ch * a.max_m + i;
+      const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + p * 2);
+      if (ml.x == -INFINITY) continue;  // the chunk holds none of the row's visible keys
+      const float f = exp2f(ml.x - mx);
+      den += f * ml.y;
+      num += f * a.part_o[p * VA_D + d];
+    }
+    const int64_t j = i / a.group, g = i % a.group;
+    a.out[((q0 + j) * a.hq + kvh * a.group + g) * VA_D + d] = va_bf16(den > 0.0f ? num / den : 0.0f);
+  }
+}
+
+int attn_chunk_tokens(int64_t batch, int32_t hkv, int64_t max_tokens, int32_t chunk) {
+  if (chunk > 0) return chunk;
+  // smallest chunk count that still leaves about 8 workgroups per CU of work
+  int ch = VA_CHMAX;
+  while (ch > 2 * VA_TOK && batch * hkv * ((max_tokens + ch - 1) / ch) < 8 * 256) ch /= 2;
+  return ch;
+}
+
 hipError_t launch_verify_attn(const AttnArgs& a, int64_t batch, hipStream_t s) {
-  hipLaunchKernelGGL(verify_attn_kernel, dim3((unsigned)(batch * a.hkv)), dim3(VA_NT), 0, s, a);
+  hipLaunchKernelGGL(verify_attn_kernel, dim3((unsigned)(a.nchunk * batch * a.hkv)), dim3(VA_NT), 0,
+                     s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.nchunk == 1) return e;
+  hipLaunchKernelGGL(verify_attn_merge_kernel, dim3((unsigned)(batch * a.hkv)), dim3(VA_NT), 0, s, a);
   return hipGetLastError();
 }
 

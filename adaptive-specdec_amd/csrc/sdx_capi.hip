@@ -506,27 +506,74 @@ int sdx_kv_append_paged(void* pool, int64_t layer_stride, int64_t side_stride, c
 }
 
 // ------------------------------------------------------------------ verify attention
+// chunking of the keys shared by the workspace query and the launch
+static int attn_plan(int64_t batch, int32_t max_q, int32_t num_q_heads, int32_t num_kv_heads,
+                     int32_t block_size, int64_t max_blocks, int32_t chunk_tokens, int32_t* chunk,
+                     int32_t* nchunk, size_t* bytes) {
+  if (batch < 0 || max_q < 1 || num_q_heads < 1 || num_kv_heads < 1 || block_size < 1 ||
+      max_blocks < 1 || chunk_tokens < 0)
+    return fail(SDX_EINVAL, "sdx_verify_attention: bad arguments");
+  if (chunk_tokens != 0 && (chunk_tokens % 64 != 0 || chunk_tokens > 1024))
+    return fail(SDX_EINVAL, "sdx_verify_attention: chunk_tokens must be 0 or a multiple of 64 "
+                            "up to 1024 (got %d)", chunk_tokens);
+  if (num_q_heads % num_kv_heads != 0)
+    return fail(SDX_EINVAL, "sdx_verify_attention: query heads must be a multiple of KV heads");
+  const int64_t max_tokens = max_blocks * block_size;
+  if (max_tokens > ((int64_t)1 << 31) - 1)
+    return fail(SDX_EUNSUPPORTED, "sdx_verify_attention: max_blocks * block_size >= 2^31");
+  const int32_t ch = sdx::attn_chunk_tokens(batch, num_kv_heads, max_tokens, chunk_tokens);
+  const int64_t nch = (max_tokens + ch - 1) / ch;
+  const int64_t m = (int64_t)max_q * (num_q_heads / num_kv_heads);
+  if (nch * batch * num_kv_heads > 0x7FFFFFFF)
+    return fail(SDX_EUNSUPPORTED, "sdx_verify_attention: grid of %lld chunks is too large",
+                (long long)(nch * batch * num_kv_heads));
+  *chunk = ch;
+  *nchunk = (int32_t)nch;
+  *bytes = nch > 1 ? (size_t)(batch * num_kv_heads * nch * m) * (128 + 2) * sizeof(float) : 0;
+  return SDX_OK;
+}
+
+size_t sdx_verify_attention_workspace(int64_t batch, int32_t max_q, int32_t num_q_heads,
+                                      int32_t num_kv_heads, int32_t block_size,
+                                      int64_t max_blocks, int32_t chunk_tokens) {
+  int32_t ch, nch;
+  size_t bytes = 0;
+  if (attn_plan(batch, max_q, num_q_heads, num_kv_heads, block_size, max_blocks, chunk_tokens,
+                &ch, &nch, &bytes) != SDX_OK)
+    return 0;
+  return bytes;
+}
+
 int sdx_verify_attention_paged(const void* q, int dtype, int64_t batch, const int64_t* cu_q,
                                int32_t max_q, int32_t num_q_heads, int32_t num_kv_heads,
                                int32_t head_dim, const void* k_pool, const void* v_pool,
                                int64_t num_blocks, int32_t block_size, const int32_t* block_table,
                                int64_t max_blocks, const int64_t* kv_len, const int32_t* row_order,
-                               float scale, void* out, int32_t* error, sdx_stream_t stream) {
-  if (!q || !cu_q || !k_pool || !v_pool || !block_table || !kv_len || !out || batch < 0 ||
-      max_q < 1 || num_q_heads < 1 || num_kv_heads < 1 || num_blocks < 1 || block_size < 1 ||
-      max_blocks < 1 || !(scale > 0.0f))
+                               float scale, int32_t chunk_tokens, void* workspace,
+                               size_t workspace_bytes, void* out, int32_t* error,
+                               sdx_stream_t stream) {
+  if (!q || !cu_q || !k_pool || !v_pool || !block_table || !kv_len || !out || num_blocks < 1 ||
+      !(scale > 0.0f))
     return fail(SDX_EINVAL, "sdx_verify_attention_paged: bad arguments");
   if (dtype != SDX_BF16 || head_dim != 128)
     return fail(SDX_EUNSUPPORTED, "sdx_verify_attention_paged: bf16 with head_dim 128 only");
-  if (num_q_heads % num_kv_heads != 0)
-    return fail(SDX_EINVAL, "sdx_verify_attention_paged: query heads must be a multiple of KV heads");
+  int32_t ch = 0, nch = 0;
+  size_t need = 0;
+  const int rc = attn_plan(batch, max_q, num_q_heads, num_kv_heads, block_size, max_blocks,
+                           chunk_tokens, &ch, &nch, &need);
+  if (rc != SDX_OK) return rc;
   const int32_t group = num_q_heads / num_kv_heads;
   if ((int64_t)max_q * group > 64)
     return fail(SDX_EUNSUPPORTED,
                 "sdx_verify_attention_paged: max_q * (query heads per KV head) must be <= 64 "
                 "(got %d * %d)", max_q, group);
+  if (num_blocks * block_size * num_kv_heads >= (int64_t)0xFFFFFFFF)
+    return fail(SDX_EUNSUPPORTED, "sdx_verify_attention_paged: pool of 2^32 or more head slices");
   if (!aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool) || !aligned16(out))
     return fail(SDX_EINVAL, "sdx_verify_attention_paged: tensors must be 16-byte aligned");
+  if (need > 0 && (!workspace || workspace_bytes < need || !aligned16(workspace)))
+    return fail(SDX_EINVAL, "sdx_verify_attention_paged: needs a 16-byte aligned workspace of "
+                            "%zu bytes (got %zu)", need, workspace ? workspace_bytes : (size_t)0);
   if (batch == 0) return SDX_OK;
   sdx::AttnArgs a = {};
   a.q = (const uint16_t*)q;
@@ -546,6 +593,12 @@ int sdx_verify_attention_paged(const void* q, int dtype, int64_t batch, const in
   a.group = group;
   a.bs = block_size;
   a.max_q = max_q;
+  a.chunk = ch;
+  a.nchunk = nch;
+  a.max_m = max_q * group;
+  const int64_t nparts = batch * num_kv_heads * (int64_t)nch * a.max_m;
+  a.part_o = need > 0 ? (float*)workspace : nullptr;
+  a.part_ml = need > 0 ? (float*)workspace + nparts * 128 : nullptr;
   a.scale_log2 = scale * 1.4426950408889634f;
   return hip_status(sdx::launch_verify_attn(a, batch, (hipStream_t)stream), "verify_attn");
 }

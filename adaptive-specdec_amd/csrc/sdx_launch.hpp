@@ -169,10 +169,15 @@ struct AttnArgs {
   const int32_t* row_order;  // [B] rows in launch order, or null (0 .. B-1)
   uint16_t* out;            // [T, hq, 128] bf16
   int32_t* error;           // set when a row's shape or pages are out of range
+  float* part_o;            // [B, hkv, nchunk, max_m, 128] chunk partials (nchunk > 1)
+  float* part_ml;           // [B, hkv, nchunk, max_m, 2] their (max, sum)
   int64_t max_blocks, num_blocks, batch;
   int32_t hq, hkv, group, bs, max_q;
+  int32_t chunk, nchunk, max_m;  // tokens per chunk, chunks of the longest row, max_q * group
   float scale_log2;         // softmax scale * log2(e)
 };
+// tokens per key chunk (chunk > 0: that value, else the default for the shape)
+int attn_chunk_tokens(int64_t batch, int32_t hkv, int64_t max_tokens, int32_t chunk);
 hipError_t launch_verify_attn(const AttnArgs& a, int64_t batch, hipStream_t s);
 // sdx_kv.hip
 hipError_t launch_kv_advance(int64_t* lengths, int64_t batch, int64_t q, hipStream_t s);

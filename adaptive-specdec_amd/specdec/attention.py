@@ -14,17 +14,28 @@ import torch
 
 from . import _lib
 
-__all__ = ["verify_attention_paged"]
+__all__ = ["verify_attention_paged", "attention_workspace"]
+
+
+def attention_workspace(B, max_q, hq, hkv, block_size, max_blocks, chunk_tokens=0,
+                        device="cuda"):
+    """A workspace for verify_attention_paged at these sizes (uint8 device tensor)."""
+    need = _lib.lib().sdx_verify_attention_workspace(B, int(max_q), hq, hkv, block_size,
+                                                     max_blocks, int(chunk_tokens))
+    return torch.empty(max(need, 1), dtype=torch.uint8, device=device)
 
 
 def verify_attention_paged(q, cu_q, k_pool, v_pool, block_table, kv_len, max_q, scale=None,
-                           out=None, error=None, row_order=None):
+                           out=None, error=None, row_order=None, chunk_tokens=0, workspace=None):
     """q [T, Hq, 128] bf16 (T = cu_q[-1]); cu_q [B+1] int64; k_pool / v_pool
     [num_blocks, block_size, Hkv * 128] bf16 (one layer's K and V sides of a
     PagedKVCache pool); block_table [B, max_blocks] int32; kv_len [B] int64 (keys
     per row, the new positions included); max_q >= every row's q_b. Returns
     out [T, Hq, 128] bf16. Rows whose shape or pages are out of range are
-    skipped and set `error` (an int32 [1] device tensor) when given. Rows are
+    skipped and set `error` (an int32 [1] device tensor) when given. Each row's
+    keys are split in chunks of `chunk_tokens` (0: the library's default) on
+    separate workgroups; rows of several chunks merge fp32 partials held in
+    `workspace` (a uint8 device tensor, allocated here when None). Rows are
     launched longest context first unless `row_order` (int32 [B]) is given."""
     _lib.require_gpu(q, cu_q, k_pool, v_pool, block_table, kv_len)
     if q.dtype != torch.bfloat16 or k_pool.dtype != torch.bfloat16 or v_pool.dtype != torch.bfloat16:
@@ -47,9 +58,14 @@ def verify_attention_paged(q, cu_q, k_pool, v_pool, block_table, kv_len, max_q, 
     row_order = row_order.to(torch.int32).contiguous()
     if out is None:
         out = torch.empty_like(q)
+    need = _lib.lib().sdx_verify_attention_workspace(B, int(max_q), hq, hkv, bs, bt.shape[1],
+                                                     int(chunk_tokens))
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
     rc = _lib.lib().sdx_verify_attention_paged(
         _lib.ptr(q), _lib.BF16, B, _lib.ptr(cu), int(max_q), hq, hkv, d,
         _lib.ptr(k_pool), _lib.ptr(v_pool), nb, bs, _lib.ptr(bt),
-        bt.shape[1], _lib.ptr(kl), _lib.ptr(row_order), scale, _lib.ptr(out), _lib.ptr(error), _lib.stream_of(q))
+        bt.shape[1], _lib.ptr(kl), _lib.ptr(row_order), scale, int(chunk_tokens),
+        _lib.ptr(workspace), workspace.numel(), _lib.ptr(out), _lib.ptr(error), _lib.stream_of(q))
     _lib.check(rc, "verify_attention_paged")
     return out

@@ -299,15 +299,18 @@ def bench_attn(args, torch):
     """Adaptive-k verify attention, one layer: B=128 rows with k_b = best_k(alpha_b, 0.1),
     alpha_b ~ U(0.4, 0.9), contexts ~ U[1024, 8192], 32 query / 8 KV heads of 128,
     paged bf16 KV (block 16). HBM roofline: every visible key and value read once."""
-    from specdec.attention import verify_attention_paged
+    from specdec.attention import attention_workspace, verify_attention_paged
     from specdec.workloads import attn_inputs
     dev = "cuda:0"
     B = 128
     inp = attn_inputs(B, seed=5, device=dev)
     out = torch.empty_like(inp["q"])
+    bs, mb = inp["k_pool"].shape[1], inp["block_table"].shape[1]
+    ws = attention_workspace(B, inp["max_q"], inp["hq"], inp["hkv"], bs, mb, args.attn_chunk,
+                             device=dev)
     call = lambda: verify_attention_paged(inp["q"], inp["cu_q"], inp["k_pool"], inp["v_pool"],  # noqa: E731
                                           inp["block_table"], inp["kv_len"], inp["max_q"],
-                                          out=out)
+                                          out=out, chunk_tokens=args.attn_chunk, workspace=ws)
     for _ in range(args.warmup):
         call()
     torch.cuda.synchronize()
@@ -327,6 +330,7 @@ def bench_attn(args, torch):
             "config": {"workload": "adaptive-k verify attention B=128, k_b=best_k(U(0.4,0.9), c=0.1), "
                                    "ctx U[1024,8192], 32/8 heads x 128, paged bf16 block 16",
                        "batch": B, "query_rows": T, "kv_tokens": kv_tokens,
+                       "chunk_tokens": args.attn_chunk,
                        "mean_k": round(float(inp["k"].float().mean()), 3)},
             "roofline": {"bound": "hbm", "kernel": "verify_attn_kernel",
                          "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -343,6 +347,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="verify", choices=["verify", "greedy", "kv", "attn"])
     ap.add_argument("--sets", type=int, default=3)
+    ap.add_argument("--attn-chunk", type=int, default=0,
+                    help="attn workload: keys per chunk (0: the library default)")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=48)
     ap.add_argument("--skip-cpu", action="store_true")

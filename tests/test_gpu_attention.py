@@ -14,10 +14,11 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def _check(inp, hq, hkv, atol=2e-2, rtol=2e-2):
+def _check(inp, hq, hkv, atol=2e-2, rtol=2e-2, chunk_tokens=0):
     err = torch.zeros(1, dtype=torch.int32, device=DEV)
     out = verify_attention_paged(inp["q"], inp["cu_q"], inp["k_pool"], inp["v_pool"],
-                                 inp["block_table"], inp["kv_len"], inp["max_q"], error=err)
+                                 inp["block_table"], inp["kv_len"], inp["max_q"], error=err,
+                                 chunk_tokens=chunk_tokens)
     torch.cuda.synchronize()
     assert int(err.item()) == 0
     d = inp["q"].shape[-1]
@@ -46,6 +47,26 @@ def test_verify_attention_matches_oracle(B, ctx_lo, ctx_hi, hq, hkv, k_max):
     _check(inp, hq, hkv)
 
 
+@pytest.mark.parametrize("chunk", [64, 128, 1024])
+def test_verify_attention_chunked_matches_oracle(chunk):
+    """Rows split over several key chunks (merged from fp32 partials) and rows of
+    one chunk, in one launch; the last chunk of a row may hold no key that a
+    query row sees (fully masked partial)."""
+    inp = attn_inputs(6, seed=chunk, device=DEV, ctx_lo=1, ctx_hi=1500, hq=32, hkv=8, k_max=8,
+                      alpha_lo=0.85, alpha_hi=0.95)
+    _check(inp, 32, 8, chunk_tokens=chunk)
+
+
+def test_verify_attention_same_for_any_chunking():
+    inp = attn_inputs(4, seed=11, device=DEV, ctx_lo=300, ctx_hi=900, hq=16, hkv=4, k_max=6)
+    outs = [verify_attention_paged(inp["q"], inp["cu_q"], inp["k_pool"], inp["v_pool"],
+                                   inp["block_table"], inp["kv_len"], inp["max_q"],
+                                   chunk_tokens=ch).float() for ch in (64, 192, 1024)]
+    for o in outs[1:]:
+        # rounding of P to bf16 is relative to each chunk's running max
+        assert torch.allclose(o, outs[0], atol=1e-2, rtol=1e-2)
+
+
 def test_verify_attention_rejects_bad_rows():
     inp = attn_inputs(3, seed=5, device=DEV, ctx_lo=20, ctx_hi=40, hq=8, hkv=2, k_max=4)
     bt = inp["block_table"].clone()
@@ -58,3 +79,6 @@ def test_verify_attention_rejects_bad_rows():
     with pytest.raises(RuntimeError):       # max_q * group > 64
         verify_attention_paged(inp["q"], inp["cu_q"], inp["k_pool"], inp["v_pool"],
                                inp["block_table"], inp["kv_len"], 17)
+    with pytest.raises(RuntimeError):       # chunk not a multiple of 64
+        verify_attention_paged(inp["q"], inp["cu_q"], inp["k_pool"], inp["v_pool"],
+                               inp["block_table"], inp["kv_len"], inp["max_q"], chunk_tokens=96)
