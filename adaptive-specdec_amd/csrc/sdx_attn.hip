@@ -88,6 +88,7 @@ verify_attn_kernel(AttnArgs a) {
   __shared__ __align__(16) uint16_t sVt[VA_D][VA_VS];
   __shared__ __align__(16) uint16_t sP[VA_NW][16][VA_PS];
   __shared__ __align__(16) uint32_t sSlot[VA_CHMAX];  // chunk token -> head slice (256 B) of the pool
+  __shared__ int64_t sRow[VA_MAXM];  // query row i -> element offset of its q / out vector
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   const int64_t rows = a.batch * a.hkv;
@@ -117,7 +118,9 @@ verify_attn_kernel(AttnArgs a) {
   if (c0 >= kvl || M == 0) return;  // no such chunk, or no queries
   const int n = (int)min((int64_t)a.chunk, kvl - c0);
   const bool whole = kvl <= a.chunk;  // the row is one chunk: write the output directly
-  __syncthreads();  // page ids in LDS
+  // row i = j * group + g is query head kvh * group + g of position j
+  if (tid < M) sRow[tid] = ((q0 + tid / a.group) * a.hq + kvh * a.group + tid % a.group) * VA_D;
+  __syncthreads();  // page ids and row offsets in LDS
 
   // ---- the chunk's slots: token t -> (page * bs + (c0 + t) % bs) * hkv + kvh
   int bad = 0;
@@ -204,13 +207,12 @@ verify_attn_kernel(AttnArgs a) {
   }
 
   // the wave's query operands, in registers: lane holds row r0 + lc, dims
-  // 16 kc + lr .. + 3 (row i = j * group + g is head kvh * group + g of position j)
+  // 16 kc + lr .. + 3
   va_s4 qa[VA_D / 16];
   {
     const int i = r0 + lc;
     const bool has = active && i < M;
-    const uint16_t* src = a.q + (has ? ((q0 + i / a.group) * a.hq + kvh * a.group + i % a.group) * VA_D
-                                     : 0);
+    const uint16_t* src = a.q + (has ? sRow[i] : 0);
 #pragma unroll
     for (int kc = 0; kc < VA_D / 16; ++kc)
       qa[kc] = has ? *reinterpret_cast<const va_s4*>(src + kc * 16 + lr) : (va_s4){0, 0, 0, 0};
@@ -291,14 +293,16 @@ verify_attn_kernel(AttnArgs a) {
   }
   if (bad && a.error) *a.error = 1;
   if (!active) return;
+  // the row index is rebuilt here rather than kept live across the tile loop
+  int lre = lr;
+  asm volatile("" : "+v"(lre));
 
   if (whole) {  // out[q0 + j, kvh * group + g, :] = O / l
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int i = r0 + lr + r;
+      const int i = r0 + lre + r;
       if (i < M) {
-        const int64_t j = i / a.group, g = i % a.group;
-        uint16_t* dst = a.out + ((q0 + j) * a.hq + kvh * a.group + g) * VA_D;
+        uint16_t* dst = a.out + sRow[i];
         const float inv = l_run[r] > 0.0f ? 1.0f / l_run[r] : 0.0f;
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) dst[jj * 16 + lc] = va_bf16(o[jj][r] * inv);
@@ -311,7 +315,7 @@ verify_attn_kernel(AttnArgs a) {
   const int64_t part = ((b * a.hkv + kvh) * a.nchunk + c) * a.max_m;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int i = r0 + lr + r;
+    const int i = r0 + lre + r;
     if (i < M) {
       float* po = a.part_o + (part + i) * VA_D;
 #pragma unroll
@@ -322,9 +326,14 @@ verify_attn_kernel(AttnArgs a) {
 }
 
 // merge of the chunk partials of every row longer than one chunk: one workgroup
-// per (row, KV head); out = sum_c 2^(m_c - m) O_c / sum_c 2^(m_c - m) l_c with
-// m the rows's largest m_c
+// per (row, KV head); out = sum_c w_c O_c with w_c = 2^(m_c - m) / sum_c' 2^(m_c' - m) l_c'
+// and m the row's largest m_c. The (m, l) pairs go through LDS and each query
+// row's weights are formed once; the O partials are then read as float4 with
+// the loads of several chunks in flight.
+constexpr int VA_MERGE_W = 4096;  // weights held in LDS (chunks x query rows)
+
 __global__ void __launch_bounds__(VA_NT) verify_attn_merge_kernel(AttnArgs a) {
+  __shared__ float sW[VA_MERGE_W], sL[VA_MERGE_W];
   const int64_t b = blockIdx.x / a.hkv;
   const int kvh = (int)(blockIdx.x % a.hkv);
   int64_t q0, qb, kvl;
@@ -332,21 +341,73 @@ __global__ void __launch_bounds__(VA_NT) verify_attn_merge_kernel(AttnArgs a) {
   const int nch = (int)((kvl + a.chunk - 1) / a.chunk);
   const int M = (int)qb * a.group;
   const int64_t part0 = (b * a.hkv + kvh) * a.nchunk * a.max_m;
-  for (int e = threadIdx.x; e < M * VA_D; e += VA_NT) {
-    const int i = e / VA_D, d = e % VA_D;
-    float mx = -INFINITY;
-    for (int ch = 0; ch < nch; ++ch) mx = fmaxf(mx, a.part_ml[(part0 + (int64_t)ch * a.max_m + i) * 2]);
-    float num = 0.0f, den = 0.0f;
-    for (int ch = 0; ch < nch; ++ch) {
-      const int64_t p = part0 + (int64_t)ch * a.max_m + i;
-      const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + p * 2);
-      if (ml.x == -INFINITY) continue;  // the chunk holds none of the row's visible keys
-      const float f = exp2f(ml.x - mx);
-      den += f * ml.y;
-      num += f * a.part_o[p * VA_D + d];
+  const bool staged = nch * M <= VA_MERGE_W;  // uniform
+  if (staged) {
+    for (int e = threadIdx.x; e < nch * M; e += VA_NT) {  // sW, sL [c * M + i] = m, l of (c, i)
+      const int ch = e / M, i = e % M;
+      const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (part0 + (int64_t)ch * a.max_m + i) * 2);
+      sW[e] = ml.x;
+      sL[e] = ml.y;
+    }
+    __syncthreads();
+    if (threadIdx.x < M) {  // one thread per query row: weights in place of the maxima
+      const int i = threadIdx.x;
+      float mx = -INFINITY;
+      for (int ch = 0; ch < nch; ++ch) mx = fmaxf(mx, sW[ch * M + i]);
+      float den = 0.0f;
+      for (int ch = 0; ch < nch; ++ch) {
+        const float m = sW[ch * M + i];
+        const float f = m == -INFINITY ? 0.0f : exp2f(m - mx);
+        sW[ch * M + i] = f;
+        den += f * sL[ch * M + i];
+      }
+      const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+      for (int ch = 0; ch < nch; ++ch) sW[ch * M + i] *= inv;
+    }
+    __syncthreads();
+  }
+  for (int e = threadIdx.x; e < M * (VA_D / 4); e += VA_NT) {
+    const int i = e / (VA_D / 4), d4 = e % (VA_D / 4);
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (staged) {
+#pragma unroll 4
+      for (int ch = 0; ch < nch; ++ch) {
+        const float wgt = sW[ch * M + i];
+        const float4 v = *reinterpret_cast<const float4*>(
+            a.part_o + (part0 + (int64_t)ch * a.max_m + i) * VA_D + d4 * 4);
+        acc.x += wgt * v.x;
+        acc.y += wgt * v.y;
+        acc.z += wgt * v.z;
+        acc.w += wgt * v.w;
+      }
+    } else {  // more chunks x rows than LDS holds: weights formed per element
+      float mx = -INFINITY;
+      for (int ch = 0; ch < nch; ++ch)
+        mx = fmaxf(mx, a.part_ml[(part0 + (int64_t)ch * a.max_m + i) * 2]);
+      float den = 0.0f;
+      for (int ch = 0; ch < nch; ++ch) {
+        const int64_t p = part0 + (int64_t)ch * a.max_m + i;
+        const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + p * 2);
+        if (ml.x == -INFINITY) continue;  // the chunk holds none of the row's visible keys
+        const float f = exp2f(ml.x - mx);
+        den += f * ml.y;
+        const float4 v = *reinterpret_cast<const float4*>(a.part_o + p * VA_D + d4 * 4);
+        acc.x += f * v.x;
+        acc.y += f * v.y;
+        acc.z += f * v.z;
+        acc.w += f * v.w;
+      }
+      const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+      acc.x *= inv;
+      acc.y *= inv;
+      acc.z *= inv;
+      acc.w *= inv;
     }
     const int64_t j = i / a.group, g = i % a.group;
-    a.out[((q0 + j) * a.hq + kvh * a.group + g) * VA_D + d] = va_bf16(den > 0.0f ? num / den : 0.0f);
+    uint16_t* dst = a.out + ((q0 + j) * a.hq + kvh * a.group + g) * VA_D + d4 * 4;
+    const uint32_t lo = (uint32_t)va_bf16(acc.x) | ((uint32_t)va_bf16(acc.y) << 16);
+    const uint32_t hi = (uint32_t)va_bf16(acc.z) | ((uint32_t)va_bf16(acc.w) << 16);
+    *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
   }
 }
 
