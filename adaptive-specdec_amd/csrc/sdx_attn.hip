@@ -6,9 +6,13 @@
 // s <= lengths[b] + j) and grouped-query heads (query head h reads KV head
 // h / group, the repeat_kv of the HF Qwen3 attention).
 //
-// Split over the keys: one workgroup per (key chunk, batch row, KV head), so a
-// long row spreads over many CUs and the grid is balanced whatever the spread
-// of context lengths. A workgroup's query rows are the q_b positions x group
+// Split over the keys: one workgroup per (key chunk, KV head), so a long row
+// spreads over many CUs. A plan kernel (one workgroup) lists the chunks longest
+// first (all whole chunks, then the rows' last partial chunks by decreasing
+// size), each with its row's shape, so the hardware's in-order dispatch ends on
+// the shortest work and a workgroup learns everything about its chunk in one
+// load; the KV heads of a chunk are adjacent workgroups and stream the same
+// page rows together. A workgroup's query rows are the q_b positions x group
 // heads that share the KV head (q_b * group <= 64, padded to 16-row MFMA
 // tiles; wave w owns rows 16w .. 16w + 15). The chunk's token -> pool slot map
 // is built in LDS once from the block table (read alongside the row's shape);
@@ -82,6 +86,89 @@ __device__ __forceinline__ bool va_row(const AttnArgs& a, int64_t b, int64_t& q0
   return qb >= 0 && qb <= a.max_q && kvl - qb >= 0 && (kvl + a.bs - 1) / a.bs <= a.max_blocks;
 }
 
+// ---- plan: one workgroup. Row b (valid, with queries) has kvl / chunk whole
+// chunks and, if kvl % chunk > 0, one partial chunk. units[0 ..) = the whole
+// chunks row by row, then the partial chunks by decreasing size, then b = -1 up
+// to nunits. A row the launch cannot serve sets *error and gets no chunk.
+constexpr int VA_PLAN_NT = 1024;
+
+// exclusive scan over the workgroup of x (one value per thread); every thread
+// gets the total
+__device__ __forceinline__ long long va_block_scan(long long x, long long* sWave, long long& total) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
+  long long inc = x;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const long long y = __shfl_up(inc, d, kWave);
+    if (lane >= d) inc += y;
+  }
+  if (lane == kWave - 1) sWave[wv] = inc;
+  __syncthreads();
+  if (tid == 0) {
+    long long run = 0;
+    for (int k = 0; k < VA_PLAN_NT / kWave; ++k) {
+      const long long t = sWave[k];
+      sWave[k] = run;
+      run += t;
+    }
+    sWave[VA_PLAN_NT / kWave] = run;
+  }
+  __syncthreads();
+  const long long ex = sWave[wv] + inc - x;
+  total = sWave[VA_PLAN_NT / kWave];
+  __syncthreads();  // sWave is reused by the next scan
+  return ex;
+}
+
+__global__ void __launch_bounds__(VA_PLAN_NT) verify_attn_plan_kernel(AttnArgs a) {
+  __shared__ long long sWave[VA_PLAN_NT / kWave + 1];
+  __shared__ int sBin[VA_CHMAX];  // partial chunks by size, then their first slot
+  const int tid = threadIdx.x;
+  for (int r = tid; r < VA_CHMAX; r += VA_PLAN_NT) sBin[r] = 0;
+  __syncthreads();
+  long long carry = 0;  // whole chunks so far
+  for (int64_t b0 = 0; b0 < a.batch; b0 += VA_PLAN_NT) {
+    const int64_t b = b0 + tid;
+    long long nfull = 0;
+    int64_t q0 = 0, qb = 0, kvl = 0;
+    if (b < a.batch) {
+      if (va_row(a, b, q0, qb, kvl)) {
+        if (qb > 0) {
+          nfull = kvl / a.chunk;
+          const int rem = (int)(kvl % a.chunk);
+          if (rem > 0) atomicAdd(&sBin[rem], 1);
+        }
+      } else if (a.error) {
+        *a.error = 1;
+      }
+    }
+    long long tot;
+    const long long f = carry + va_block_scan(nfull, sWave, tot);
+    for (long long c = 0; c < nfull; ++c)
+      a.units[f + c] = AttnUnit{(int32_t)b, (int32_t)c, a.chunk, (int32_t)qb, q0, kvl};
+    carry += tot;
+  }
+  // first slot of each partial size, largest first: thread t takes size chunk - 1 - t
+  {
+    const int r = a.chunk - 1 - tid;
+    const long long cnt = r >= 1 ? sBin[r] : 0;
+    long long tot;
+    const long long ex = va_block_scan(cnt, sWave, tot);
+    if (r >= 1) sBin[r] = (int)(carry + ex);
+    __syncthreads();
+    carry += tot;  // all chunks
+  }
+  for (int64_t b = tid; b < a.batch; b += VA_PLAN_NT) {
+    int64_t q0, qb, kvl;
+    if (!va_row(a, b, q0, qb, kvl) || qb <= 0) continue;
+    const int rem = (int)(kvl % a.chunk);
+    if (rem == 0) continue;
+    const int at = atomicAdd(&sBin[rem], 1);
+    a.units[at] = AttnUnit{(int32_t)b, (int32_t)(kvl / a.chunk), rem, (int32_t)qb, q0, kvl};
+  }
+  for (int64_t u = carry + tid; u < a.nunits; u += VA_PLAN_NT) a.units[u].b = -1;
+}
+
 __global__ void __launch_bounds__(VA_NT) __attribute__((amdgpu_waves_per_eu(3)))
 verify_attn_kernel(AttnArgs a) {
   __shared__ __align__(16) uint16_t sK[VA_TOK][VA_KS];
@@ -91,32 +178,19 @@ verify_attn_kernel(AttnArgs a) {
   __shared__ int64_t sRow[VA_MAXM];  // query row i -> element offset of its q / out vector
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
-  const int64_t rows = a.batch * a.hkv;
-  const int c = (int)(blockIdx.x / rows);
-  const int64_t slot = (blockIdx.x % rows) / a.hkv;
   const int kvh = (int)(blockIdx.x % a.hkv);
-  const int64_t b = a.row_order ? (int64_t)a.row_order[slot] : slot;
-  if (b < 0 || b >= a.batch) {  // uniform: a row order outside [0, batch)
-    if (c == 0 && tid == 0 && a.error) *a.error = 1;
-    return;
-  }
+  const AttnUnit un = a.units[blockIdx.x / a.hkv];
+  if (un.b < 0) return;  // uniform: no chunk in this slot
+  const int64_t b = un.b, q0 = un.q0, qb = un.qb, kvl = un.kvl;
+  const int c = un.c, n = un.n;
   const int64_t c0 = (int64_t)c * a.chunk;
   const int64_t p0 = c0 / a.bs;  // first page of the chunk
-  if (p0 >= a.max_blocks) return;  // past every row the block table can hold
-  // the row's shape and the chunk's page ids are fetched together: the ids of
-  // every page the chunk can touch go to LDS (in the V tile's space, unused yet)
-  const int64_t q0 = a.cu_q[b], qb = a.cu_q[b + 1] - q0, kvl = a.kv_len[b];
-  const int np = (int)min((int64_t)(a.chunk / a.bs + 2), a.max_blocks - p0);
+  const int np = (int)((c0 + n - 1) / a.bs - p0 + 1);
+  // the chunk's page ids go to LDS (in the V tile's space, unused yet)
   int32_t* sPage = reinterpret_cast<int32_t*>(&sVt[0][0]);
   for (int i = tid; i < np; i += VA_NT) sPage[i] = a.block_table[b * a.max_blocks + p0 + i];
   const int64_t base = kvl - qb;
-  if (qb < 0 || qb > a.max_q || base < 0 || (kvl + a.bs - 1) / a.bs > a.max_blocks) {
-    if (c == 0 && tid == 0 && a.error) *a.error = 1;  // uniform: a row the launch cannot serve
-    return;
-  }
   const int M = (int)qb * a.group;
-  if (c0 >= kvl || M == 0) return;  // no such chunk, or no queries
-  const int n = (int)min((int64_t)a.chunk, kvl - c0);
   const bool whole = kvl <= a.chunk;  // the row is one chunk: write the output directly
   // row i = j * group + g is query head kvh * group + g of position j
   if (tid < M) sRow[tid] = ((q0 + tid / a.group) * a.hq + kvh * a.group + tid % a.group) * VA_D;
@@ -420,9 +494,11 @@ int attn_chunk_tokens(int64_t batch, int32_t hkv, int64_t max_tokens, int32_t ch
 }
 
 hipError_t launch_verify_attn(const AttnArgs& a, int64_t batch, hipStream_t s) {
-  hipLaunchKernelGGL(verify_attn_kernel, dim3((unsigned)(a.nchunk * batch * a.hkv)), dim3(VA_NT), 0,
-                     s, a);
+  hipLaunchKernelGGL(verify_attn_plan_kernel, dim3(1), dim3(VA_PLAN_NT), 0, s, a);
   hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(verify_attn_kernel, dim3((unsigned)(a.nunits * a.hkv)), dim3(VA_NT), 0, s, a);
+  e = hipGetLastError();
   if (e != hipSuccess || a.nchunk == 1) return e;
   hipLaunchKernelGGL(verify_attn_merge_kernel, dim3((unsigned)(batch * a.hkv)), dim3(VA_NT), 0, s, a);
   return hipGetLastError();

@@ -529,7 +529,9 @@ static int attn_plan(int64_t batch, int32_t max_q, int32_t num_q_heads, int32_t 
                 (long long)(nch * batch * num_kv_heads));
   *chunk = ch;
   *nchunk = (int32_t)nch;
-  *bytes = nch > 1 ? (size_t)(batch * num_kv_heads * nch * m) * (128 + 2) * sizeof(float) : 0;
+  // the chunk list, then (rows of several chunks) the parts
+  const size_t units = ((size_t)(batch * nch) * sizeof(sdx::AttnUnit) + 15) & ~(size_t)15;
+  *bytes = units + (nch > 1 ? (size_t)(batch * num_kv_heads * nch * m) * (128 + 2) * sizeof(float) : 0);
   return SDX_OK;
 }
 
@@ -548,8 +550,8 @@ int sdx_verify_attention_paged(const void* q, int dtype, int64_t batch, const in
                                int32_t max_q, int32_t num_q_heads, int32_t num_kv_heads,
                                int32_t head_dim, const void* k_pool, const void* v_pool,
                                int64_t num_blocks, int32_t block_size, const int32_t* block_table,
-                               int64_t max_blocks, const int64_t* kv_len, const int32_t* row_order,
-                               float scale, int32_t chunk_tokens, void* workspace,
+                               int64_t max_blocks, const int64_t* kv_len, float scale,
+                               int32_t chunk_tokens, void* workspace,
                                size_t workspace_bytes, void* out, int32_t* error,
                                sdx_stream_t stream) {
   if (!q || !cu_q || !k_pool || !v_pool || !block_table || !kv_len || !out || num_blocks < 1 ||
@@ -571,9 +573,11 @@ int sdx_verify_attention_paged(const void* q, int dtype, int64_t batch, const in
     return fail(SDX_EUNSUPPORTED, "sdx_verify_attention_paged: pool of 2^32 or more head slices");
   if (!aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool) || !aligned16(out))
     return fail(SDX_EINVAL, "sdx_verify_attention_paged: tensors must be 16-byte aligned");
-  if (need > 0 && (!workspace || workspace_bytes < need || !aligned16(workspace)))
-    return fail(SDX_EINVAL, "sdx_verify_attention_paged: needs a 16-byte aligned workspace of "
-                            "%zu bytes (got %zu)", need, workspace ? workspace_bytes : (size_t)0);
+  if (!workspace || !aligned16(workspace))
+    return fail(SDX_EINVAL, "sdx_verify_attention_paged: needs a 16-byte aligned workspace");
+  if (workspace_bytes < need)
+    return fail(SDX_EWORKSPACE, "sdx_verify_attention_paged: needs a workspace of %zu bytes "
+                                "(got %zu)", need, workspace_bytes);
   if (batch == 0) return SDX_OK;
   sdx::AttnArgs a = {};
   a.q = (const uint16_t*)q;
@@ -582,7 +586,6 @@ int sdx_verify_attention_paged(const void* q, int dtype, int64_t batch, const in
   a.v_pool = (const uint16_t*)v_pool;
   a.block_table = block_table;
   a.kv_len = kv_len;
-  a.row_order = row_order;
   a.batch = batch;
   a.out = (uint16_t*)out;
   a.error = error;
@@ -596,9 +599,12 @@ int sdx_verify_attention_paged(const void* q, int dtype, int64_t batch, const in
   a.chunk = ch;
   a.nchunk = nch;
   a.max_m = max_q * group;
+  a.nunits = batch * (int64_t)nch;
+  const size_t ubytes = ((size_t)a.nunits * sizeof(sdx::AttnUnit) + 15) & ~(size_t)15;
+  a.units = (sdx::AttnUnit*)workspace;
   const int64_t nparts = batch * num_kv_heads * (int64_t)nch * a.max_m;
-  a.part_o = need > 0 ? (float*)workspace : nullptr;
-  a.part_ml = need > 0 ? (float*)workspace + nparts * 128 : nullptr;
+  a.part_o = nch > 1 ? (float*)((char*)workspace + ubytes) : nullptr;
+  a.part_ml = nch > 1 ? a.part_o + nparts * 128 : nullptr;
   a.scale_log2 = scale * 1.4426950408889634f;
   return hip_status(sdx::launch_verify_attn(a, batch, (hipStream_t)stream), "verify_attn");
 }

@@ -47,7 +47,7 @@ _SIGS = {
     "sdx_kv_append_paged": (INT, [P, I64, I64, P, INT, I32, I64, I64, I64, P, I64, I32, I64, P,
                                   P, P]),
     "sdx_verify_attention_paged": (INT, [P, INT, I64, P, I32, I32, I32, I32, P, P, I64, I32, P,
-                                         I64, P, P, F, I32, P, SZ, P, P, P]),
+                                         I64, P, F, I32, P, SZ, P, P, P]),
     "sdx_verify_attention_workspace": (SZ, [I64, I32, I32, I32, I32, I64, I32]),
 }
 

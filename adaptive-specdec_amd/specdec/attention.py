@@ -22,11 +22,13 @@ def attention_workspace(B, max_q, hq, hkv, block_size, max_blocks, chunk_tokens=
     """A workspace for verify_attention_paged at these sizes (uint8 device tensor)."""
     need = _lib.lib().sdx_verify_attention_workspace(B, int(max_q), hq, hkv, block_size,
                                                      max_blocks, int(chunk_tokens))
-    return torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+    if need == 0:
+        _lib.check(-1, "verify_attention workspace query")
+    return torch.empty(need, dtype=torch.uint8, device=device)
 
 
 def verify_attention_paged(q, cu_q, k_pool, v_pool, block_table, kv_len, max_q, scale=None,
-                           out=None, error=None, row_order=None, chunk_tokens=0, workspace=None):
+                           out=None, error=None, chunk_tokens=0, workspace=None):
     """q [T, Hq, 128] bf16 (T = cu_q[-1]); cu_q [B+1] int64; k_pool / v_pool
     [num_blocks, block_size, Hkv * 128] bf16 (one layer's K and V sides of a
     PagedKVCache pool); block_table [B, max_blocks] int32; kv_len [B] int64 (keys
@@ -35,8 +37,8 @@ def verify_attention_paged(q, cu_q, k_pool, v_pool, block_table, kv_len, max_q, 
     skipped and set `error` (an int32 [1] device tensor) when given. Each row's
     keys are split in chunks of `chunk_tokens` (0: the library's default) on
     separate workgroups; rows of several chunks merge fp32 partials held in
-    `workspace` (a uint8 device tensor, allocated here when None). Rows are
-    launched longest context first unless `row_order` (int32 [B]) is given."""
+    `workspace` (a uint8 device tensor, allocated here when None); the chunks
+    are launched longest first."""
     _lib.require_gpu(q, cu_q, k_pool, v_pool, block_table, kv_len)
     if q.dtype != torch.bfloat16 or k_pool.dtype != torch.bfloat16 or v_pool.dtype != torch.bfloat16:
         raise TypeError("verify_attention_paged: bf16 q and pools")
@@ -53,19 +55,14 @@ def verify_attention_paged(q, cu_q, k_pool, v_pool, block_table, kv_len, max_q, 
     cu = cu_q.to(torch.int64).contiguous()
     kl = kv_len.to(torch.int64).contiguous()
     bt = block_table.to(torch.int32).contiguous()
-    if row_order is None:
-        row_order = torch.argsort(kl, descending=True).to(torch.int32)
-    row_order = row_order.to(torch.int32).contiguous()
     if out is None:
         out = torch.empty_like(q)
-    need = _lib.lib().sdx_verify_attention_workspace(B, int(max_q), hq, hkv, bs, bt.shape[1],
-                                                     int(chunk_tokens))
-    if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    if workspace is None:
+        workspace = attention_workspace(B, max_q, hq, hkv, bs, bt.shape[1], chunk_tokens, q.device)
     rc = _lib.lib().sdx_verify_attention_paged(
         _lib.ptr(q), _lib.BF16, B, _lib.ptr(cu), int(max_q), hq, hkv, d,
         _lib.ptr(k_pool), _lib.ptr(v_pool), nb, bs, _lib.ptr(bt),
-        bt.shape[1], _lib.ptr(kl), _lib.ptr(row_order), scale, int(chunk_tokens),
+        bt.shape[1], _lib.ptr(kl), scale, int(chunk_tokens),
         _lib.ptr(workspace), workspace.numel(), _lib.ptr(out), _lib.ptr(error), _lib.stream_of(q))
     _lib.check(rc, "verify_attention_paged")
     return out

@@ -189,27 +189,26 @@ int sdx_kv_append_paged(void* pool, int64_t layer_stride, int64_t side_stride,
  * query head h reads KV head h / (num_q_heads / num_kv_heads). Pools: [num_blocks,
  * block_size, num_kv_heads * head_dim] bf16 (the K and V sides of one layer of
  * sdx_kv_append_paged's pool); block_table [batch, max_blocks] int32; cu_q and
- * kv_len int64 on the device; row_order (nullable, int32 [batch]) gives the order
- * in which rows are launched (any permutation gives the same output).
- * softmax(q k^T * scale) v in fp32, P rounded to bf16 for the P V product, output
- * rounded to bf16. The keys of a row are split in chunks of chunk_tokens (0: the
- * library's default for the shape; else a multiple of 64, at most 1024) handled by
- * separate workgroups; rows of more than one chunk merge fp32 partials in
- * `workspace` (sdx_verify_attention_workspace bytes, 16-byte aligned; none needed
- * when that is 0). A row whose shape is out of range sets *error (nullable) and is
- * skipped; page ids outside the pool set *error and the row's output is unspecified.
- * bf16, head_dim 128, max_q * (num_q_heads / num_kv_heads) <= 64. */
+ * kv_len int64 on the device. softmax(q k^T * scale) v in fp32, P rounded to
+ * bf16 for the P V product, output rounded to bf16. The keys of a row are split
+ * in chunks of chunk_tokens (0: the library's default for the shape; else a
+ * multiple of 64, at most 1024) handled by separate workgroups, longest chunks
+ * first; rows of more than one chunk merge fp32 partials. `workspace` holds the
+ * chunk list and the partials (sdx_verify_attention_workspace bytes, 16-byte
+ * aligned, no initial contents). Three kernels are queued on `stream`. A row
+ * whose shape is out of range sets *error (nullable) and is skipped; page ids
+ * outside the pool set *error and the row's output is unspecified. bf16,
+ * head_dim 128, max_q * (num_q_heads / num_kv_heads) <= 64. */
 int sdx_verify_attention_paged(const void* q, int dtype, int64_t batch, const int64_t* cu_q,
                                int32_t max_q, int32_t num_q_heads, int32_t num_kv_heads,
                                int32_t head_dim, const void* k_pool, const void* v_pool,
                                int64_t num_blocks, int32_t block_size, const int32_t* block_table,
-                               int64_t max_blocks, const int64_t* kv_len, const int32_t* row_order,
-                               float scale, int32_t chunk_tokens, void* workspace,
-                               size_t workspace_bytes, void* out, int32_t* error,
-                               sdx_stream_t stream);
+                               int64_t max_blocks, const int64_t* kv_len, float scale,
+                               int32_t chunk_tokens, void* workspace, size_t workspace_bytes,
+                               void* out, int32_t* error, sdx_stream_t stream);
 
 /* Workspace bytes sdx_verify_attention_paged needs for these sizes and chunk_tokens
- * (0 on invalid arguments, or when every row fits one chunk). */
+ * (0 on invalid arguments). */
 size_t sdx_verify_attention_workspace(int64_t batch, int32_t max_q, int32_t num_q_heads,
                                       int32_t num_kv_heads, int32_t block_size,
                                       int64_t max_blocks, int32_t chunk_tokens);
