@@ -187,10 +187,10 @@ def bench_verify(args, torch):
     return result
 
 
-def traffic_per_launch():
+def traffic_per_launch(name="traffic_verify.json"):
     """HBM bytes per launch of the dominant kernel, from the committed rocprofv3
     FETCH_SIZE/WRITE_SIZE summary (scaled by the copy-kernel calibration), or None."""
-    p = os.path.join(REPO, "profiles", "traffic_verify.json")
+    p = os.path.join(REPO, "profiles", name)
     try:
         with open(p) as f:
             return json.load(f).get("bytes_per_launch")
@@ -314,8 +314,17 @@ def bench_attn(args, torch):
     for _ in range(args.warmup):
         call()
     torch.cuda.synchronize()
-    g = capture(call, torch)
-    ms = timed_graphs([g], args.steps, torch)
+    if args.no_graph:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+    else:
+        g = capture(call, torch)
+        ms = timed_graphs([g], args.steps, torch)
     kv_tokens = int(inp["kv_len"].sum().item())
     d, hkv, hq = inp["d"], inp["hkv"], inp["hq"]
     T = int(inp["cu_q"][-1].item())
@@ -332,9 +341,12 @@ def bench_attn(args, torch):
                        "batch": B, "query_rows": T, "kv_tokens": kv_tokens,
                        "chunk_tokens": args.attn_chunk,
                        "mean_k": round(float(inp["k"].float().mean()), 3)},
-            "roofline": {"bound": "hbm", "kernel": "verify_attn_kernel",
+            "roofline": {"bound": "hbm",
+                         "kernel": "whole call: verify_attn_plan + verify_attn_kernel + "
+                                   "verify_attn_merge",
                          "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                         "frac": round(ach / HBM_PEAK_GBS, 4),
+                         "traffic": traffic_per_launch("traffic_attn.json"),
                          "algorithmic_bytes": alg, "avg_launch_us": round(ms * 1e3, 2),
                          "mfma_tflops": round(flops / (ms / 1e3) / 1e12, 2)},
             "cpu_baseline": None}
