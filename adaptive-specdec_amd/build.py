@@ -53,7 +53,8 @@ def build(jobs=None, verbose=False):
     with cf.ThreadPoolExecutor(jobs) as ex:
         objs = list(ex.map(lambda s: compile_one(cc, s), srcs))
     tmp = OUT + ".tmp"
-    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    # -z defs: an undefined symbol fails the link here instead of the first load
+    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")

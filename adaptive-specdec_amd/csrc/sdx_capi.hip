@@ -270,16 +270,32 @@ int sdx_gather_prob(const float* probs, int64_t rows, int64_t vocab, int64_t ld,
 }
 
 // ------------------------------------------------------------------ verify
-size_t sdx_verify_workspace(int64_t batch, int32_t k, int64_t vocab, int dtype) {
+// verify workspace for ntgt target and ndrf draft rows (per-row k adds the
+// target row map and the bad-row bytes)
+static size_t verify_ws_bytes(int64_t batch, int64_t ntgt, int64_t ndrf, int64_t vocab, int dtype,
+                              bool ragged) {
   Carve c{nullptr};
   sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; sdx::ChunkRec* rc; uint32_t* ct;
   uint64_t* ra;
-  const int64_t rows = batch * (2 * (int64_t)k + 1);
+  const int64_t rows = ntgt + ndrf;
   transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jb, &rc, &ct, &ra);
-  c.take<int64_t>(batch * ((int64_t)k + 1));  // greedy argmax
+  c.take<int64_t>(ntgt);  // greedy argmax
   // rows split over blocks (counters that stay zero between calls, part histograms)
   c.take<uint8_t>(dtype == SDX_BF16 ? sdx::rowstream_split_bytes(rows, vocab) : 0);
+  if (ragged) {
+    c.take<int64_t>(ntgt);
+    c.take<uint8_t>(batch);
+  }
   return c.used;
+}
+
+size_t sdx_verify_workspace(int64_t batch, int32_t k, int64_t vocab, int dtype) {
+  return verify_ws_bytes(batch, batch * ((int64_t)k + 1), batch * (int64_t)k, vocab, dtype, false);
+}
+
+size_t sdx_verify_ragged_workspace(int64_t batch, int64_t target_rows, int64_t vocab, int dtype) {
+  if (batch < 0 || target_rows < batch) return 0;
+  return verify_ws_bytes(batch, target_rows, target_rows - batch, vocab, dtype, true);
 }
 
 static int verify_impl(const void* target_logits, const void* draft_logits, int dtype,
@@ -287,7 +303,8 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
                        const float* u_accept, const float* u_final, const uint8_t* active,
                        float temperature, float top_p, int32_t top_k, int64_t* n_acc, int64_t* y,
                        uint8_t* flags, void* workspace, size_t workspace_bytes,
-                       sdx_stream_t stream, bool stats_only);
+                       sdx_stream_t stream, bool stats_only, const int64_t* cu_k = nullptr,
+                       int64_t target_rows = 0);
 
 int sdx_verify(const void* target_logits, const void* draft_logits, int dtype, int64_t batch,
                int32_t k, int64_t vocab, const int64_t* draft_ids, const float* u_accept,
@@ -298,6 +315,22 @@ int sdx_verify(const void* target_logits, const void* draft_logits, int dtype, i
   return verify_impl(target_logits, draft_logits, dtype, batch, k, vocab, draft_ids, u_accept,
                      u_final, active, temperature, top_p, top_k, n_acc, y, flags, workspace,
                      workspace_bytes, stream, false);
+}
+
+int sdx_verify_ragged(const void* target_logits, const void* draft_logits, int dtype,
+                      int64_t batch, int32_t k_max, int64_t target_rows, int64_t vocab,
+                      const int64_t* cu_k, const int64_t* draft_ids, const float* u_accept,
+                      const float* u_final, const uint8_t* active, float temperature,
+                      float top_p, int32_t top_k, int64_t* n_acc, int64_t* y, uint8_t* flags,
+                      void* workspace, size_t workspace_bytes, sdx_stream_t stream) {
+  if (!n_acc || !y || !flags || !cu_k || target_rows < batch || k_max < 1)
+    return fail(SDX_EINVAL, "sdx_verify_ragged: bad arguments");
+  if (target_rows - batch > batch * (int64_t)k_max)
+    return fail(SDX_EINVAL, "sdx_verify_ragged: %lld draft rows exceed batch * k_max",
+                (long long)(target_rows - batch));
+  return verify_impl(target_logits, draft_logits, dtype, batch, k_max, vocab, draft_ids, u_accept,
+                     u_final, active, temperature, top_p, top_k, n_acc, y, flags, workspace,
+                     workspace_bytes, stream, false, cu_k, target_rows);
 }
 
 int sdx_verify_stats(const void* target_logits, const void* draft_logits, int dtype,
@@ -317,13 +350,17 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
                        const float* u_accept, const float* u_final, const uint8_t* active,
                        float temperature, float top_p, int32_t top_k, int64_t* n_acc, int64_t* y,
                        uint8_t* flags, void* workspace, size_t workspace_bytes,
-                       sdx_stream_t stream, bool stats_only) {
+                       sdx_stream_t stream, bool stats_only, const int64_t* cu_k,
+                       int64_t target_rows) {
   if (!target_logits || (!draft_ids && !stats_only) || !u_accept || !u_final || batch < 0 ||
       k < 1 || !dtype_ok(dtype))
     return fail(SDX_EINVAL, "sdx_verify: bad arguments");
   if (int e = check_vocab(dtype, vocab)) return e;
   if (batch == 0) return SDX_OK;
-  const size_t need = sdx_verify_workspace(batch, k, vocab, dtype);
+  // per-row k: target rows [sum (k_b + 1)], draft rows [sum k_b]
+  const int64_t ntgt = cu_k ? target_rows : batch * ((int64_t)k + 1);
+  const int64_t ndrf = cu_k ? target_rows - batch : batch * (int64_t)k;
+  const size_t need = verify_ws_bytes(batch, ntgt, ndrf, vocab, dtype, cu_k != nullptr);
   if (!workspace || workspace_bytes < need)
     return fail(SDX_EWORKSPACE, "sdx_verify: workspace %zu < %zu", workspace_bytes, need);
   hipStream_t s = (hipStream_t)stream;
@@ -332,12 +369,20 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
   sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jobs; sdx::ChunkRec* recs;
   uint32_t* counters;
   uint64_t* rank_acc;
-  const int64_t ntgt = batch * ((int64_t)k + 1), ndrf = batch * (int64_t)k;
   const int64_t rows = ntgt + ndrf;
   transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jobs, &recs, &counters, &rank_acc);
   int64_t* am = c.take<int64_t>(ntgt);
   const size_t split_bytes = dtype == SDX_BF16 ? sdx::rowstream_split_bytes(rows, vocab) : 0;
   uint8_t* split_ws = c.take<uint8_t>(split_bytes);
+  int64_t* tgt_idx = nullptr;
+  uint8_t* bad = nullptr;
+  if (cu_k) {
+    tgt_idx = c.take<int64_t>(ntgt);
+    bad = c.take<uint8_t>(batch);
+    if (int e = hip_status(sdx::launch_ragged_rows(cu_k, batch, k, ntgt, ndrf, tgt_idx, bad, s),
+                           "ragged_rows"))
+      return e;
+  }
   if (sw.greedy) {
     // one-hot p: only the target argmax matters (see sdx_verify_greedy)
     const bool vec = aligned16(target_logits) && (vocab % (dtype == SDX_F32 ? 4 : 8)) == 0;
@@ -345,7 +390,7 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
                            "argmax"))
       return e;
     return hip_status(sdx::launch_greedy_accept(am, batch, k, draft_ids, u_accept, active, n_acc,
-                                                y, flags, s),
+                                                y, flags, s, cu_k, bad),
                       "greedy_accept");
   }
   if (!draft_logits) return fail(SDX_EINVAL, "sdx_verify: draft_logits required when T > 0");
@@ -353,7 +398,7 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
     sdx::F32Args a = {};
     a.base[0] = (const float*)target_logits; a.nrows[0] = ntgt; a.ld[0] = vocab;
     a.base[1] = (const float*)draft_logits; a.nrows[1] = ndrf; a.ld[1] = vocab;
-    a.V = vocab; a.ids = draft_ids; a.k = k;
+    a.V = vocab; a.ids = draft_ids; a.k = k; a.tgt_idx = tgt_idx;
     a.T = temperature; a.top_p = top_p; a.top_k = top_k;
     a.use_p = sw.use_p; a.use_k = sw.use_k; a.greedy = 0;
     a.out = dn; a.ld_out = vocab; a.stats = st;
@@ -366,7 +411,7 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
     sdx::RowStatArgs a = {};
     a.base[0] = (const uint16_t*)target_logits; a.nrows[0] = ntgt; a.ld[0] = vocab;
     a.base[1] = (const uint16_t*)draft_logits; a.nrows[1] = ndrf; a.ld[1] = vocab;
-    a.V = vocab; a.ids = draft_ids; a.k = k;
+    a.V = vocab; a.ids = draft_ids; a.k = k; a.tgt_idx = tgt_idx;
     a.T = temperature; a.top_p = top_p; a.top_k = top_k;
     a.use_p = sw.use_p; a.use_k = sw.use_k; a.greedy = 0;
     a.stats = st; a.tables = tb;
@@ -382,7 +427,8 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
       if (int e = hip_status(sdx::launch_rank_bf16(a, rows, s), "rank_bf16")) return e;
   }
   if (stats_only) return SDX_OK;
-  sdx::AcceptArgs aa{st, batch, k, u_accept, u_final, active, jobs, n_acc, flags, draft_ids};
+  sdx::AcceptArgs aa{st,    batch, k,         u_accept, u_final, active, jobs,
+                     n_acc, flags, draft_ids, cu_k,     bad,     ntgt};
   if (dtype == SDX_F32) {
     sdx::RowSourceF32 src{dn, vocab, dn, vocab, rows, (vocab % 4) == 0};
     return hip_status(sdx::launch_draw_probs(src, &aa, jobs, batch, vocab, recs,

@@ -275,4 +275,20 @@ __device__ __forceinline__ U128 wave_sum_u128(U128 v) {
   return v;
 }
 
+// Drafted id whose probability row `r` of group g gathers: target rows (g = 0)
+// are [batch, k+1] with position i < k gathering ids[b k + i] (the bonus
+// position none), or, with per-row k, tgt_idx[r] indexes ids (-1: bonus);
+// draft rows (g = 1) gather ids[r]. -1 when there is none.
+__device__ __forceinline__ int64_t draft_id_of_row(const int64_t* ids, const int64_t* tgt_idx,
+                                                   int32_t k, int64_t ndrf, int g, int64_t r) {
+  if (!ids) return -1;
+  if (g) return ids[r];
+  if (tgt_idx) {
+    const int64_t x = tgt_idx[r];
+    return (x >= 0 && x < ndrf) ? ids[x] : -1;
+  }
+  const int64_t b = r / (k + 1), i = r % (k + 1);
+  return i < k ? ids[b * k + i] : -1;
+}
+
 }  // namespace sdx

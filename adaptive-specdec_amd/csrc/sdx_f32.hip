@@ -42,15 +42,7 @@ __global__ void __launch_bounds__(F32_NT) to_probs_f32_kernel(F32Args a) {
   const int64_t r = g ? row - a.nrows[0] : row;
   const float* x = a.base[g] + r * a.ld[g];
   const int V = (int)a.V;
-  int64_t gid = -1;
-  if (a.ids) {
-    if (g == 0) {
-      const int64_t b = r / (a.k + 1), i = r % (a.k + 1);
-      if (i < a.k) gid = a.ids[b * a.k + i];
-    } else {
-      gid = a.ids[r];
-    }
-  }
+  const int64_t gid = draft_id_of_row(a.ids, a.tgt_idx, a.k, a.nrows[1], g, r);
   float* o = a.out + row * a.ld_out;
 
   float v[F32_PER];

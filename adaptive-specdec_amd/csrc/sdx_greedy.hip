@@ -83,20 +83,35 @@ __global__ void __launch_bounds__(AM_NT) argmax_kernel(const void* data, int64_t
   }
 }
 
-// Greedy accept: argmax of target rows [batch, k+1] already in `am`.
+// Greedy accept: argmax of target rows [batch, k+1] already in `am`. With
+// per-row k (cu_k non-null) row b has k_b = cu_k[b+1] - cu_k[b] positions, its
+// target rows start at cu_k[b] + b and its drafted ids / uniforms at cu_k[b];
+// bad[b] marks a row whose offsets failed the check (n_acc 0, y -1, flag set).
 __global__ void greedy_accept_kernel(const int64_t* am, int64_t batch, int32_t k,
                                      const int64_t* ids, const float* u_accept,
                                      const uint8_t* active, int64_t* n_acc, int64_t* y,
-                                     uint8_t* flags) {
+                                     uint8_t* flags, const int64_t* cu_k, const uint8_t* bad) {
   const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= batch) return;
+  int64_t t0 = b * (k + 1), i0 = b * k;
+  if (cu_k) {
+    if (bad[b]) {
+      n_acc[b] = 0;
+      y[b] = -1;
+      flags[b] = (uint8_t)SDX_FLAG_BAD_ROW;
+      return;
+    }
+    i0 = cu_k[b];
+    t0 = i0 + b;
+    k = (int32_t)(cu_k[b + 1] - i0);
+  }
   bool alive = active ? active[b] != 0 : true;
   int n = 0;
   uint32_t fl = 0;
   for (int i = 0; i < k; ++i) {
     // p is one-hot at the argmax, q(x) = 1: ratio = p(x) in {0, 1}
-    const float r1 = ids[b * k + i] == am[b * (k + 1) + i] ? 1.0f : 0.0f;
-    const float u = u_accept ? u_accept[b * k + i] : 0.0f;
+    const float r1 = ids[i0 + i] == am[t0 + i] ? 1.0f : 0.0f;
+    const float u = u_accept ? u_accept[i0 + i] : 0.0f;
     const bool evaluated = alive && n == i;
     const bool ok = evaluated && (u < r1);
     if (evaluated && fabsf(u - r1) < 1e-5f) fl |= SDX_FLAG_ACCEPT_NEAR_TIE;
@@ -104,7 +119,7 @@ __global__ void greedy_accept_kernel(const int64_t* am, int64_t batch, int32_t k
     alive = alive && ok;
   }
   n_acc[b] = n;
-  y[b] = am[b * (k + 1) + n];
+  y[b] = am[t0 + n];
   flags[b] = (uint8_t)fl;
 }
 
@@ -139,10 +154,40 @@ hipError_t launch_argmax(int dtype, const void* data, int64_t rows, int64_t V, i
 
 hipError_t launch_greedy_accept(const int64_t* am, int64_t batch, int32_t k, const int64_t* ids,
                                 const float* u_accept, const uint8_t* active, int64_t* n_acc,
-                                int64_t* y, uint8_t* flags, hipStream_t s) {
+                                int64_t* y, uint8_t* flags, hipStream_t s, const int64_t* cu_k,
+                                const uint8_t* bad) {
   const int nt = 128;
   hipLaunchKernelGGL(greedy_accept_kernel, dim3((unsigned)((batch + nt - 1) / nt)), dim3(nt), 0,
-                     s, am, batch, k, ids, u_accept, active, n_acc, y, flags);
+                     s, am, batch, k, ids, u_accept, active, n_acc, y, flags, cu_k, bad);
+  return hipGetLastError();
+}
+
+// Per-row k: one workgroup checks cu_k (cu_k[0] = 0, cu_k[batch] = ndrf, non-
+// decreasing, every k_b <= k_max) and maps each target row to the drafted id
+// it gathers. Inconsistent offsets mark every row bad: rows then overlap, so
+// none of their row sets can be trusted.
+__global__ void __launch_bounds__(1024) ragged_rows_kernel(const int64_t* cu_k, int64_t batch,
+                                                          int32_t k_max, int64_t ntgt,
+                                                          int64_t ndrf, int64_t* tgt_idx,
+                                                          uint8_t* bad) {
+  int ok = cu_k[0] == 0 && cu_k[batch] == ndrf && ndrf + batch == ntgt;
+  for (int64_t b = threadIdx.x; b < batch; b += blockDim.x) {
+    const int64_t kb = cu_k[b + 1] - cu_k[b];
+    ok &= kb >= 0 && kb <= k_max;
+  }
+  ok = __syncthreads_and(ok);
+  for (int64_t b = threadIdx.x; b < batch; b += blockDim.x) {
+    bad[b] = ok ? 0 : 1;
+    if (!ok) continue;
+    const int64_t c0 = cu_k[b], kb = cu_k[b + 1] - c0;
+    for (int64_t i = 0; i <= kb; ++i) tgt_idx[c0 + b + i] = i < kb ? c0 + i : -1;
+  }
+}
+
+hipError_t launch_ragged_rows(const int64_t* cu_k, int64_t batch, int32_t k_max, int64_t ntgt,
+                              int64_t ndrf, int64_t* tgt_idx, uint8_t* bad, hipStream_t s) {
+  hipLaunchKernelGGL(ragged_rows_kernel, dim3(1), dim3(1024), 0, s, cu_k, batch, k_max, ntgt, ndrf,
+                     tgt_idx, bad);
   return hipGetLastError();
 }
 

@@ -13,6 +13,7 @@ struct RowStatArgs {
   int64_t V;
   const int64_t* ids;  // draft ids [batch, k] (gather source), or null
   int32_t k;           // target rows are [batch, k+1], draft rows [batch, k]
+  const int64_t* tgt_idx;  // per-row k: target row -> index into ids (-1: bonus), or null
   float T;
   float top_p;
   int32_t top_k;
@@ -43,6 +44,7 @@ struct F32Args {
   int64_t V;
   const int64_t* ids;
   int32_t k;
+  const int64_t* tgt_idx;  // per-row k: target row -> index into ids (-1: bonus), or null
   float T, top_p;
   int32_t top_k, use_p, use_k, greedy;
   float* out;  // dense probabilities [rows, ld_out]
@@ -63,15 +65,34 @@ struct SampleJob {
 struct AcceptArgs {
   const RowStat* stats;  // target rows [batch*(k+1)] then draft rows [batch*k]
   int64_t batch;
-  int32_t k;
-  const float* u_accept;  // [batch, k]
+  int32_t k;              // k, or with per-row k its maximum
+  const float* u_accept;  // [batch, k] (per-row k: [sum k_b], row b from cu_k[b])
   const float* u_final;   // [batch]
   const uint8_t* active;  // [batch] or null
   SampleJob* jobs;        // [batch]
   int64_t* n_acc;
   uint8_t* flags;
   const int64_t* draft_ids;  // [batch, k] (16-bit rows: ranks of flagged drafted tokens)
+  // per-row k (null: uniform k): row b drafts k_b = cu_k[b+1] - cu_k[b] tokens; its
+  // target rows start at cu_k[b] + b, its draft rows at ntgt + cu_k[b]; bad[b] marks
+  // a row whose offsets are inconsistent (checked by ragged_rows_kernel)
+  const int64_t* cu_k;
+  const uint8_t* bad;
+  int64_t ntgt;  // target rows (the draft rows' RowStats follow them)
 };
+// Where batch row b's rows are: its k, first target and draft rows, the offset of
+// its drafted ids / accept uniforms; bad rows get k = 0 on row 0
+struct RowGeom {
+  int k;
+  int64_t trow0, drow0, ibase;
+  bool bad;
+};
+__device__ __forceinline__ RowGeom row_geom(const AcceptArgs& a, int64_t b) {
+  if (!a.cu_k) return RowGeom{a.k, b * (a.k + 1), a.ntgt + b * a.k, b * a.k, false};
+  if (a.bad[b]) return RowGeom{0, 0, a.ntgt, 0, true};
+  const int64_t c0 = a.cu_k[b];
+  return RowGeom{(int)(a.cu_k[b + 1] - c0), c0 + b, a.ntgt + c0, c0, false};
+}
 
 // Partial sums of one draw over one chunk of ids, before the member ranks of
 // the boundary tie groups are known (f = fixed62, vp / vq = group values of
@@ -155,9 +176,14 @@ hipError_t launch_argmax(int dtype, const void* data, int64_t rows, int64_t V, i
                          bool vec, int64_t* out, hipStream_t s);
 hipError_t launch_onehot(const int64_t* am, int64_t rows, int64_t V, float* out, int64_t ld_out,
                          hipStream_t s);
+// per-row k: validates cu_k [batch+1] against k_max and the row counts; writes
+// tgt_idx [ntgt] (target row -> index into the drafted ids, -1: bonus) and bad [batch]
+hipError_t launch_ragged_rows(const int64_t* cu_k, int64_t batch, int32_t k_max, int64_t ntgt,
+                              int64_t ndrf, int64_t* tgt_idx, uint8_t* bad, hipStream_t s);
 hipError_t launch_greedy_accept(const int64_t* am, int64_t batch, int32_t k, const int64_t* ids,
                                 const float* u_accept, const uint8_t* active, int64_t* n_acc,
-                                int64_t* y, uint8_t* flags, hipStream_t s);
+                                int64_t* y, uint8_t* flags, hipStream_t s,
+                                const int64_t* cu_k = nullptr, const uint8_t* bad = nullptr);
 // sdx_attn.hip: multi-query verify attention over paged KV (bf16, head_dim 128)
 struct AttnUnit {   // one key chunk of one row (b < 0: no chunk)
   int32_t b, c, n, qb;  // row, chunk index, tokens in the chunk, query positions of the row

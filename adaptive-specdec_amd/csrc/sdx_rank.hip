@@ -43,13 +43,8 @@ __global__ void __launch_bounds__(RK_NT) rank_bf16_kernel(RowStatArgs a, int64_t
     const int g = row < a.nrows[0] ? 0 : 1;
     const int64_t r = g ? row - a.nrows[0] : row;
     const uint16_t* __restrict__ ptr = a.base[g] + r * a.ld[g];
-    int64_t gid;
-    if (g == 0) {
-      const int64_t b = r / (a.k + 1), ii = r % (a.k + 1);
-      gid = a.ids[b * a.k + ii];  // ii < k: the row kernel flags only rows with a token
-    } else {
-      gid = a.ids[r];
-    }
+    // the row kernel flags only rows with a drafted token (gid >= 0)
+    const int64_t gid = draft_id_of_row(a.ids, a.tgt_idx, a.k, a.nrows[1], g, r);
     const int64_t len = ((gid + RK_SEG - 1) / RK_SEG + 7) / 8 * 8;
     const int64_t x0 = min<int64_t>(gid, (int64_t)s * len), x1 = min<int64_t>(gid, x0 + len);
     const uint32_t glo = (uint32_t)st.glo, span = (uint32_t)(st.ghi - st.glo);
@@ -78,7 +73,7 @@ __global__ void __launch_bounds__(RK_NT) rank_bf16_kernel(RowStatArgs a, int64_t
       if ((uint32_t)prev == (uint32_t)(RK_SEG - 1)) {  // last segment: the full count is known
         const uint32_t rank = (uint32_t)(prev >> 32) + tot;
         float pg = 0.0f;
-        if (rank < (uint32_t)st.rstar) {
+        if (gid >= 0 && rank < (uint32_t)st.rstar) {
           const float d = decode16<SDX_BF16>(ptr[gid]) / a.T - st.m;
           pg = exp_det(d) / st.zf / st.totf;
         }

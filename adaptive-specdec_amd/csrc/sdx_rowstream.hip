@@ -421,15 +421,7 @@ rowstream_bf16_kernel(RowStatArgs a) {
   const int g = row < a.nrows[0] ? 0 : 1;
   const int64_t r = g ? row - a.nrows[0] : row;
   const uint16_t* __restrict__ ptr = a.base[g] + r * a.ld[g];
-  int64_t gid = -1;
-  if (a.ids) {
-    if (g == 0) {
-      const int64_t b = r / (a.k + 1), i = r % (a.k + 1);
-      if (i < a.k) gid = a.ids[b * a.k + i];
-    } else {
-      gid = a.ids[r];
-    }
-  }
+  const int64_t gid = draft_id_of_row(a.ids, a.tgt_idx, a.k, a.nrows[1], g, r);
   const int64_t V = a.V;
   RowStat* st_out = a.stats + row;
   float* tbl_out = a.tables + row * kTbl;

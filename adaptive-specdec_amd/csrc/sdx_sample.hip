@@ -216,12 +216,12 @@ struct EvalProb {
 __device__ inline int64_t accept_chain_wave(const AcceptArgs& a, int64_t b, SampleJob* job,
                                             uint32_t* fl_out) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int k = a.k;
-  const int64_t trow0 = b * (k + 1);
-  const int64_t drow0 = a.batch * (k + 1) + b * k;
-  const bool alive = a.active ? a.active[b] != 0 : true;
+  const RowGeom gm = row_geom(a, b);
+  const int k = gm.k;
+  const int64_t trow0 = gm.trow0, drow0 = gm.drow0;
+  const bool alive = (a.active ? a.active[b] != 0 : true) && !gm.bad;
   int n = alive ? k : 0;
-  uint32_t fl = 0;
+  uint32_t fl = gm.bad ? (uint32_t)SDX_FLAG_BAD_ROW : 0u;
   for (int i0 = 0; alive && n == k && i0 < k; i0 += kWave) {  // uniform loop
     const int i = i0 + lane;
     bool ok = true, near = false;
@@ -229,7 +229,7 @@ __device__ inline int64_t accept_chain_wave(const AcceptArgs& a, int64_t b, Samp
       const float px = a.stats[trow0 + i].pgather;
       const float qx = a.stats[drow0 + i].pgather;
       const float r1 = fminf(px / fmaxf(qx, 1e-10f), 1.0f);
-      const float u = a.u_accept[b * k + i];
+      const float u = a.u_accept[gm.ibase + i];
       ok = u < r1;
       near = fabsf(u - r1) < 1e-5f;
     }
@@ -823,8 +823,9 @@ template <int FMT>
 __device__ inline int64_t chain16_wave(const AcceptArgs& a, const Eval16<FMT>& ev, int64_t b,
                                        SampleJob* job, uint32_t* fl_out, RowStat* st) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int k = a.k;
-  const int64_t trow0 = b * (k + 1), drow0 = a.batch * (k + 1) + b * k;
+  const RowGeom gm = row_geom(a, b);
+  const int k = gm.k;
+  const int64_t trow0 = gm.trow0, drow0 = gm.drow0;
   const int nr = 2 * k + 1;
   uint4 w0 = make_uint4(0, 0, 0, 0), w1 = w0, w2 = w0, w3 = w0;
   if (lane < nr) {
@@ -832,9 +833,9 @@ __device__ inline int64_t chain16_wave(const AcceptArgs& a, const Eval16<FMT>& e
     const uint4* src = reinterpret_cast<const uint4*>(a.stats + row);
     w0 = src[0]; w1 = src[1]; w2 = src[2]; w3 = src[3];
   }
-  const float u = lane < k ? a.u_accept[b * k + lane] : 2.0f;
+  const float u = lane < k ? a.u_accept[gm.ibase + lane] : 2.0f;
   const float uf = a.u_final[b];
-  const bool alive = a.active ? a.active[b] != 0 : true;
+  const bool alive = (a.active ? a.active[b] != 0 : true) && !gm.bad;
   // drafted tokens the row kernel left unranked (their tie group spans several
   // values; rare): the wave counts the group members before the token
   uint64_t todo = __ballot(lane < nr && lane != k && (w3.x & kRowRank) != 0);
@@ -844,7 +845,7 @@ __device__ inline int64_t chain16_wave(const AcceptArgs& a, const Eval16<FMT>& e
     const int i = l < k ? l : l - k - 1;  // draft position of that row
     const int64_t row = l <= k ? trow0 + l : drow0 + i;
     const uint16_t* ptr = row < ev.split ? ev.base + row * ev.ld : ev.base2 + (row - ev.split) * ev.ld2;
-    const int64_t gid = a.draft_ids[b * k + i];
+    const int64_t gid = a.draft_ids[gm.ibase + i];
     const int32_t glo = (int32_t)rdlane(w1.z, l), ghi = (int32_t)rdlane(w1.w, l);
     uint32_t cnt = 0;
     for (int64_t e = lane; e < gid; e += kWave) {
@@ -868,7 +869,7 @@ __device__ inline int64_t chain16_wave(const AcceptArgs& a, const Eval16<FMT>& e
     near = fabsf(u - r1) < 1e-5f;
   }
   int n = alive ? k : 0;
-  uint32_t fl = 0;
+  uint32_t fl = gm.bad ? (uint32_t)SDX_FLAG_BAD_ROW : 0u;
   if (alive) {
     const uint64_t fm = __ballot(!ok);
     const int first = fm ? __ffsll((unsigned long long)fm) - 1 : kWave;

@@ -35,6 +35,9 @@ _SIGS = {
     "sdx_gather_prob": (INT, [P, I64, I64, I64, P, P, P]),
     "sdx_verify_workspace": (SZ, [I64, I32, I64, INT]),
     "sdx_verify": (INT, [P, P, INT, I64, I32, I64, P, P, P, P, F, F, I32, P, P, P, P, SZ, P]),
+    "sdx_verify_ragged_workspace": (SZ, [I64, I64, I64, INT]),
+    "sdx_verify_ragged": (INT, [P, P, INT, I64, I32, I64, I64, P, P, P, P, P, F, F, I32, P, P, P, P,
+                                SZ, P]),
     "sdx_verify_stats": (INT, [P, P, INT, I64, I32, I64, P, F, F, I32, P, SZ, P]),
     "sdx_verify_greedy_workspace": (SZ, [I64, I32]),
     "sdx_verify_greedy": (INT, [P, INT, I64, I32, I64, P, P, P, P, P, P, P, SZ, P]),

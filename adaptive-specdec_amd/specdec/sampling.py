@@ -25,10 +25,11 @@ import torch
 from . import _lib
 
 __all__ = ["to_probs", "sample_from_probs", "residual_probs", "gather_prob", "rejection_sample",
-           "Verifier"]
+           "rejection_sample_ragged", "Verifier"]
 
 FLAG_ACCEPT_NEAR_TIE = 1
 FLAG_NONFINITE = 2
+FLAG_BAD_ROW = 8
 
 
 def _switch_args(temperature, top_p, top_k):
@@ -195,6 +196,72 @@ def rejection_sample(target_logits, draft_logits, draft_ids, u_accept, u_final, 
                           _lib.ptr(uf), _lib.ptr(act), T, tp, tk, _lib.ptr(n_acc), _lib.ptr(y),
                           _lib.ptr(flags), _lib.ptr(ws), ws.numel(), st)
     _lib.check(rc, "rejection_sample")
+    return n_acc, y, flags
+
+
+def rejection_sample_ragged(target_logits, draft_logits, draft_ids, u_accept, u_final, cu_k, *,
+                            k_max=None, temperature=1.0, top_p=1.0, top_k=0, active=None,
+                            workspace=None, out=None):
+    """`rejection_sample` with a different k per batch row (adaptive k per row).
+
+    Row b drafts k_b = cu_k[b+1] - cu_k[b] tokens (cu_k int64 [B+1], cu_k[0] = 0).
+    Rows are packed: target_logits [sum(k_b+1), V] with row b's positions at
+    cu_k[b] + b, draft_logits [sum k_b, V], draft_ids and u_accept [sum k_b] with
+    row b's at cu_k[b]; u_final [B]. k_max bounds every k_b (None: read from cu_k,
+    one host sync). Returns (n_acc, y, flags) as `rejection_sample`: row b emits
+    draft_ids[cu_k[b] : cu_k[b] + n_acc[b]] then y[b] and drops k_b - n_acc[b]
+    cached positions. Offsets that are inconsistent set FLAG_BAD_ROW on every row.
+    """
+    T, tp, tk = _switch_args(temperature, top_p, top_k)
+    greedy = T == 0.0
+    _lib.require_gpu(target_logits, draft_ids, u_accept, u_final, cu_k,
+                     None if greedy else draft_logits, active)
+    L = _lib.lib()
+    NT, V = target_logits.shape
+    B = cu_k.numel() - 1
+    if NT < B:
+        raise ValueError(f"target_logits has {NT} rows, fewer than the {B} batch rows")
+    cu = cu_k.to(torch.int64).contiguous()
+    if k_max is None:
+        k_max = int((cu[1:] - cu[:-1]).max().item()) if B > 0 else 1
+    k_max = max(int(k_max), 1)
+    dev = target_logits.device
+    tl = target_logits
+    if tl.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        tl = tl.float()
+    dl = None if greedy else draft_logits.to(tl.dtype)
+    if not greedy and tuple(dl.shape) != (NT - B, V):
+        raise ValueError(f"draft_logits must be [{NT - B}, {V}], got {tuple(dl.shape)}")
+    if tl.dtype != torch.float32 and V % 8 != 0:
+        tl = tl.float()
+        dl = None if dl is None else dl.float()
+    tl = tl.contiguous()
+    if greedy:
+        dl = tl  # not read; the C ABI wants a pointer of the right type
+    dl = dl.contiguous()
+    ids = draft_ids.to(torch.int64).contiguous()
+    ua = u_accept.to(torch.float32).contiguous()
+    uf = u_final.to(torch.float32).contiguous()
+    if ids.numel() != NT - B or ua.numel() != NT - B or uf.numel() != B:
+        raise ValueError("draft_ids / u_accept must hold sum(k_b) entries and u_final B")
+    act = None if active is None else active.to(torch.uint8).contiguous()
+    if out is None:
+        n_acc = torch.empty(B, dtype=torch.int64, device=dev)
+        y = torch.empty(B, dtype=torch.int64, device=dev)
+        flags = torch.empty(B, dtype=torch.uint8, device=dev)
+    else:
+        n_acc, y, flags = out
+    if B == 0:
+        return n_acc, y, flags
+    dt = _lib.dtype_code(tl)
+    need = L.sdx_verify_ragged_workspace(B, NT, V, dt)
+    if workspace is None or workspace.numel() < need:
+        workspace = _lib.workspace(need, dev)
+    rc = L.sdx_verify_ragged(_lib.ptr(tl), _lib.ptr(dl), dt, B, k_max, NT, V, _lib.ptr(cu),
+                             _lib.ptr(ids), _lib.ptr(ua), _lib.ptr(uf), _lib.ptr(act), T, tp, tk,
+                             _lib.ptr(n_acc), _lib.ptr(y), _lib.ptr(flags), _lib.ptr(workspace),
+                             workspace.numel(), _lib.stream_of(tl))
+    _lib.check(rc, "rejection_sample_ragged")
     return n_acc, y, flags
 
 

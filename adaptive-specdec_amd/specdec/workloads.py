@@ -5,6 +5,9 @@
            per row; draft = target + N(0, draft_noise^2); draft ids drawn from
            the transformed draft distribution; fp32 uniforms for the accept
            test [B, k] and the final draw [B].
+* ragged:  the verify workload with per-row k_b = best_k(alpha_b, c), alpha_b ~
+           U(alpha_lo, alpha_hi), rows packed: targets [sum(k_b+1), V], drafts,
+           ids and accept uniforms [sum k_b], offsets cu_k [B+1].
 * greedy:  the same logits, draft ids equal to the target argmax with a given
            probability per position (else a different id).
 * kv:      per-row lengths, a shuffled block table, staged K/V vectors.
@@ -14,8 +17,8 @@
 """
 import torch
 
-__all__ = ["zipf_logits", "uniforms", "verify_inputs", "greedy_inputs", "kv_inputs",
-           "attn_inputs"]
+__all__ = ["zipf_logits", "uniforms", "verify_inputs", "ragged_verify_inputs", "greedy_inputs",
+           "kv_inputs", "attn_inputs"]
 
 
 def uniforms(shape, generator, device):
@@ -47,6 +50,40 @@ def verify_inputs(B, k, V, seed, device, temperature=0.8, top_p=0.95, top_k=0, s
     return {
         "target": tgt, "draft": drf, "draft_ids": ids,
         "u_accept": uniforms((B, k), g, device), "u_final": uniforms((B,), g, device),
+        "temperature": temperature, "top_p": top_p, "top_k": top_k,
+    }
+
+
+def ragged_verify_inputs(B, V, seed, device, temperature=0.7, top_p=0.9, top_k=50, alpha_lo=0.4,
+                         alpha_hi=0.9, c=0.1, k_max=8, sigma=3.0, draft_noise=1.0,
+                         dtype=torch.bfloat16, k=None):
+    """Adaptive-k verify: returns a dict of device tensors (packed rows) plus the
+    host list of k_b. `k` (a list) overrides the controller's choice."""
+    from .controller import best_k
+    from .sampling import sample_from_probs, to_probs
+    gc = torch.Generator(device="cpu").manual_seed(int(seed))
+    if k is None:
+        alphas = torch.rand(B, generator=gc) * (alpha_hi - alpha_lo) + alpha_lo
+        k = [best_k(float(a), c, k_max) for a in alphas]
+    k = [int(x) for x in k]
+    cu = torch.zeros(B + 1, dtype=torch.int64)
+    cu[1:] = torch.cumsum(torch.tensor(k, dtype=torch.int64), 0)
+    nd = int(cu[-1])
+    g = torch.Generator(device=device).manual_seed(int(seed))
+    tgt = zipf_logits(nd + B, V, g, device, sigma=sigma, dtype=torch.float32)
+    # draft row j of batch row b sits at cu[b] + j, its target position at cu[b] + b + j
+    rows = torch.cat([torch.arange(int(cu[b]) + b, int(cu[b]) + b + k[b]) for b in range(B)]
+                     ) if nd else torch.zeros(0, dtype=torch.int64)
+    rows = rows.to(device)
+    drf = (tgt[rows] + torch.randn((nd, V), generator=g, device=device) * draft_noise).to(dtype)
+    tgt = tgt.to(dtype)
+    if nd:
+        ids = sample_from_probs(to_probs(drf, temperature, top_p, top_k), u=uniforms((nd,), g, device))
+    else:
+        ids = torch.zeros(0, dtype=torch.int64, device=device)
+    return {
+        "target": tgt, "draft": drf, "draft_ids": ids, "cu_k": cu.to(device), "k": k,
+        "u_accept": uniforms((nd,), g, device), "u_final": uniforms((B,), g, device),
         "temperature": temperature, "top_p": top_p, "top_k": top_k,
     }
 

@@ -46,10 +46,12 @@ enum sdx_status {
 enum sdx_flag {
   SDX_FLAG_ACCEPT_NEAR_TIE = 1, /* an evaluated accept test had |u - min(p/q,1)| < 1e-5 */
   SDX_FLAG_NONFINITE = 2,       /* a logit row held +inf or NaN: results unspecified */
-  SDX_FLAG_UNSUPPORTED = 4      /* a row's probability mass spans more distinct logit values
+  SDX_FLAG_UNSUPPORTED = 4,     /* a row's probability mass spans more distinct logit values
                                    than the row kernels' histogram windows cover (only with
                                    |logit| >= 2^18 at temperatures above ~2500, or fp16 rows
                                    spanning over 36 binades of mass): results unspecified */
+  SDX_FLAG_BAD_ROW = 8          /* per-row k: the row offsets (cu_k) were inconsistent with
+                                   k_max or the row counts; n_acc 0, y unspecified */
 };
 
 const char* sdx_last_error(void);
@@ -104,6 +106,26 @@ int sdx_verify(const void* target_logits, const void* draft_logits, int dtype,
                const uint8_t* active, float temperature, float top_p, int32_t top_k,
                int64_t* n_acc, int64_t* y, uint8_t* flags,
                void* workspace, size_t workspace_bytes, sdx_stream_t stream);
+
+/* Verify with a different k per batch row (config 5's adaptive k): row b drafts
+ * k_b = cu_k[b+1] - cu_k[b] tokens, 0 <= k_b <= k_max (cu_k int64 [batch+1] on the
+ * device, cu_k[0] = 0). Rows are packed: target_logits [target_rows, vocab] with
+ * row b's k_b + 1 positions at cu_k[b] + b (target_rows = sum (k_b + 1), known to the
+ * caller from the tensor's shape), draft_logits / draft_ids / u_accept
+ * [target_rows - batch] with row b's at cu_k[b]. Same rules and outputs as
+ * sdx_verify (emitted tokens of row b: draft_ids[cu_k[b] .. + n_acc[b]] then y[b]; KV
+ * rows to drop: k_b - n_acc[b]). The offsets are checked on the device: if they are
+ * inconsistent (not non-decreasing from 0 to target_rows - batch, or a k_b > k_max),
+ * every row gets SDX_FLAG_BAD_ROW and n_acc 0. Workspace: sdx_verify_ragged_workspace,
+ * zero-filled once, as for sdx_verify. No reference counterpart: the reference engine
+ * verifies one k for the whole batch (engine.py:281-312). */
+size_t sdx_verify_ragged_workspace(int64_t batch, int64_t target_rows, int64_t vocab, int dtype);
+int sdx_verify_ragged(const void* target_logits, const void* draft_logits, int dtype,
+                      int64_t batch, int32_t k_max, int64_t target_rows, int64_t vocab,
+                      const int64_t* cu_k, const int64_t* draft_ids, const float* u_accept,
+                      const float* u_final, const uint8_t* active, float temperature,
+                      float top_p, int32_t top_k, int64_t* n_acc, int64_t* y, uint8_t* flags,
+                      void* workspace, size_t workspace_bytes, sdx_stream_t stream);
 
 /* Phase 1 of sdx_verify alone: the fused to_probs statistics of every target and draft
  * row (normaliser, top-k/top-p boundary, drafted-token probabilities) into the workspace,

@@ -194,6 +194,44 @@ def rejection_sample(target_logits, draft_logits, draft_ids, u_accept, u_final,
     return n_acc, y, flags
 
 
+def rejection_sample_ragged(target_logits, draft_logits, draft_ids, u_accept, u_final, cu_k,
+                            temperature=1.0, top_p=1.0, top_k=0, active=None):
+    """Verify with k_b = cu_k[b+1] - cu_k[b] drafts in row b: row b is the verify
+    step of `engine.py:281-303` run at its own k on its packed rows (targets
+    [cu_k[b] + b, + k_b + 1), drafts, ids and uniforms [cu_k[b], + k_b)); with
+    k_b = 0 the row draws its bonus token from its one target row.
+    Returns (n_acc [B], y [B], flags [B])."""
+    tl = np.asarray(target_logits, np.float32)
+    dl = None if draft_logits is None else np.asarray(draft_logits, np.float32)
+    ids = np.asarray(draft_ids, np.int64)
+    ua = np.asarray(u_accept, np.float32)
+    uf = np.asarray(u_final, np.float32)
+    cu = np.asarray(cu_k, np.int64)
+    B = cu.size - 1
+    act = np.ones(B, bool) if active is None else np.asarray(active, bool)
+    n_acc = np.zeros(B, np.int64)
+    y = np.zeros(B, np.int64)
+    flags = np.zeros(B, np.uint8)
+    for b in range(B):
+        c0, kb = int(cu[b]), int(cu[b + 1] - cu[b])
+        t = tl[c0 + b:c0 + b + kb + 1]
+        if kb == 0:                                  # nothing drafted: the bonus draw
+            if temperature is None or temperature <= 0:
+                y[b] = argmax_first(t[0])
+            else:
+                y[b] = sample_fixed(fixed62(_transform_row(t[0], temperature, top_p, top_k)), uf[b])
+            continue
+        if temperature is None or temperature <= 0:
+            n, yy, f = greedy_verify(t[None], ids[c0:c0 + kb][None], ua[c0:c0 + kb][None],
+                                     act[b:b + 1])
+        else:
+            n, yy, f = rejection_sample(t[None], dl[c0:c0 + kb][None], ids[c0:c0 + kb][None],
+                                        ua[c0:c0 + kb][None], uf[b:b + 1], temperature, top_p,
+                                        top_k, act[b:b + 1])
+        n_acc[b], y[b], flags[b] = n[0], yy[0], f[0]
+    return n_acc, y, flags
+
+
 def argmax_first(x):
     """Row-wise argmax, first index among equal maxima (torch/numpy rule)."""
     x = np.asarray(x, np.float32)

@@ -11,7 +11,7 @@ import torch
 
 from oracle import sampling as O
 from specdec import sampling as S
-from specdec.workloads import uniforms, verify_inputs, zipf_logits
+from specdec.workloads import ragged_verify_inputs, uniforms, verify_inputs, zipf_logits
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -326,3 +326,71 @@ def test_rejection_sample_multivalue_tie_group_ranks(T, tp):
     assert np.array_equal(n.cpu().numpy(), rn)
     assert np.array_equal(y.cpu().numpy(), ry)
     assert np.array_equal(f.cpu().numpy(), rf)
+
+
+# ---------------------------------------------------------------- per-row k
+def _ragged_oracle(inp, T, tp, tk, active=None):
+    return O.rejection_sample_ragged(_np(inp["target"]), _np(inp["draft"]),
+                                     inp["draft_ids"].cpu().numpy(), _np(inp["u_accept"]),
+                                     _np(inp["u_final"]), inp["cu_k"].cpu().numpy(), T, tp, tk,
+                                     active)
+
+
+@pytest.mark.parametrize("T,tp,tk", [(0.7, 0.9, 50), (0.8, 0.95, 0), (0.0, 1.0, 0)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rejection_sample_ragged_matches_oracle(T, tp, tk, dtype):
+    """Rows of k_b from 0 to 8 packed in one call (k_b = 0: bonus draw only)."""
+    ks = [3, 0, 8, 1, 5, 2, 8, 4, 0, 6]
+    inp = ragged_verify_inputs(len(ks), 4096, seed=21, device=DEV, temperature=T, top_p=tp,
+                               top_k=tk, dtype=dtype, k=ks)
+    n, y, f = S.rejection_sample_ragged(inp["target"], inp["draft"], inp["draft_ids"],
+                                        inp["u_accept"], inp["u_final"], inp["cu_k"], k_max=8,
+                                        temperature=T, top_p=tp, top_k=tk)
+    rn, ry, rf = _ragged_oracle(inp, T, tp, tk)
+    assert np.array_equal(n.cpu().numpy(), rn)
+    assert np.array_equal(y.cpu().numpy(), ry)
+    assert np.array_equal(f.cpu().numpy(), rf)
+
+
+def test_rejection_sample_ragged_config5_vocab():
+    """Config 5's sampler: k_b from the controller at alpha_b ~ U(0.4, 0.9),
+    c = 0.1, V = 151936 bf16, T = 0.7, top-k 50, top-p 0.9; some rows inactive."""
+    B = 24
+    inp = ragged_verify_inputs(B, 151936, seed=5, device=DEV)
+    active = torch.tensor([b % 5 != 2 for b in range(B)], device=DEV)
+    n, y, f = S.rejection_sample_ragged(inp["target"], inp["draft"], inp["draft_ids"],
+                                        inp["u_accept"], inp["u_final"], inp["cu_k"],
+                                        temperature=0.7, top_p=0.9, top_k=50, active=active)
+    rn, ry, rf = _ragged_oracle(inp, 0.7, 0.9, 50, active.cpu().numpy())
+    assert np.array_equal(n.cpu().numpy(), rn)
+    assert np.array_equal(y.cpu().numpy(), ry)
+    assert np.array_equal(f.cpu().numpy(), rf)
+
+
+def test_rejection_sample_ragged_equal_k_is_uniform():
+    """cu_k = 4 * arange(B+1) over the reshaped B=64, k=4, V=151936 step gives
+    the uniform verify bit for bit (576 rows, split rows included)."""
+    B, k, V, T, tp = 64, 4, 151936, 0.8, 0.95
+    inp = verify_inputs(B, k, V, seed=1000, device=DEV, temperature=T, top_p=tp)
+    n, y, f = S.rejection_sample(inp["target"], inp["draft"], inp["draft_ids"], inp["u_accept"],
+                                 inp["u_final"], temperature=T, top_p=tp)
+    cu = torch.arange(B + 1, device=DEV, dtype=torch.int64) * k
+    n2, y2, f2 = S.rejection_sample_ragged(inp["target"].reshape(-1, V), inp["draft"].reshape(-1, V),
+                                           inp["draft_ids"].reshape(-1),
+                                           inp["u_accept"].reshape(-1), inp["u_final"], cu,
+                                           k_max=k, temperature=T, top_p=tp)
+    assert torch.equal(n, n2) and torch.equal(y, y2) and torch.equal(f, f2)
+
+
+def test_rejection_sample_ragged_rejects_bad_offsets():
+    """Offsets that decrease, or a k_b above k_max, flag every row and accept nothing."""
+    ks = [2, 3, 1]
+    inp = ragged_verify_inputs(3, 512, seed=3, device=DEV, k=ks)
+    for cu in ([0, 4, 3, 6], [0, 2, 5, 6]):
+        cu_k = torch.tensor(cu, dtype=torch.int64, device=DEV)
+        kmax = 2 if cu == [0, 2, 5, 6] else 8   # second: k_1 = 3 > k_max = 2
+        n, y, f = S.rejection_sample_ragged(inp["target"], inp["draft"], inp["draft_ids"],
+                                            inp["u_accept"], inp["u_final"], cu_k, k_max=kmax,
+                                            temperature=0.7, top_p=0.9, top_k=50)
+        assert np.all(f.cpu().numpy() & S.FLAG_BAD_ROW)
+        assert np.all(n.cpu().numpy() == 0)

@@ -250,3 +250,48 @@ def test_residual_probs_degenerate_is_p():
     assert np.array_equal(S.residual_probs(p, p), p)
     out = S.residual_probs(f32(0.5, 0.5, 0, 0), f32(0.25, 0.75, 0, 0))
     assert np.array_equal(out, f32(1, 0, 0, 0))
+
+
+# ---------------------------------------------------------------- per-row k
+@pytest.mark.parametrize("T,tp,tk", [(0.8, 0.95, 0), (0.7, 0.9, 5), (0.0, 1.0, 0)])
+def test_ragged_with_equal_k_is_the_uniform_verify(T, tp, tk):
+    """Packing [B, k+1, V] / [B, k, V] row by row with cu_k = k * arange(B+1)
+    must give exactly the uniform-k verify."""
+    rs = np.random.RandomState(9)
+    B, k, V = 5, 3, 40
+    tl = torch.tensor(rs.randn(B, k + 1, V) * 2, dtype=torch.bfloat16).float().numpy()
+    dl = torch.tensor(tl[:, :k] + rs.randn(B, k, V), dtype=torch.bfloat16).float().numpy()
+    ids = rs.randint(0, V, (B, k))
+    ua = rs.uniform(0, 1, (B, k)).astype(np.float32)
+    uf = rs.uniform(0, 1, B).astype(np.float32)
+    want = S.rejection_sample(tl, dl, ids, ua, uf, T, tp, tk)
+    got = S.rejection_sample_ragged(tl.reshape(-1, V), dl.reshape(-1, V), ids.reshape(-1),
+                                    ua.reshape(-1), uf, np.arange(B + 1) * k, T, tp, tk)
+    for x, y in zip(got, want):
+        assert np.array_equal(x, y)
+
+
+def test_ragged_rows_use_their_own_slices():
+    """Rows of k_b = 2, 0, 3: each equals the uniform verify of that row alone
+    on its packed slices, and the k_b = 0 row emits the bonus draw of its one
+    target row (to_probs then the fixed-point inverse CDF)."""
+    rs = np.random.RandomState(10)
+    V, ks = 32, [2, 0, 3]
+    cu = np.concatenate([[0], np.cumsum(ks)])
+    nt, nd = sum(ks) + len(ks), sum(ks)
+    tl = torch.tensor(rs.randn(nt, V) * 2, dtype=torch.bfloat16).float().numpy()
+    dl = torch.tensor(rs.randn(nd, V) * 2, dtype=torch.bfloat16).float().numpy()
+    ids = rs.randint(0, V, nd)
+    ua = rs.uniform(0, 1, nd).astype(np.float32)
+    uf = rs.uniform(0, 1, len(ks)).astype(np.float32)
+    n, y, f = S.rejection_sample_ragged(tl, dl, ids, ua, uf, cu, 0.9, 0.9, 0)
+    for b, kb in enumerate(ks):
+        c0 = int(cu[b])
+        if kb == 0:
+            p = S.to_probs(tl[c0 + b][None], 0.9, 0.9, 0)
+            assert n[b] == 0 and y[b] == S.sample_from_probs(p, uf[b:b + 1])[0]
+            continue
+        rn, ry, rf = S.rejection_sample(tl[None, c0 + b:c0 + b + kb + 1], dl[None, c0:c0 + kb],
+                                        ids[None, c0:c0 + kb], ua[None, c0:c0 + kb], uf[b:b + 1],
+                                        0.9, 0.9, 0)
+        assert (n[b], y[b], f[b]) == (rn[0], ry[0], rf[0])
