@@ -295,6 +295,67 @@ def bench_kv(args, torch):
             "cpu_baseline": None}
 
 
+def bench_ragged(args, torch):
+    """Config 5's sampler: B=128 rows with per-row k_b = best_k(alpha_b, 0.1),
+    alpha_b ~ U(0.4, 0.9), V=151936 bf16 logits as in the fused verify, T=0.7,
+    top-k 50, top-p 0.9; one call verifies all rows (packed [sum(k_b+1), V] and
+    [sum k_b, V])."""
+    from specdec.sampling import rejection_sample_ragged
+    from specdec.workloads import ragged_verify_inputs
+    B, V, T, tp, tk = 128, 151936, 0.7, 0.9, 50
+    dev = "cuda:0"
+    sets = [ragged_verify_inputs(B, V, seed=2000 + i, device=dev, temperature=T, top_p=tp, top_k=tk)
+            for i in range(args.sets)]
+    outs = [tuple(torch.empty(B, dtype=dt, device=dev) for dt in (torch.int64, torch.int64,
+                                                                   torch.uint8)) for _ in sets]
+    wss = [None] * len(sets)
+
+    def call(i):
+        s = sets[i]
+        return rejection_sample_ragged(s["target"], s["draft"], s["draft_ids"], s["u_accept"],
+                                       s["u_final"], s["cu_k"], k_max=8, temperature=T,
+                                       top_p=tp, top_k=tk, workspace=wss[i], out=outs[i])
+    from specdec import _lib
+    for i, s in enumerate(sets):  # one workspace per input set, zero-filled once
+        nt = s["target"].shape[0]
+        wss[i] = _lib.workspace(_lib.lib().sdx_verify_ragged_workspace(B, nt, V, _lib.BF16), dev)
+    eager = []
+    for i in range(len(sets)):
+        n, y, f = call(i)
+        eager.append((n.clone(), y.clone(), f.clone()))
+    for i in range(args.warmup):
+        call(i % len(sets))
+    torch.cuda.synchronize()
+    graphs = [capture(lambda i=i: call(i), torch) for i in range(len(sets))]
+    for rep in range(3):                       # every replay must equal the eager result
+        for g, o, (n, y, f) in zip(graphs, outs, eager):
+            g.replay()
+            torch.cuda.synchronize()
+            if not (torch.equal(o[0], n) and torch.equal(o[1], y) and torch.equal(o[2], f)):
+                raise RuntimeError("graph replay differs from the eager verify")
+    ms = timed_graphs(graphs, args.steps, torch)
+    tokens = sum(int((n + 1).sum().item()) for n, _, _ in eager) / len(eager)
+    rows = sum(int(s["target"].shape[0]) + int(s["draft"].shape[0]) for s in sets) / len(sets)
+    alg = rows * V * 2
+    ach = alg / (ms / 1e3) / 1e9
+    mean_k = sum(sum(s["k"]) for s in sets) / (len(sets) * B)
+    return {"metric": "verified tokens/sec, adaptive-k verify B=128 (per-row k), V=151936",
+            "value": round(tokens / (ms / 1e3), 1), "unit": "verified tokens/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic",
+            "config": {"workload": "adaptive-k fused verify B=128, k_b=best_k(U(0.4,0.9), c=0.1), "
+                                   "V=151936 bf16, T=0.7 top-k 50 top-p 0.9",
+                       "batch": B, "mean_k": round(mean_k, 3), "rows": rows,
+                       "input_sets": len(sets), "hip_graph": True},
+            "mean_accepted": round(tokens / B - 1, 4),
+            "roofline": {"bound": "hbm", "kernel": "whole call (row statistics + draw)",
+                         "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                         "algorithmic_bytes": int(alg), "avg_launch_us": round(ms * 1e3, 2)},
+            "cpu_baseline": None}
+
+
 def bench_attn(args, torch):
     """Adaptive-k verify attention, one layer: B=128 rows with k_b = best_k(alpha_b, 0.1),
     alpha_b ~ U(0.4, 0.9), contexts ~ U[1024, 8192], 32 query / 8 KV heads of 128,
@@ -357,7 +418,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="verify", choices=["verify", "greedy", "kv", "attn"])
+    ap.add_argument("--workload", default="verify",
+                    choices=["verify", "greedy", "kv", "attn", "ragged"])
     ap.add_argument("--sets", type=int, default=3)
     ap.add_argument("--attn-chunk", type=int, default=0,
                     help="attn workload: keys per chunk (0: the library default)")
@@ -377,7 +439,7 @@ def main():
         print("bench.py: no ROCm device visible", file=sys.stderr)
         sys.exit(1)
     fn = {"verify": bench_verify, "greedy": bench_greedy, "kv": bench_kv,
-          "attn": bench_attn}[args.workload]
+          "attn": bench_attn, "ragged": bench_ragged}[args.workload]
     result = fn(args, torch)
     if args.calibrate_copy:
         # a device-to-device copy of known size: its FETCH_SIZE / WRITE_SIZE per
