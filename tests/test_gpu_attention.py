@@ -57,6 +57,15 @@ def test_verify_attention_chunked_matches_oracle(chunk):
     _check(inp, 32, 8, chunk_tokens=chunk)
 
 
+@pytest.mark.parametrize("bs,chunk", [(1, 1024), (12, 128), (16, 64)])
+def test_verify_attention_block_sizes(bs, chunk):
+    """Pages of 1 token (a page id per token), 12 tokens (page boundaries
+    inside tiles, general index arithmetic) and 16, with long rows."""
+    inp = attn_inputs(2, seed=bs, device=DEV, ctx_lo=1500, ctx_hi=2600, hq=8, hkv=2, k_max=6,
+                      block_size=bs)
+    _check(inp, 8, 2, chunk_tokens=chunk)
+
+
 def test_verify_attention_same_for_any_chunking():
     inp = attn_inputs(4, seed=11, device=DEV, ctx_lo=300, ctx_hi=900, hq=16, hkv=4, k_max=6)
     outs = [verify_attention_paged(inp["q"], inp["cu_q"], inp["k_pool"], inp["v_pool"],
