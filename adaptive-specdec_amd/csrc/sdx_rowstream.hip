@@ -392,6 +392,7 @@ struct SkLds {
   SkRed red;
   int32_t i32[12];
   uint64_t x64[2];
+  uint32_t unit_ctr;  // next 4 KB unit of the row to stream
 };
 
 __global__ void __launch_bounds__(SK_NT) __attribute__((amdgpu_waves_per_eu(6)))
@@ -429,6 +430,7 @@ rowstream_bf16_kernel(RowStatArgs a) {
   if (tid == 0 && part <= 0 && a.rank_acc) a.rank_acc[row] = 0ull;
 
   for (int b = tid; b < SK_SPLIT_CHUNKS * 8; b += SK_NT) hist[b] = 0u;
+  if (tid == 0) L.unit_ctr = 0u;
   __syncthreads();
 
   // ---- 1. stream the row: 16-byte loads two stages deep, packed codes ->
@@ -439,13 +441,12 @@ rowstream_bf16_kernel(RowStatArgs a) {
   if ((int64_t)blockIdx.x >= a.late_block) __builtin_amdgcn_s_setprio(3);
   uint32_t omx = 0;
   // The drafted token's member rank, when its tie group turns out to be its own
-  // value alone: equal codes before it. The histogram is read at a barrier
-  // just before the stream iteration holding the token (every earlier element
-  // is counted there); that iteration's elements before it are counted by hand.
+  // value alone: equal codes before it, counted while streaming (a token in the
+  // last V % 8 elements: the histogram's count, read once every unit is in).
   const bool has_g = gid >= 0 && gid < V;
   const uint32_t cg = has_g ? (uint32_t)ptr[gid] : 0u;
   const int bin_g = sk_bin_of_key(key_of_code16(cg));
-  uint32_t snap = 0, pre = 0;  // pre: per thread, equal codes in the held iteration
+  uint32_t snap = 0, pre = 0;  // pre: per thread, equal codes before the token
   // this block's range: 8-element groups [g0, g1), then the last V % 8 elements
   // when it holds the row's end
   const uint32_t n4_all = (uint32_t)(V >> 3);  // whole 8-element groups (V < 2^31)
@@ -459,41 +460,46 @@ rowstream_bf16_kernel(RowStatArgs a) {
   const bool g_in_groups = has_g && gid_l >= 0 && gid_l < (int64_t)(g1 - g0) * 8;
   const bool g_in_tail = has_g && has_tail && gid >= (int64_t)n4_all * 8;
   {
-    // raw buffer loads: per-lane offset tid * 16 stays in a register, the
-    // iteration offset is scalar; loads past the range read zeros (unused)
+    // Units of 4 KB (64 lanes x 4 x 16 bytes) are dealt to the waves from an LDS
+    // counter, so a wave that streams faster takes more of them and the block's
+    // waves finish together (with a fixed split the second wave on each SIMD
+    // finished about 4 us after the first). Raw buffer loads: the lane offset
+    // stays in a register, the unit offset is scalar; loads past the range read
+    // zeros without touching memory (a wave's last grab), and are not processed.
     constexpr int U = 4;
-    constexpr uint32_t kStep = (uint32_t)SK_NT * U;
+    constexpr uint32_t kUnit = (uint32_t)kWave * U;  // 8-element groups per unit
     const uint32_t n4 = g1 - g0;
-    const uint32_t iters = (n4 + kStep - 1) / kStep;
+    const uint32_t nunits = (n4 + kUnit - 1) / kUnit;
+    // the resource from scalar copies of its (uniform) fields: built from values the
+    // compiler cannot prove uniform it would wrap every load in a readfirstlane loop
+    const uint64_t rb = (uint64_t)(uintptr_t)(ptr + (int64_t)g0 * 8);
+    const uint64_t rbu = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(rb >> 32))
+                          << 32) |
+                         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)rb);
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(ptr + (int64_t)g0 * 8), (short)0, (int)(n4 * 16u), 0x00020000);
-    const uint32_t voff = (uint32_t)tid * 16u;
+        (void*)(uintptr_t)rbu, (short)0, __builtin_amdgcn_readfirstlane((int)(n4 * 16u)),
+        0x00020000);
+    const uint32_t voff = (uint32_t)lane * 16u;
     char* const hb = reinterpret_cast<char*>(hist);
-    const uint32_t it_g = g_in_groups ? (uint32_t)((gid_l >> 3) / kStep) : 0xFFFFFFFFu;
-    auto at_token = [&](const uint4 (&d)[U], uint32_t it) {  // before processing iteration it
-      if (it != it_g) return;  // uniform
-      __syncthreads();
-      snap = hist[bin_g];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int64_t e0 = ((int64_t)it * kStep + (uint32_t)u * SK_NT + (uint32_t)tid) * 8;
-        const uint32_t wd[4] = {d[u].x, d[u].y, d[u].z, d[u].w};
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          const uint32_t c = (t & 1) ? wd[t >> 1] >> 16 : wd[t >> 1] & 0xFFFFu;
-          pre += (e0 + t < gid_l && c == cg) ? 1u : 0u;
-        }
-      }
+    // the drafted token's rank: every equal code in units before the token's unit,
+    // and those before it inside that unit (bin_g holds its value alone whenever
+    // the count is used, so equal bins are equal codes)
+    const uint32_t u_tok = g_in_groups ? (uint32_t)((gid_l >> 3) / kUnit) : 0u;
+    const uint32_t og = 4u * (uint32_t)bin_g;
+    auto grab = [&]() -> uint32_t {
+      uint32_t u = 0;
+      if (lane == 0) u = atomicAdd(&L.unit_ctr, 1u);
+      return (uint32_t)__builtin_amdgcn_readfirstlane((int)u);
     };
-    auto load = [&](uint4 (&d)[U], uint32_t it) {
+    auto load = [&](uint4 (&d)[U], uint32_t u) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
+      for (int k = 0; k < U; ++k) {
         const auto x = __builtin_amdgcn_raw_buffer_load_b128(
-            rsrc, (int)voff, (int)((it * kStep + (uint32_t)u * SK_NT) * 16u), 0);
-        d[u] = make_uint4(x[0], x[1], x[2], x[3]);
+            rsrc, (int)voff, (int)((u * kUnit + (uint32_t)k * kWave) * 16u), 0);
+        d[k] = make_uint4(x[0], x[1], x[2], x[3]);
       }
     };
-    auto proc = [&](const uint4& v) {
+    auto proc = [&](const uint4& v, bool cnt) {
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
@@ -501,29 +507,46 @@ rowstream_bf16_kernel(RowStatArgs a) {
         omx = max2(omx, o);
         atomicAdd(reinterpret_cast<uint32_t*>(hb + (o & 0xFFFFu)), 1u);
         atomicAdd(reinterpret_cast<uint32_t*>(hb + (o >> 16)), 1u);
+        if (cnt) pre += ((o & 0xFFFFu) == og ? 1u : 0u) + ((o >> 16) == og ? 1u : 0u);
       }
     };
-    auto proc_all = [&](const uint4 (&d)[U]) {
+    auto proc_unit = [&](const uint4 (&d)[U], uint32_t u) {
+      const bool full = (u + 1) * kUnit <= n4;  // uniform
+      const bool cnt = u < u_tok;               // uniform
 #pragma unroll
-      for (int u = 0; u < U; ++u) proc(d[u]);
-    };
-    auto proc_last = [&](const uint4 (&d)[U], uint32_t it) {
+      for (int k = 0; k < U; ++k) {
+        const uint32_t grp = u * kUnit + (uint32_t)k * kWave + (uint32_t)lane;
+        if (full || grp < n4) {
+          if (cnt) proc(d[k], true);
+          else proc(d[k], false);
+        }
+      }
+      if (g_in_groups && u == u_tok) {  // uniform: the token's unit, counted by hand
 #pragma unroll
-      for (int u = 0; u < U; ++u)
-        if (it * kStep + (uint32_t)u * SK_NT + (uint32_t)tid < n4) proc(d[u]);
+        for (int k = 0; k < U; ++k) {
+          const int64_t e0 = (int64_t)(u * kUnit + (uint32_t)k * kWave + (uint32_t)lane) * 8;
+          const uint32_t wd[4] = {d[k].x, d[k].y, d[k].z, d[k].w};
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            const uint32_t c = (t & 1) ? wd[t >> 1] >> 16 : wd[t >> 1] & 0xFFFFu;
+            pre += (e0 + t < gid_l && c == cg) ? 1u : 0u;
+          }
+        }
+      }
     };
-    if (iters > 0) {
+    if (nunits > 0) {  // uniform
       uint4 A[U], B[U];
-      load(A, 0);
-      for (uint32_t it = 0;; it += 2) {  // uniform control flow
-        at_token(A, it);
-        if (it + 1 >= iters) { proc_last(A, it); break; }
-        load(B, it + 1);
-        proc_all(A);
-        at_token(B, it + 1);
-        if (it + 2 >= iters) { proc_last(B, it + 1); break; }
-        load(A, it + 2);
-        proc_all(B);
+      uint32_t ua = grab();
+      load(A, ua);
+      for (;;) {  // grabs only grow, so a unit past the end ends the wave's work
+        const uint32_t ub = grab();
+        load(B, ub);
+        if (ua >= nunits) break;
+        proc_unit(A, ua);
+        ua = grab();
+        load(A, ua);
+        if (ub >= nunits) break;
+        proc_unit(B, ub);
       }
     }
     if (g_in_tail) {  // the token among the last V % 8 elements
