@@ -66,6 +66,25 @@ def test_verify_attention_block_sizes(bs, chunk):
     _check(inp, 8, 2, chunk_tokens=chunk)
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_verify_attention_random_shapes(seed):
+    """Seeded random shapes: batch, query/KV heads (group 1 to 8), k_max within
+    the 64-row limit, context range, block size and chunk size."""
+    rng = np.random.RandomState(100 + seed)
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    group = int(rng.choice([1, 2, 4, 8]))
+    hq = hkv * group
+    k_max = int(min(8, 64 // group - 1))
+    lo = int(rng.randint(0, 1500))
+    hi = lo + int(rng.randint(1, 1500))
+    bs = int(rng.choice([1, 3, 8, 16, 32]))
+    chunk = int(rng.choice([0, 64, 192, 512]))
+    B = int(rng.randint(1, 7))
+    inp = attn_inputs(B, seed=seed, device=DEV, ctx_lo=lo, ctx_hi=hi, hq=hq, hkv=hkv, k_max=k_max,
+                      block_size=bs, alpha_lo=0.5, alpha_hi=0.95)
+    _check(inp, hq, hkv, chunk_tokens=chunk)
+
+
 def test_verify_attention_same_for_any_chunking():
     inp = attn_inputs(4, seed=11, device=DEV, ctx_lo=300, ctx_hi=900, hq=16, hkv=4, k_max=6)
     outs = [verify_attention_paged(inp["q"], inp["cu_q"], inp["k_pool"], inp["v_pool"],

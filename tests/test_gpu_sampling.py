@@ -337,7 +337,7 @@ def _ragged_oracle(inp, T, tp, tk, active=None):
 
 
 @pytest.mark.parametrize("T,tp,tk", [(0.7, 0.9, 50), (0.8, 0.95, 0), (0.0, 1.0, 0)])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_rejection_sample_ragged_matches_oracle(T, tp, tk, dtype):
     """Rows of k_b from 0 to 8 packed in one call (k_b = 0: bonus draw only)."""
     ks = [3, 0, 8, 1, 5, 2, 8, 4, 0, 6]
@@ -394,3 +394,23 @@ def test_rejection_sample_ragged_rejects_bad_offsets():
                                             temperature=0.7, top_p=0.9, top_k=50)
         assert np.all(f.cpu().numpy() & S.FLAG_BAD_ROW)
         assert np.all(n.cpu().numpy() == 0)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_rejection_sample_ragged_random(seed):
+    """Seeded random row counts, k lists (0 to k_max), vocab and transform."""
+    rng = np.random.RandomState(seed)
+    B = int(rng.randint(1, 20))
+    k_max = int(rng.randint(1, 12))
+    ks = [int(x) for x in rng.randint(0, k_max + 1, B)]
+    V = int(rng.choice([64, 1000, 4096]))
+    T, tp, tk = [(0.7, 0.9, 50), (1.0, 1.0, 0), (1.3, 0.5, 7), (0.0, 1.0, 0)][seed]
+    inp = ragged_verify_inputs(B, V, seed=seed + 50, device=DEV, temperature=T, top_p=tp,
+                               top_k=tk, k=ks)
+    n, y, f = S.rejection_sample_ragged(inp["target"], inp["draft"], inp["draft_ids"],
+                                        inp["u_accept"], inp["u_final"], inp["cu_k"],
+                                        k_max=k_max, temperature=T, top_p=tp, top_k=tk)
+    rn, ry, rf = _ragged_oracle(inp, T, tp, tk)
+    assert np.array_equal(n.cpu().numpy(), rn)
+    assert np.array_equal(y.cpu().numpy(), ry)
+    assert np.array_equal(f.cpu().numpy(), rf)
