@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from oracle import attention as OA
-from specdec.attention import verify_attention_paged
+from specdec.attention import attention_workspace, verify_attention_paged
 from specdec.workloads import attn_inputs
 
 pytestmark = pytest.mark.gpu
@@ -110,3 +110,35 @@ def test_verify_attention_rejects_bad_rows():
     with pytest.raises(RuntimeError):       # chunk not a multiple of 64
         verify_attention_paged(inp["q"], inp["cu_q"], inp["k_pool"], inp["v_pool"],
                                inp["block_table"], inp["kv_len"], inp["max_q"], chunk_tokens=96)
+
+
+def test_verify_attention_graph_replays():
+    """The call captured in a graph (plan, attention, merge; no memsets): every
+    replay, with eager calls and synchronizations between replays, equals the
+    eager output bit for bit (the kernels are deterministic)."""
+    hq, hkv = 32, 8
+    inp = attn_inputs(8, seed=31, device=DEV, ctx_lo=500, ctx_hi=3000, hq=hq, hkv=hkv, k_max=8,
+                      alpha_lo=0.85, alpha_hi=0.95)
+    args = (inp["q"], inp["cu_q"], inp["k_pool"], inp["v_pool"], inp["block_table"],
+            inp["kv_len"], inp["max_q"])
+    eager = verify_attention_paged(*args).clone()
+    torch.cuda.synchronize()
+    _check(inp, hq, hkv)
+    B = inp["cu_q"].numel() - 1
+    ws = attention_workspace(B, inp["max_q"], hq, hkv, inp["k_pool"].shape[1],
+                             inp["block_table"].shape[1], device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = torch.empty_like(inp["q"])
+    verify_attention_paged(*args, out=out, error=err, workspace=ws)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        verify_attention_paged(*args, out=out, error=err, workspace=ws)
+    for _ in range(5):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        assert torch.equal(verify_attention_paged(*args), eager)  # eager work between replays
+        torch.cuda.synchronize()
+    assert int(err.item()) == 0

@@ -108,6 +108,40 @@ def test_rejection_sample_bf16_b64_k4_v151936(seed):
         assert np.array_equal(f.cpu().numpy(), rf)
 
 
+def test_verifier_graph_replays():
+    """The fixed-shape Verifier captured in a graph (nothing in it is a memset:
+    counters are cleared by the kernels): replays over two input sets, with
+    eager calls and synchronizations between them, each equal to the oracle."""
+    B, k, V, T, tp = 16, 4, 151936, 0.8, 0.95
+    names = ("target", "draft", "draft_ids", "u_accept", "u_final")
+    sets = [verify_inputs(B, k, V, seed=s, device=DEV, temperature=T, top_p=tp) for s in (7, 8)]
+    ref = [O.rejection_sample(_np(x["target"]), _np(x["draft"]), x["draft_ids"].cpu().numpy(),
+                              _np(x["u_accept"]), _np(x["u_final"]), T, tp, 0) for x in sets]
+    v = S.Verifier(B, k, V, torch.bfloat16, temperature=T, top_p=tp)
+    static = {n: sets[0][n].clone() for n in names}
+
+    def check(out, i):
+        n, y, f = (t.cpu().numpy() for t in out)
+        assert np.array_equal(n, ref[i][0])
+        assert np.array_equal(y, ref[i][1])
+        assert np.array_equal(f, ref[i][2])
+
+    check(v(*(static[n] for n in names)), 0)  # eager, before capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = v(*(static[n] for n in names))
+    for rep in range(6):
+        i = rep % 2
+        for n in names:
+            static[n].copy_(sets[i][n])
+        g.replay()
+        torch.cuda.synchronize()
+        check(out, i)
+        check(v(*(sets[1 - i][n] for n in names)), 1 - i)  # eager work between replays
+        torch.cuda.synchronize()
+
+
 def test_rejection_sample_active_and_fp32():
     B, k, V = 12, 3, 640
     inp = verify_inputs(B, k, V, seed=7, device=DEV, dtype=torch.float32)
