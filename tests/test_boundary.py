@@ -3,7 +3,8 @@
 * libspecdec_amd.so loads and exports every function include/specdec_amd.h declares;
 * the ctypes signature table covers exactly that set;
 * the Python entry points refuse CPU tensors (there is no CPU fallback);
-* host logic: controller closed form, RaggedCache host bookkeeping errors.
+* host logic: controller closed form, RaggedCache host bookkeeping errors;
+* argument checks of the C ABI, which return their status before any HIP work.
 """
 import ctypes
 import os
@@ -84,3 +85,37 @@ def test_ragged_cache_host_bookkeeping():
     c2 = RaggedCache(1, 2, 16, "cpu")
     c2.set_lengths([4, 4])
     assert c2.attn_mask(2, torch.float32) is None          # uniform, no pad: no mask
+
+
+def test_c_abi_argument_errors():
+    """Status codes of the argument checks: a workspace one byte short, a vocab
+    past the 16-bit row kernel's capacity, an unsupported head size and a bad
+    chunk size fail with SDX_EWORKSPACE / SDX_EUNSUPPORTED / SDX_EINVAL and a
+    message, before anything is launched (the pointers are never dereferenced)."""
+    from specdec import _lib
+    L = _lib.lib()
+    OK, EINVAL, EUNSUP, EWS = 0, -1, -2, -4
+    BF16 = 1
+    fake = ctypes.c_void_p(4096)
+    B, k, V = 4, 2, 1024
+    need = L.sdx_verify_workspace(B, k, V, BF16)
+    assert need > 0
+
+    def verify(batch, kk, vocab, ws_bytes, draft_ids=fake):
+        return L.sdx_verify(fake, fake, BF16, batch, kk, vocab, draft_ids, fake, fake, None,
+                            ctypes.c_float(0.8), ctypes.c_float(0.95), 0, fake, fake, fake,
+                            fake, ws_bytes, None)
+
+    assert verify(B, k, V, need - 1) == EWS
+    assert b"workspace" in L.sdx_last_error()
+    assert verify(B, k, 163840 + 8, 1 << 40) == EUNSUP
+    assert verify(B, 0, V, need) == EINVAL
+    assert verify(B, k, V, need, draft_ids=None) == EINVAL
+    assert verify(0, k, V, need) == OK  # an empty batch is a no-op
+    # verify attention: chunk sizes are 0 or multiples of 64 up to 1024; head_dim 128
+    assert L.sdx_verify_attention_workspace(8, 5, 32, 8, 16, 64, 96) == 0
+    assert L.sdx_verify_attention_workspace(8, 5, 32, 8, 16, 64, 0) > 0
+    rc = L.sdx_verify_attention_paged(fake, BF16, 8, fake, 5, 32, 8, 64, fake, fake, 100, 16,
+                                      fake, 64, fake, ctypes.c_float(0.125), 0, fake, 1 << 30,
+                                      fake, None, None)
+    assert rc == EUNSUP and b"head_dim" in L.sdx_last_error()
