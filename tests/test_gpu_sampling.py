@@ -401,6 +401,49 @@ def test_rejection_sample_ragged_config5_vocab():
     assert np.array_equal(f.cpu().numpy(), rf)
 
 
+def test_rejection_sample_ragged_graph_replays():
+    """Per-row k captured in a graph (k_max, workspace and outputs given, so the
+    call makes no host sync): replays over two input sets of one row layout,
+    with eager calls between, each equal to the oracle."""
+    from specdec import _lib
+    B, V = 16, 151936
+    ks = [1 + (3 * b) % 8 for b in range(B)]
+    names = ("target", "draft", "draft_ids", "u_accept", "u_final", "cu_k")
+    sets = [ragged_verify_inputs(B, V, seed=s, device=DEV, k=ks) for s in (11, 12)]
+    ref = [_ragged_oracle(x, 0.7, 0.9, 50) for x in sets]
+    static = {n: sets[0][n].clone() for n in names}
+    need = _lib.lib().sdx_verify_ragged_workspace(B, sum(ks) + B, V, 1)
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    out = (torch.empty(B, dtype=torch.int64, device=DEV),
+           torch.empty(B, dtype=torch.int64, device=DEV),
+           torch.empty(B, dtype=torch.uint8, device=DEV))
+
+    def call(src):
+        return S.rejection_sample_ragged(src["target"], src["draft"], src["draft_ids"],
+                                         src["u_accept"], src["u_final"], src["cu_k"],
+                                         k_max=max(ks), temperature=0.7, top_p=0.9, top_k=50,
+                                         workspace=ws, out=out)
+
+    def check(res, i):
+        for got, want in zip(res, ref[i]):
+            assert np.array_equal(got.cpu().numpy(), want)
+
+    check(call(static), 0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        res = call(static)
+    for rep in range(6):
+        i = rep % 2
+        for n in names:
+            static[n].copy_(sets[i][n])
+        g.replay()
+        torch.cuda.synchronize()
+        check(res, i)
+        check(call(sets[1 - i]), 1 - i)  # eager work between replays
+        torch.cuda.synchronize()
+
+
 def test_rejection_sample_ragged_equal_k_is_uniform():
     """cu_k = 4 * arange(B+1) over the reshaped B=64, k=4, V=151936 step gives
     the uniform verify bit for bit (576 rows, split rows included)."""
