@@ -108,7 +108,15 @@ int check_vocab(int dtype, int64_t V) {
 extern "C" {
 
 const char* sdx_last_error(void) { return g_err; }
-int sdx_version(void) { return 1; }
+int sdx_version(void) { return 2; }
+
+int sdx_workspace_init(void* workspace, size_t bytes, sdx_stream_t stream) {
+  if (!workspace && bytes) return fail(SDX_EINVAL, "sdx_workspace_init: null workspace");
+  if (((uintptr_t)workspace & 3u) != 0)
+    return fail(SDX_EINVAL, "sdx_workspace_init: workspace must be 4-byte aligned");
+  return hip_status(sdx::launch_workspace_init(workspace, bytes, (hipStream_t)stream),
+                    "workspace_init");
+}
 
 // ------------------------------------------------------------------ to_probs
 size_t sdx_to_probs_workspace(int64_t rows, int64_t vocab, int dtype) {
@@ -278,9 +286,10 @@ static size_t verify_ws_bytes(int64_t batch, int64_t ntgt, int64_t ndrf, int64_t
   sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; sdx::ChunkRec* rc; uint32_t* ct;
   uint64_t* ra;
   const int64_t rows = ntgt + ndrf;
+  c.take<uint8_t>(sdx::kWsHeaderBytes);  // magic word + split-row counters, fixed offsets
   transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jb, &rc, &ct, &ra);
   c.take<int64_t>(ntgt);  // greedy argmax
-  // rows split over blocks (counters that stay zero between calls, part histograms)
+  // part histograms of rows split over blocks
   c.take<uint8_t>(dtype == SDX_BF16 ? sdx::rowstream_split_bytes(rows, vocab) : 0);
   if (ragged) {
     c.take<int64_t>(ntgt);
@@ -370,6 +379,7 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
   uint32_t* counters;
   uint64_t* rank_acc;
   const int64_t rows = ntgt + ndrf;
+  uint32_t* header = c.take<uint32_t>(sdx::kWsHeaderBytes / 4);
   transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jobs, &recs, &counters, &rank_acc);
   int64_t* am = c.take<int64_t>(ntgt);
   const size_t split_bytes = dtype == SDX_BF16 ? sdx::rowstream_split_bytes(rows, vocab) : 0;
@@ -419,6 +429,7 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
     a.rank_acc = dtype == SDX_BF16 ? rank_acc : nullptr;
     a.split_ws = split_ws;
     a.split_bytes = split_bytes;
+    a.ws_header = header;
     if (int e = row_stats16(dtype, a, rows, s)) return e;
     // bf16: drafted tokens the row kernel could not rank (a tie group of several
     // values) are ranked by the draw's accept chain; the statistics-only call

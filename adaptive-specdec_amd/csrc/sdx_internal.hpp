@@ -20,8 +20,10 @@ enum RowFlag : uint32_t {
   kRowUnsupported = 1u << 2, // decision fell outside the histogram window
   kRowBelowWindow = 1u << 3, // elements below the histogram window carry mass
   kRowProbs = 1u << 4,       // final probabilities stored densely (fp32 path)
-  kRowRank = 1u << 5         // drafted token inside the partial tie group: pgather is
+  kRowRank = 1u << 5,        // drafted token inside the partial tie group: pgather is
                              // set by the rank kernel from its member rank
+  kRowBadWs = 1u << 6        // split row whose workspace header was not initialised
+                             // (sdx_workspace_init): statistics not computed
 };
 
 // 64 bytes per row. Keys in [glo, ghi] form the tie group that straddles the

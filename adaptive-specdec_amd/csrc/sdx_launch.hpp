@@ -6,6 +6,15 @@
 
 namespace sdx {
 
+// Workspaces of the verify entry points start with a fixed header: a magic
+// word that sdx_workspace_init writes, then the arrival counters of rows split
+// over several blocks. The counters sit at fixed offsets, so a workspace reused
+// for other shapes finds them where the last call left them, at zero.
+constexpr size_t kWsHeaderBytes = 4096;
+constexpr uint32_t kWsMagic = 0x53445857u;
+constexpr int kWsCounterWord = 64;  // first counter word (256-byte aligned)
+constexpr int kWsMaxCounters = (int)(kWsHeaderBytes / 4) - kWsCounterWord;
+
 struct RowStatArgs {
   const uint16_t* base[2];  // group 0: target rows, group 1: draft rows
   int64_t nrows[2];
@@ -28,12 +37,13 @@ struct RowStatArgs {
   // bf16 streaming kernel, rows split over several blocks (set by launch_rowstream_bf16
   // from split_ws / split_bytes): blocks [0, nwhole) take whole rows, the rows after
   // nwhole are taken by nparts blocks each, the last of which to finish merges them
-  uint8_t* split_ws;   // caller region: arrival counters (zero between launches), then
-  size_t split_bytes;  // the parts' packed histograms; null / too small: no split
+  uint8_t* split_ws;   // caller region for the parts' packed histograms; null / too
+  size_t split_bytes;  // small: no split
+  uint32_t* ws_header;  // the workspace header (magic, then the arrival counters), or null
   int64_t nwhole;
   int32_t nparts;
   int32_t xcd_group;  // a row's parts on blocks of one XCD (block index mod 8)
-  uint32_t* split_cnt;
+  uint32_t* split_cnt;  // the header's counters (set by launch_rowstream_bf16)
   uint8_t* split_parts;
 };
 
@@ -142,6 +152,8 @@ hipError_t launch_rowstream_bf16(const RowStatArgs& a, int64_t rows, hipStream_t
 // bytes of RowStatArgs::split_ws that let launch_rowstream_bf16 split rows over
 // several blocks on the current device (0: it would not split)
 size_t rowstream_split_bytes(int64_t rows, int64_t V);
+// zero `bytes` of a workspace and write the header's magic word
+hipError_t launch_workspace_init(void* ws, size_t bytes, hipStream_t s);
 // sdx_rank.hip: pgather of drafted tokens inside a partial tie group (after rowstream)
 hipError_t launch_rank_bf16(const RowStatArgs& a, int64_t rows, hipStream_t s);
 // sdx_f32.hip

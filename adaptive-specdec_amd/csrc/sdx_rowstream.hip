@@ -307,12 +307,20 @@ __device__ U128 below_sum(const uint16_t* __restrict__ ptr, int64_t V, uint32_t 
 // header with device-coherent stores, waits for them, then counts itself in on
 // the row's arrival counter; the part that arrives last adds the other parts
 // into its LDS histogram, their largest offsets into *omx and their token
-// counts into *cp, resets the counter to zero and returns true. The others
-// return false (and leave the kernel).
+// counts into *cp, resets the counter to zero and returns 1. The others return
+// 0 (and leave the kernel). When the workspace header lacks its magic word the
+// counters cannot be trusted: no part counts in and every part returns 2.
+//
+// Hand-off invariant: every store of a part's histogram and header and every
+// load of them by the merging part carries the sc1 cache policy (device
+// coherent: no XCD's L2 keeps a stale copy), and each part waits for its stores
+// (vmcnt(0)) before its relaxed agent-scope counter increment. A plain store or
+// load of the handed-off data added here would race across XCDs.
 typedef uint32_t sk_u32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ bool split_merge(uint32_t* __restrict__ cnt, uint8_t* parts, int P,
-                                            int64_t sidx, int part, uint32_t* hist,
-                                            uint32_t* omx, uint32_t* cp, int32_t* flag) {
+__device__ __forceinline__ int split_merge(const uint32_t* magic, uint32_t* __restrict__ cnt,
+                                           uint8_t* parts, int P, int64_t sidx, int part,
+                                           uint32_t* hist, uint32_t* omx, uint32_t* cp,
+                                           int32_t* flag) {
   const int tid = threadIdx.x;
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
       parts + sidx * P * (int64_t)SK_SPLIT_BYTES, (short)0, (int)(P * SK_SPLIT_BYTES), 0x00020000);
@@ -333,14 +341,18 @@ __device__ __forceinline__ bool split_merge(uint32_t* __restrict__ cnt, uint8_t*
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __syncthreads();
   if (tid == 0) {
-    const uint32_t prev =
-        __hip_atomic_fetch_add(cnt + sidx, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = prev == (uint32_t)(P - 1);
-    if (last) __hip_atomic_store(cnt + sidx, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    flag[0] = last ? 1 : 0;
+    int f = 2;
+    if (__hip_atomic_load(magic, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == kWsMagic) {
+      const uint32_t prev =
+          __hip_atomic_fetch_add(cnt + sidx, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = prev == (uint32_t)(P - 1);
+      if (last) __hip_atomic_store(cnt + sidx, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      f = last ? 1 : 0;
+    }
+    flag[0] = f;
   }
   __syncthreads();
-  if (!flag[0]) return false;
+  if (flag[0] != 1) return flag[0];
   // thread t owns chunks t, t + SK_NT, t + 2 SK_NT (SK_SPLIT_CHUNKS <= 3 SK_NT)
   static_assert(SK_SPLIT_CHUNKS <= 3 * SK_NT, "chunks per thread");
   uint32_t acc[3][8];
@@ -380,7 +392,7 @@ __device__ __forceinline__ bool split_merge(uint32_t* __restrict__ cnt, uint8_t*
   __syncthreads();
   *omx = om;
   *cp = cc;
-  return true;
+  return 1;
 }
 
 // All LDS of the kernel in one object, histogram first (LDS address 0, so the
@@ -570,8 +582,15 @@ rowstream_bf16_kernel(RowStatArgs a) {
     uint32_t cp = 0;
     if (g_in_groups || g_in_tail) cp = snap + blk_sum_u32(pre, L.red, rs);
     else if (has_g && gid >= (int64_t)g1 * 8) cp = hist[bin_g];
-    if (!split_merge(a.split_cnt, a.split_parts, P, sidx, part, hist, &omx_b, &cp, L.i32 + 11))
-      return;
+    const int mg = split_merge(a.ws_header, a.split_cnt, a.split_parts, P, sidx, part, hist,
+                               &omx_b, &cp, L.i32 + 11);
+    if (mg == 2 && part == 0 && tid == 0) {  // uninitialised workspace: flag the row
+      RowStat st = {};
+      st.flags = kRowBadWs | kRowUnsupported;
+      st.zf = 1.0f; st.totf = 1.0f; st.klo = 0x7FFFFFFF; st.glo = 1; st.ghi = 0; st.argmax = -1;
+      *st_out = st;
+    }
+    if (mg != 1) return;
     snap = cp;  // every part's count, this one's included
     pre = 0;
   }
@@ -965,7 +984,7 @@ static int split_layout(int64_t rows, int64_t V, int cus, int64_t* nwhole) {
   *nwhole = rows;
   if (cus <= 0 || rows <= 0) return 0;
   const int64_t whole = rows / cus * cus, rest = rows - whole;
-  if (rest == 0) return 0;
+  if (rest == 0 || rest > kWsMaxCounters) return 0;
   const int64_t n4 = V >> 3;
   int64_t p = cus / rest;
   if (p > 8) p = 8;
@@ -978,7 +997,7 @@ static int split_layout(int64_t rows, int64_t V, int cus, int64_t* nwhole) {
 static size_t split_need(int64_t rows, int64_t nwhole, int p) {
   if (p < 2) return 0;
   const int64_t rest = rows - nwhole;
-  return ((size_t)rest * 4 + 255) / 256 * 256 + (size_t)rest * p * SK_SPLIT_BYTES;
+  return (size_t)rest * p * SK_SPLIT_BYTES;
 }
 
 size_t rowstream_split_bytes(int64_t rows, int64_t V) {
@@ -993,15 +1012,16 @@ hipError_t launch_rowstream_bf16(const RowStatArgs& args, int64_t rows, hipStrea
   a.late_block = cus > 0 ? 2 * (int64_t)cus : INT64_MAX;
   int64_t nwhole;
   int p = split_layout(rows, a.V, cus, &nwhole);
-  if (p >= 2 && (!a.split_ws || a.split_bytes < split_need(rows, nwhole, p))) p = 0;
+  if (p >= 2 && (!a.split_ws || !a.ws_header || a.split_bytes < split_need(rows, nwhole, p)))
+    p = 0;
   int64_t grid = rows;
   if (p >= 2) {
     const int64_t rest = rows - nwhole;
     a.nwhole = nwhole;
     a.nparts = p;
     a.xcd_group = (nwhole % 8 == 0 && rest % 8 == 0) ? 1 : 0;
-    a.split_cnt = reinterpret_cast<uint32_t*>(a.split_ws);
-    a.split_parts = a.split_ws + ((size_t)rest * 4 + 255) / 256 * 256;
+    a.split_cnt = a.ws_header + kWsCounterWord;
+    a.split_parts = a.split_ws;
     grid = nwhole + rest * p;
   } else {
     a.nwhole = rows;
@@ -1011,6 +1031,24 @@ hipError_t launch_rowstream_bf16(const RowStatArgs& args, int64_t rows, hipStrea
     a.split_parts = nullptr;
   }
   hipLaunchKernelGGL(rowstream_bf16_kernel, dim3((unsigned)grid), dim3(SK_NT), 0, s, a);
+  return hipGetLastError();
+}
+
+// Zero a workspace and write the header's magic word, in one kernel (no memset,
+// so the call can sit in a captured graph).
+__global__ void workspace_init_kernel(uint32_t* ws, int64_t words) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += stride)
+    ws[i] = i == 0 ? kWsMagic : 0u;
+}
+
+hipError_t launch_workspace_init(void* ws, size_t bytes, hipStream_t s) {
+  const int64_t words = (int64_t)(bytes / 4);
+  if (words == 0) return hipSuccess;
+  int64_t blocks = (words + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(workspace_init_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                     (uint32_t*)ws, words);
   return hipGetLastError();
 }
 

@@ -244,6 +244,7 @@ __device__ inline int64_t accept_chain_wave(const AcceptArgs& a, int64_t b, Samp
     if (i < 2 * k + 1) rf = a.stats[i <= k ? trow0 + i : drow0 + (i - k - 1)].flags;
     if (__ballot((rf & kRowNonfinite) != 0)) fl |= SDX_FLAG_NONFINITE;
     if (__ballot((rf & kRowUnsupported) != 0)) fl |= SDX_FLAG_UNSUPPORTED;
+    if (__ballot((rf & kRowBadWs) != 0)) fl |= SDX_FLAG_WORKSPACE;
   }
   job->prow = n == k ? trow0 + k : trow0 + n;
   job->qrow = n == k ? -1 : drow0 + n;
@@ -879,6 +880,7 @@ __device__ inline int64_t chain16_wave(const AcceptArgs& a, const Eval16<FMT>& e
   const uint32_t rf = w3.x;  // RowStat::flags
   if (__ballot(lane < nr && (rf & kRowNonfinite) != 0)) fl |= SDX_FLAG_NONFINITE;
   if (__ballot(lane < nr && (rf & kRowUnsupported) != 0)) fl |= SDX_FLAG_UNSUPPORTED;
+  if (__ballot(lane < nr && (rf & kRowBadWs) != 0)) fl |= SDX_FLAG_WORKSPACE;
   const int lp = n == k ? k : n, lq = n == k ? -1 : k + 1 + n;
   if (lane == lp || lane == lq) {
     uint4* d = reinterpret_cast<uint4*>(st + (lane == lp ? 0 : 1));

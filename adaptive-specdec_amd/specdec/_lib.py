@@ -26,6 +26,7 @@ INT = ctypes.c_int
 _SIGS = {
     "sdx_last_error": (ctypes.c_char_p, []),
     "sdx_version": (INT, []),
+    "sdx_workspace_init": (INT, [P, SZ, P]),
     "sdx_to_probs_workspace": (SZ, [I64, I64, INT]),
     "sdx_to_probs": (INT, [P, INT, I64, I64, I64, F, F, I32, P, I64, P, SZ, P]),
     "sdx_sample_probs_workspace": (SZ, [I64, I64]),
@@ -113,5 +114,31 @@ def stream_of(t):
 
 
 def workspace(nbytes, device):
-    # zero-filled: the verify workspace carries counters that calls leave at zero
-    return torch.zeros(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+    """A new workspace of at least `nbytes`, prepared by sdx_workspace_init on the
+    current stream (zero-filled, header word set: the verify entry points keep
+    arrival counters in it that every call leaves at zero)."""
+    n = (max(int(nbytes), 1) + 255) // 256 * 256
+    ws = torch.empty(n, dtype=torch.uint8, device=device)
+    check(lib().sdx_workspace_init(ptr(ws), n, stream_of(ws)), "sdx_workspace_init")
+    return ws
+
+
+_WS_CACHE = {}
+
+
+def cached_workspace(nbytes, device, kind):
+    """The current stream's reusable workspace for entry points of one `kind`,
+    grown when too small. Calls queued on one stream run in order, so they may
+    share it; each stream has its own. Kinds never share memory: the verify
+    workspaces keep their header (magic word and zeroed counters) at fixed
+    offsets that other entry points would overwrite. Under graph capture a new
+    workspace is allocated (from the graph's pool) and not kept."""
+    dev = torch.device(device)
+    if torch.cuda.is_current_stream_capturing():
+        return workspace(nbytes, dev)
+    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream, kind)
+    ws = _WS_CACHE.get(key)
+    if ws is None or ws.numel() < int(nbytes):
+        ws = workspace(nbytes, dev)
+        _WS_CACHE[key] = ws
+    return ws

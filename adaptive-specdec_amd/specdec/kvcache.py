@@ -97,12 +97,17 @@ class RaggedCache(_HFCache):
         self.capacity = int(capacity)
         self._batch = int(batch_size)
         self.device = torch.device(device)
-        self.lengths_cpu = torch.zeros(self._batch, dtype=torch.long)
+        self._lengths_cpu = torch.zeros(self._batch, dtype=torch.long)
         self.lengths = torch.zeros(self._batch, dtype=torch.long, device=self.device)
         # device-side error flag of the scatter / device rollback kernels
         self.error = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.max_len = 0
         self._uniform = True
+        # After rollback_device the device lengths are authoritative and the host
+        # mirror is stale ("dirty"): max_len is then an upper bound of the true
+        # maximum (rollbacks only shrink rows), masks are built on the device from
+        # the device lengths, and host-side mutations re-read the lengths first.
+        self._dirty = False
         layers = [_RaggedLayer(self) for _ in range(n_layers)]
         if _HFCache is not object:
             super().__init__(layers=layers)
@@ -113,11 +118,25 @@ class RaggedCache(_HFCache):
     def batch_size(self):
         return self._batch
 
+    @property
+    def lengths_cpu(self):
+        """Host copy of the row lengths (`kvcache.py:102-113`). After
+        `rollback_device` it is re-read from the device first (one sync)."""
+        if self._dirty:
+            self.sync_lengths()
+        return self._lengths_cpu
+
+    @property
+    def host_stale(self):
+        """True while the device lengths have moved past the host mirror."""
+        return self._dirty
+
     def _push(self):
         """Mirror host lengths to the device (`kvcache.py:118-122`)."""
-        self.lengths.copy_(self.lengths_cpu, non_blocking=True)
-        self.max_len = int(self.lengths_cpu.max()) if self.batch_size else 0
-        self._uniform = bool(int(self.lengths_cpu.min()) == self.max_len) if self.batch_size else True
+        self.lengths.copy_(self._lengths_cpu, non_blocking=True)
+        self._dirty = False
+        self.max_len = int(self._lengths_cpu.max()) if self.batch_size else 0
+        self._uniform = bool(int(self._lengths_cpu.min()) == self.max_len) if self.batch_size else True
 
     # ---- geometry (`kvcache.py:125-162`)
     def kv_len_for(self, q):
@@ -132,8 +151,10 @@ class RaggedCache(_HFCache):
 
     def attn_mask(self, q, dtype, valid=None):
         """Additive [B, 1, q, kv_len] mask, 0 where s <= lengths[b] + j (and
-        s < valid[b]), finfo(dtype).min elsewhere; None when uniform and unpadded."""
-        if valid is None and self._uniform:
+        s < valid[b]), finfo(dtype).min elsewhere; None when uniform and unpadded.
+        While the host mirror is stale the mask is always built (from the device
+        lengths) and kv_len is the host's upper bound: the extra columns are masked."""
+        if valid is None and self._uniform and not self._dirty:
             return None
         kv_len = self.kv_len_for(q)
         out = torch.empty((self.batch_size, 1, q, kv_len), dtype=dtype, device=self.device)
@@ -146,11 +167,20 @@ class RaggedCache(_HFCache):
 
     # ---- mutation (`kvcache.py:165-202`)
     def advance(self, q):
-        self.lengths_cpu += int(q)
+        """lengths += q (`kvcache.py:165-168`). While the host mirror is stale the
+        device lengths advance in place (no host sync) and max_len stays an upper
+        bound."""
+        if self._dirty:
+            rc = _lib.lib().sdx_kv_advance(_lib.ptr(self.lengths), self.batch_size, int(q),
+                                           _lib.stream_of(self.lengths))
+            _lib.check(rc, "RaggedCache.advance")
+            self.max_len += int(q)
+            return
+        self._lengths_cpu += int(q)
         self._push()
 
     def set_lengths(self, lengths):
-        self.lengths_cpu.copy_(torch.as_tensor(lengths, dtype=torch.long).cpu())
+        self._lengths_cpu.copy_(torch.as_tensor(lengths, dtype=torch.long).cpu())
         self._push()
 
     def rollback(self, n):
@@ -161,32 +191,39 @@ class RaggedCache(_HFCache):
             n_cpu = n.detach().to("cpu", torch.long)
         else:
             n_cpu = torch.as_tensor(list(n), dtype=torch.long)
-        self.lengths_cpu -= n_cpu
-        if bool((self.lengths_cpu < 0).any()):
+        cur = self.lengths_cpu  # re-read first if a device rollback left it stale
+        new = cur - n_cpu
+        if bool((new < 0).any()):
             raise RuntimeError("RaggedCache.rollback below zero")
+        cur.copy_(new)
         self._push()
 
     def rollback_device(self, n):
         """Sync-free rollback by device counts n [B] (int64). Applies to the device
-        lengths only; if any row would go negative nothing changes and
-        `self.error` is set. The host mirror is refreshed by `sync_lengths()`."""
+        lengths; if any row would go negative nothing changes and `self.error` is
+        set. The host mirror becomes stale: until `sync_lengths()` (or a host-side
+        mutation, which re-reads it) `advance` runs on the device, max_len is an
+        upper bound and `attn_mask` is built from the device lengths."""
         _lib.require_gpu(n)
         n = n.to(torch.int64).contiguous()
         rc = _lib.lib().sdx_kv_rollback(_lib.ptr(self.lengths), self.batch_size, _lib.ptr(n),
                                         _lib.ptr(self.error), _lib.stream_of(n))
         _lib.check(rc, "RaggedCache.rollback_device")
+        self._dirty = True
+        self._uniform = False
 
     def sync_lengths(self):
         """Re-read device lengths into the host mirror (one device sync)."""
-        self.lengths_cpu.copy_(self.lengths.cpu())
-        self.max_len = int(self.lengths_cpu.max()) if self.batch_size else 0
-        self._uniform = bool(int(self.lengths_cpu.min()) == self.max_len) if self.batch_size else True
+        self._lengths_cpu.copy_(self.lengths.cpu())
+        self._dirty = False
+        self.max_len = int(self._lengths_cpu.max()) if self.batch_size else 0
+        self._uniform = bool(int(self._lengths_cpu.min()) == self.max_len) if self.batch_size else True
 
     def get_seq_length(self, layer_idx: int = 0):
         return self.max_len
 
     def reset(self):
-        self.lengths_cpu.zero_()
+        self._lengths_cpu.zero_()
         self._push()
         for layer in self.layers:
             if layer.is_initialized:

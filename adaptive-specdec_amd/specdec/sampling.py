@@ -68,7 +68,7 @@ def to_probs(logits, temperature=1.0, top_p=1.0, top_k=0):
         return out.reshape(shape)
     T, tp, tk = _switch_args(temperature, top_p, top_k)
     dt = _lib.dtype_code(x)
-    ws = _lib.workspace(L.sdx_to_probs_workspace(rows, V, dt), x.device)
+    ws = _lib.cached_workspace(L.sdx_to_probs_workspace(rows, V, dt), x.device, "to_probs")
     rc = L.sdx_to_probs(_lib.ptr(x), dt, rows, V, ld, T, tp, tk, _lib.ptr(out), V,
                         _lib.ptr(ws), ws.numel(), _lib.stream_of(x))
     _lib.check(rc, "to_probs")
@@ -91,7 +91,7 @@ def sample_from_probs(probs, generator=None, u=None):
     u = u.reshape(-1).to(torch.float32).contiguous()
     ids = torch.empty(rows, dtype=torch.int64, device=p.device)
     if rows:
-        ws = _lib.workspace(L.sdx_sample_probs_workspace(rows, V), p.device)
+        ws = _lib.cached_workspace(L.sdx_sample_probs_workspace(rows, V), p.device, "sample")
         rc = L.sdx_sample_probs(_lib.ptr(p), rows, V, ld, _lib.ptr(u), _lib.ptr(ids),
                                 _lib.ptr(ws), ws.numel(), _lib.stream_of(p))
         _lib.check(rc, "sample_from_probs")
@@ -110,7 +110,7 @@ def residual_probs(p, q):
     rows = pp.shape[0]
     out = torch.empty((rows, V), dtype=torch.float32, device=pp.device)
     if rows:
-        ws = _lib.workspace(L.sdx_residual_probs_workspace(rows, V), pp.device)
+        ws = _lib.cached_workspace(L.sdx_residual_probs_workspace(rows, V), pp.device, "residual")
         rc = L.sdx_residual_probs(_lib.ptr(pp), _lib.ptr(qq), rows, V, ld, _lib.ptr(out), V,
                                   _lib.ptr(ws), ws.numel(), _lib.stream_of(pp))
         _lib.check(rc, "residual_probs")
@@ -186,12 +186,12 @@ def rejection_sample(target_logits, draft_logits, draft_ids, u_accept, u_final, 
     dt = _lib.dtype_code(tl)
     st = _lib.stream_of(tl)
     if greedy:
-        ws = _lib.workspace(L.sdx_verify_greedy_workspace(B, k), dev)
+        ws = _lib.cached_workspace(L.sdx_verify_greedy_workspace(B, k), dev, "greedy")
         rc = L.sdx_verify_greedy(_lib.ptr(tl), dt, B, k, V, _lib.ptr(ids), _lib.ptr(ua),
                                  _lib.ptr(act), _lib.ptr(n_acc), _lib.ptr(y), _lib.ptr(flags),
                                  _lib.ptr(ws), ws.numel(), st)
     else:
-        ws = _lib.workspace(L.sdx_verify_workspace(B, k, V, dt), dev)
+        ws = _lib.cached_workspace(L.sdx_verify_workspace(B, k, V, dt), dev, "verify")
         rc = L.sdx_verify(_lib.ptr(tl), _lib.ptr(dl), dt, B, k, V, _lib.ptr(ids), _lib.ptr(ua),
                           _lib.ptr(uf), _lib.ptr(act), T, tp, tk, _lib.ptr(n_acc), _lib.ptr(y),
                           _lib.ptr(flags), _lib.ptr(ws), ws.numel(), st)
@@ -256,7 +256,7 @@ def rejection_sample_ragged(target_logits, draft_logits, draft_ids, u_accept, u_
     dt = _lib.dtype_code(tl)
     need = L.sdx_verify_ragged_workspace(B, NT, V, dt)
     if workspace is None or workspace.numel() < need:
-        workspace = _lib.workspace(need, dev)
+        workspace = _lib.cached_workspace(need, dev, "verify")
     rc = L.sdx_verify_ragged(_lib.ptr(tl), _lib.ptr(dl), dt, B, k_max, NT, V, _lib.ptr(cu),
                              _lib.ptr(ids), _lib.ptr(ua), _lib.ptr(uf), _lib.ptr(act), T, tp, tk,
                              _lib.ptr(n_acc), _lib.ptr(y), _lib.ptr(flags), _lib.ptr(workspace),

@@ -50,12 +50,24 @@ enum sdx_flag {
                                    than the row kernels' histogram windows cover (only with
                                    |logit| >= 2^18 at temperatures above ~2500, or fp16 rows
                                    spanning over 36 binades of mass): results unspecified */
-  SDX_FLAG_BAD_ROW = 8          /* per-row k: the row offsets (cu_k) were inconsistent with
+  SDX_FLAG_BAD_ROW = 8,         /* per-row k: the row offsets (cu_k) were inconsistent with
                                    k_max or the row counts; n_acc 0, y unspecified */
+  SDX_FLAG_WORKSPACE = 16       /* the verify workspace was not prepared by
+                                   sdx_workspace_init: results of the row unspecified */
 };
 
 const char* sdx_last_error(void);
 int sdx_version(void);
+
+/* Prepare a workspace for the entry points below: zero-fill `bytes` and write the
+ * header word the verify kernels check. Required once for a workspace of
+ * sdx_verify / sdx_verify_ragged / sdx_verify_stats (which keep arrival counters
+ * at fixed offsets of its first 4 KB and leave them at zero after every call);
+ * harmless for the others. Asynchronous on `stream`; no memset, so it may be
+ * captured in a graph. A verify call on a workspace that was never prepared does
+ * not trust its counters: the rows that would use them get SDX_FLAG_WORKSPACE.
+ * No reference counterpart (the reference allocates per call in torch). */
+int sdx_workspace_init(void* workspace, size_t bytes, sdx_stream_t stream);
 
 /* ---- sampling transforms: specdec/sampling.py ---------------------------
  * Switches follow sampling.py:43,52,56: temperature <= 0 -> greedy one-hot
@@ -95,9 +107,10 @@ int sdx_gather_prob(const float* probs, int64_t rows, int64_t vocab, int64_t ld,
  * (residual draw at position n_acc, or the bonus draw from p_{k+1} when n_acc == k),
  * flags [batch] (sdx_flag bits). Emitted tokens of row b: draft_ids[b, :n_acc[b]] then y[b];
  * KV rows to drop: k - n_acc[b] (engine.py:310).
- * Workspace: sized by sdx_verify_workspace for the current device. Zero-fill it once
- * before its first call: with bf16 logits it carries arrival counters of rows split
- * over several blocks, which every call leaves at zero. Calls that share a workspace
+ * Workspace: sized by sdx_verify_workspace for the current device and prepared once
+ * by sdx_workspace_init: with bf16 logits it carries arrival counters of rows split
+ * over several blocks at fixed offsets, which every call leaves at zero, so one
+ * workspace serves calls of any shape that fits it. Calls that share a workspace
  * must not overlap. */
 size_t sdx_verify_workspace(int64_t batch, int32_t k, int64_t vocab, int dtype);
 int sdx_verify(const void* target_logits, const void* draft_logits, int dtype,
@@ -117,7 +130,7 @@ int sdx_verify(const void* target_logits, const void* draft_logits, int dtype,
  * rows to drop: k_b - n_acc[b]). The offsets are checked on the device: if they are
  * inconsistent (not non-decreasing from 0 to target_rows - batch, or a k_b > k_max),
  * every row gets SDX_FLAG_BAD_ROW and n_acc 0. Workspace: sdx_verify_ragged_workspace,
- * zero-filled once, as for sdx_verify. No reference counterpart: the reference engine
+ * prepared once by sdx_workspace_init, as for sdx_verify. No reference counterpart: the reference engine
  * verifies one k for the whole batch (engine.py:281-312). */
 size_t sdx_verify_ragged_workspace(int64_t batch, int64_t target_rows, int64_t vocab, int dtype);
 int sdx_verify_ragged(const void* target_logits, const void* draft_logits, int dtype,

@@ -142,3 +142,15 @@ def test_verify_attention_graph_replays():
         assert torch.equal(verify_attention_paged(*args), eager)  # eager work between replays
         torch.cuda.synchronize()
     assert int(err.item()) == 0
+
+
+def test_verify_attention_long_rows_unstaged_merge():
+    """Chunks of 64 keys over contexts near 8192 with 9 query positions x group 4
+    (36 rows per KV head): 128 chunks x 36 rows = 4608 > 4096 chunk weights, so
+    the merge kernel forms its weights per element instead of staging them in
+    LDS."""
+    inp = attn_inputs(2, seed=64, device=DEV, ctx_lo=8000, ctx_hi=8192, hq=32, hkv=8, k_max=8,
+                      alpha_lo=0.97, alpha_hi=0.99)
+    nch = (int(inp["kv_len"].max()) + 63) // 64
+    assert nch * inp["max_q"] * 4 > 4096
+    _check(inp, 32, 8, chunk_tokens=64)

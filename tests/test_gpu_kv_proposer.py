@@ -68,6 +68,98 @@ def test_ragged_device_rollback_and_overflow_flag():
     assert int(cache.error.item()) == 1
 
 
+def test_ragged_device_rollback_then_advance_without_sync():
+    """The engine loop with device counts (`engine.py:248-312`): rollback_device,
+    then the next forward's positions / mask / update / advance with no
+    sync_lengths in between. Device lengths, mask and written slots equal the
+    oracle's; the host mirror is re-read only when asked for."""
+    B, H, Cap, D, q = 4, 2, 64, 16, 4
+    cache = RaggedCache(1, B, Cap, DEV)
+    plen = np.array([7, 5, 6, 9])
+    cache.set_lengths(plen)
+    keys = np.zeros((B, H, Cap, D), np.float32)
+    vals = np.zeros((B, H, Cap, D), np.float32)
+    k1 = torch.randn(B, H, q, D, device=DEV, dtype=torch.bfloat16)
+    v1 = torch.randn(B, H, q, D, device=DEV, dtype=torch.bfloat16)
+    cache.layers[0].update(k1, v1)
+    OK.ragged_update(keys, vals, plen, k1.float().cpu().numpy(), v1.float().cpu().numpy())
+    cache.advance(q)
+    drop = torch.tensor([3, 0, 2, 4], device=DEV)
+    cache.rollback_device(drop)                       # no host sync
+    assert cache.host_stale
+    len1 = OK.rollback(OK.advance(plen, q), drop.cpu().numpy())
+    q2 = 3
+    assert np.array_equal(cache.positions(q2).cpu().numpy(), OK.positions(len1, q2))
+    m = cache.attn_mask(q2, torch.float32)            # built from the device lengths
+    neg = float(torch.finfo(torch.float32).min)
+    ref = OK.attn_mask(len1, q2, neg)
+    kv = ref.shape[-1]
+    assert m.shape[-1] >= kv                          # host upper bound of max_len + q2
+    assert np.array_equal(m[..., :kv].cpu().numpy(), ref.astype(np.float32))
+    assert bool((m[..., kv:] == neg).all())
+    k2 = torch.randn(B, H, q2, D, device=DEV, dtype=torch.bfloat16)
+    v2 = torch.randn(B, H, q2, D, device=DEV, dtype=torch.bfloat16)
+    ks, _ = cache.layers[0].update(k2, v2)            # writes at the rolled-back offsets
+    assert ks.shape[2] == m.shape[-1]
+    OK.ragged_update(keys, vals, len1, k2.float().cpu().numpy(), v2.float().cpu().numpy())
+    cache.advance(q2)                                 # on the device while stale
+    assert cache.host_stale
+    assert np.array_equal(cache.layers[0].keys.float().cpu().numpy(), keys)
+    assert np.array_equal(cache.layers[0].values.float().cpu().numpy(), vals)
+    assert np.array_equal(cache.lengths.cpu().numpy(), OK.advance(len1, q2))
+    assert cache.lengths_cpu.tolist() == OK.advance(len1, q2).tolist()   # re-read on access
+    assert not cache.host_stale and cache.max_len == int(OK.advance(len1, q2).max())
+    cache.rollback_device(torch.tensor([1, 1, 1, 1], device=DEV))
+    cache.rollback([1, 0, 0, 2])                      # host rollback re-reads first
+    assert cache.lengths.cpu().tolist() == (OK.advance(len1, q2) - [2, 1, 1, 3]).tolist()
+    assert int(cache.error.item()) == 0
+
+
+def _checksum(flat, chunk=1 << 28):
+    """Sum of an int16 tensor in int64, a chunk at a time (torch would upcast the
+    whole tensor at once)."""
+    tot = torch.zeros((), dtype=torch.int64, device=flat.device)
+    for i in range(0, flat.numel(), chunk):
+        tot += flat[i:i + chunk].sum(dtype=torch.int64)
+    return int(tot)
+
+
+def test_paged_append_config4_full_size():
+    """The paged-KV workload at full size: 64 layers sharing one block table, B=64,
+    lengths ~ U[512, 4096], 5 positions per row, 8 x 128 bf16, block 16 (69 GB of
+    pool). The appended slots of every (layer, side, row) equal the staged rows
+    byte for byte; a checksum of the whole pool moves by exactly the bytes
+    written (no stray writes); lengths after commit + rollback equal len + keep."""
+    L, B, q, H, D, bs = 64, 64, 5, 8, 128, 16
+    inp = kv_inputs(L, B, q, H, D, bs, 512, 4096, seed=3, device=DEV)
+    c = PagedKVCache(L, B, inp["num_blocks"], bs, H, D, inp["max_blocks"], device=DEV)
+    c.block_table.copy_(inp["block_table"])
+    c.lengths.copy_(inp["lengths"])
+    flat = c.pool.view(torch.int16).view(-1)
+    flat.random_(-32768, 32767)                       # pre-existing pages: random bytes
+    lengths = inp["lengths"].cpu().numpy()
+    bt = inp["block_table"].cpu().numpy()
+    pos = lengths[:, None] + np.arange(q)[None, :]                        # [B, q]
+    slot = bt[np.arange(B)[:, None], pos // bs].astype(np.int64) * bs + pos % bs
+    assert pos.min() >= 512 and (pos // bs).max() >= 250    # positions >= 512, block index >= 32
+    side_rows = inp["num_blocks"] * bs                                    # rows per (layer, side)
+    base = (np.arange(L)[:, None] * 2 + np.arange(2)[None, :]) * side_rows    # [L, 2]
+    rows = torch.tensor((base[:, :, None, None] + slot[None, None]).reshape(-1), device=DEV)
+    view = c.pool.view(-1, H * D)
+    old = view[rows].view(torch.int16)
+    before = _checksum(flat) - int(old.sum(dtype=torch.int64))
+    c.append(inp["staged"])
+    got = view[rows].view(torch.int16)
+    staged = inp["staged"].view(torch.int16).reshape(-1, H * D)           # [L, 2, B, q] order
+    assert torch.equal(got, staged)
+    after = _checksum(flat) - int(staged.sum(dtype=torch.int64))
+    assert after == before
+    c.commit(q)
+    c.rollback(q - inp["keep"])
+    assert np.array_equal(c.lengths.cpu().numpy(), lengths + inp["keep"].cpu().numpy())
+    assert int(c.error.item()) == 0
+
+
 def test_paged_append_commit_rollback():
     L, B, q, H, D, bs = 4, 8, 5, 8, 128, 16
     inp = kv_inputs(L, B, q, H, D, bs, 20, 100, seed=1, device=DEV)

@@ -412,8 +412,7 @@ def test_rejection_sample_ragged_graph_replays():
     sets = [ragged_verify_inputs(B, V, seed=s, device=DEV, k=ks) for s in (11, 12)]
     ref = [_ragged_oracle(x, 0.7, 0.9, 50) for x in sets]
     static = {n: sets[0][n].clone() for n in names}
-    need = _lib.lib().sdx_verify_ragged_workspace(B, sum(ks) + B, V, 1)
-    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    ws = _lib.workspace(_lib.lib().sdx_verify_ragged_workspace(B, sum(ks) + B, V, _lib.BF16), DEV)
     out = (torch.empty(B, dtype=torch.int64, device=DEV),
            torch.empty(B, dtype=torch.int64, device=DEV),
            torch.empty(B, dtype=torch.uint8, device=DEV))
