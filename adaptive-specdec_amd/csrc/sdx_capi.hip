@@ -4,6 +4,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "sdx_launch.hpp"
 
 namespace {
@@ -277,6 +279,45 @@ int sdx_gather_prob(const float* probs, int64_t rows, int64_t vocab, int64_t ld,
                     "gather");
 }
 
+// ------------------------------------------------------------------ allocation-free verify
+// sdx_verify_noalloc runs sdx_verify on a library-owned device array instead of
+// a caller workspace. Each GPU the library runs on holds its own copy of the
+// array until the process ends. In host code `scratch` names a host-side
+// stand-in, not device memory: the device address comes from
+// hipGetSymbolAddress, once per device (with that device current), and only
+// that address is ever handed to kernels.
+namespace {
+constexpr size_t kScratchBytes = (size_t)24 << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address; on a device's first use, looked up and
+// prepared (zero-filled, header word written) by a kernel queued on `s`.
+int scratch_for_current_device(hipStream_t s, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(SDX_EHIP, "sdx_verify_noalloc: no current device (or device index >= %d)",
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (int e = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                           "sdx_verify_noalloc: hipGetSymbolAddress"))
+      return e;
+    if (!p) return fail(SDX_EHIP, "sdx_verify_noalloc: scratch has no device address");
+    if (int e = hip_status(sdx::launch_workspace_init(p, kScratchBytes, s),
+                           "sdx_verify_noalloc: scratch init"))
+      return e;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SDX_OK;
+}
+}  // namespace
+
 // ------------------------------------------------------------------ verify
 // verify workspace for ntgt target and ndrf draft rows (per-row k adds the
 // target row map and the bad-row bytes)
@@ -451,6 +492,26 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
   return hip_status(sdx::launch_draw16(dtype, src, st, tb, temperature, &aa, jobs, batch, vocab,
                                        recs, counters, y, s),
                     "draw16");
+}
+
+int sdx_verify_noalloc(const void* target_logits, const void* draft_logits, int dtype,
+                       int64_t batch, int32_t k, int64_t vocab, const int64_t* draft_ids,
+                       const float* u_accept, const float* u_final, const uint8_t* active,
+                       float temperature, float top_p, int32_t top_k, int64_t* n_acc, int64_t* y,
+                       uint8_t* flags, sdx_stream_t stream) {
+  if (batch < 0 || k < 1 || !dtype_ok(dtype))
+    return fail(SDX_EINVAL, "sdx_verify_noalloc: bad arguments");
+  const size_t need = sdx_verify_workspace(batch, k, vocab, dtype);
+  if (need > kScratchBytes)
+    return fail(SDX_EWORKSPACE,
+                "sdx_verify_noalloc: batch %lld, k %d, vocab %lld need %zu bytes of scratch, more "
+                "than its %zu; use sdx_verify with a workspace",
+                (long long)batch, k, (long long)vocab, need, kScratchBytes);
+  void* ws = nullptr;
+  if (int e = scratch_for_current_device((hipStream_t)stream, &ws)) return e;
+  return sdx_verify(target_logits, draft_logits, dtype, batch, k, vocab, draft_ids, u_accept,
+                    u_final, active, temperature, top_p, top_k, n_acc, y, flags, ws,
+                    kScratchBytes, stream);
 }
 
 size_t sdx_verify_greedy_workspace(int64_t batch, int32_t k) {

@@ -36,6 +36,7 @@ _SIGS = {
     "sdx_gather_prob": (INT, [P, I64, I64, I64, P, P, P]),
     "sdx_verify_workspace": (SZ, [I64, I32, I64, INT]),
     "sdx_verify": (INT, [P, P, INT, I64, I32, I64, P, P, P, P, F, F, I32, P, P, P, P, SZ, P]),
+    "sdx_verify_noalloc": (INT, [P, P, INT, I64, I32, I64, P, P, P, P, F, F, I32, P, P, P, P]),
     "sdx_verify_ragged_workspace": (SZ, [I64, I64, I64, INT]),
     "sdx_verify_ragged": (INT, [P, P, INT, I64, I32, I64, I64, P, P, P, P, P, F, F, I32, P, P, P, P,
                                 SZ, P]),

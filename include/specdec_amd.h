@@ -120,6 +120,22 @@ int sdx_verify(const void* target_logits, const void* draft_logits, int dtype,
                int64_t* n_acc, int64_t* y, uint8_t* flags,
                void* workspace, size_t workspace_bytes, sdx_stream_t stream);
 
+/* sdx_verify without a workspace, for callers that cannot allocate device memory
+ * (code under graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. Same arguments, outputs and
+ * rules as sdx_verify; the scratch is a 24 MiB device array inside the library,
+ * one per GPU, held until the process ends, prepared by a kernel queued on
+ * `stream` at the first call on each device. Nothing is allocated. Requests
+ * whose sdx_verify_workspace exceeds 24 MiB (more than about 1,152 logit rows
+ * at vocab 151,936, e.g. batch 128 at k = 4) return SDX_EWORKSPACE. All calls on
+ * one GPU share its array: calls that may overlap (other streams, other host
+ * threads) race and must be serialised by the caller. */
+int sdx_verify_noalloc(const void* target_logits, const void* draft_logits, int dtype,
+                       int64_t batch, int32_t k, int64_t vocab,
+                       const int64_t* draft_ids, const float* u_accept, const float* u_final,
+                       const uint8_t* active, float temperature, float top_p, int32_t top_k,
+                       int64_t* n_acc, int64_t* y, uint8_t* flags, sdx_stream_t stream);
+
 /* Verify with a different k per batch row (config 5's adaptive k): row b drafts
  * k_b = cu_k[b+1] - cu_k[b] tokens, 0 <= k_b <= k_max (cu_k int64 [batch+1] on the
  * device, cu_k[0] = 0). Rows are packed: target_logits [target_rows, vocab] with
