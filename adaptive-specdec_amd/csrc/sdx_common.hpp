@@ -52,60 +52,51 @@ __device__ __forceinline__ uint32_t key_of_f32(float x) {
 }
 
 // ---------------------------------------------------------------- exp_det
-// fp32 exp(d): Cody-Waite reduction and a degree-13 Taylor polynomial in
-// float64 with plain multiply/add, one rounding to fp32 at the end; 0 below
-// -104 (under half the smallest fp32 denormal).
-__device__ __forceinline__ float exp_det(float d) {
+// Deterministic fp32 exp(d), one fixed sequence of IEEE operations:
+//   k = floor(fl64(d * (1/ln2)))  and  r = fl32(fl64(d - fl64(k * ln2))),
+//   clamped below at 0, so r lies in [0, ln2];
+//   p = the degree-9 Taylor polynomial of exp at r in fp32 Horner form
+//       (coefficients fl32(1/n!), plain multiply then add), clamped above at 2;
+//   e = p * 2^k, rounded once when the result is subnormal;
+//   0 for d < -104 (below half the smallest fp32 denormal) and for NaN.
+// Within 2 ulps of a correctly rounded expf. Non-decreasing in d, which the
+// value-ordered histogram walks rely on: inside one k every Horner step is
+// monotone in r (r >= 0, positive coefficients), and across k -> k+1 the left
+// value is at most 2 * 2^k (the clamp) while the right one is at least 2^(k+1)
+// (r >= 0 gives p >= 1).
+__device__ __forceinline__ float exp_det_core(float d) {
 #pragma clang fp contract(off)
-  if (!(d >= -104.0f)) return 0.0f;
   const double kInvLn2 = 0x1.71547652b82fep+0;
-  const double kLn2Hi = 0x1.62e42fee00000p-1;
-  const double kLn2Lo = 0x1.a39ef35793c76p-33;
+  const double kLn2 = 0x1.62e42fefa39efp-1;
   const double dd = (double)d;
-  const double k = rint(dd * kInvLn2);
-  const double r = (dd - k * kLn2Hi) - k * kLn2Lo;
-  double p = 0x1.6124613a86d09p-33;
-  p = p * r + 0x1.1eed8eff8d898p-29;
-  p = p * r + 0x1.ae64567f544e4p-26;
-  p = p * r + 0x1.27e4fb7789f5cp-22;
-  p = p * r + 0x1.71de3a556c734p-19;
-  p = p * r + 0x1.a01a01a01a01ap-16;
-  p = p * r + 0x1.a01a01a01a01ap-13;
-  p = p * r + 0x1.6c16c16c16c17p-10;
-  p = p * r + 0x1.1111111111111p-7;
-  p = p * r + 0x1.5555555555555p-5;
-  p = p * r + 0x1.5555555555555p-3;
-  p = p * r + 0x1.0000000000000p-1;
-  p = p * r + 0x1.0000000000000p+0;
-  p = p * r + 0x1.0000000000000p+0;
-  return (float)ldexp(p, (int)k);
+  const double kf = floor(dd * kInvLn2);
+  const float r = fmaxf((float)(dd - kf * kLn2), 0.0f);
+  float p = 0x1.71de3ap-19f;  // 1/9!
+  p = p * r + 0x1.a01a02p-16f;  // 1/8!
+  p = p * r + 0x1.a01a02p-13f;  // 1/7!
+  p = p * r + 0x1.6c16c2p-10f;  // 1/6!
+  p = p * r + 0x1.111112p-7f;   // 1/5!
+  p = p * r + 0x1.555556p-5f;   // 1/4!
+  p = p * r + 0x1.555556p-3f;   // 1/3!
+  p = p * r + 0x1p-1f;          // 1/2!
+  p = p * r + 1.0f;             // 1/1!
+  p = p * r + 1.0f;             // 1/0!
+  p = fminf(p, 2.0f);
+  const int k = (int)kf;
+  const bool normal = k >= -126;
+  // 2^k, or 2^(k+64) then 2^-64 below the normal range (one rounding)
+  const float e = p * __uint_as_float((uint32_t)((normal ? k : k + 64) + 127) << 23);
+  return normal ? e : e * 0x1p-64f;
+}
+__device__ __forceinline__ float exp_det(float d) {
+  if (!(d >= -104.0f)) return 0.0f;
+  return exp_det_core(d);
 }
 
 // exp_det without the early exit: the same value, 0 below -104 (and for NaN)
 // by a final select, so that independent evaluations can interleave.
 __device__ __forceinline__ float exp_det_sel(float d) {
-#pragma clang fp contract(off)
-  const double kInvLn2 = 0x1.71547652b82fep+0;
-  const double kLn2Hi = 0x1.62e42fee00000p-1;
-  const double kLn2Lo = 0x1.a39ef35793c76p-33;
-  const double dd = (double)fmaxf(d, -105.0f);
-  const double k = rint(dd * kInvLn2);
-  const double r = (dd - k * kLn2Hi) - k * kLn2Lo;
-  double p = 0x1.6124613a86d09p-33;
-  p = p * r + 0x1.1eed8eff8d898p-29;
-  p = p * r + 0x1.ae64567f544e4p-26;
-  p = p * r + 0x1.27e4fb7789f5cp-22;
-  p = p * r + 0x1.71de3a556c734p-19;
-  p = p * r + 0x1.a01a01a01a01ap-16;
-  p = p * r + 0x1.a01a01a01a01ap-13;
-  p = p * r + 0x1.6c16c16c16c17p-10;
-  p = p * r + 0x1.1111111111111p-7;
-  p = p * r + 0x1.5555555555555p-5;
-  p = p * r + 0x1.5555555555555p-3;
-  p = p * r + 0x1.0000000000000p-1;
-  p = p * r + 0x1.0000000000000p+0;
-  p = p * r + 0x1.0000000000000p+0;
-  const float e = (float)ldexp(p, (int)k);
+  const float e = exp_det_core(fmaxf(d, -105.0f));
   return d >= -104.0f ? e : 0.0f;
 }
 

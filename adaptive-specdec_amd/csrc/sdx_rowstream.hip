@@ -59,6 +59,7 @@ constexpr int SK_BIN_EXC = 2 * SK_WIN + 2;
 constexpr int SK_NB = 2 * SK_WIN + 4;     // bins, the last one (SK_NB - 1) unused
 constexpr int SK_ETOP = 1024;             // exp values cached for the top bins
 constexpr int SK_ZQ = 3 * kWave;          // per-wave queue of occupied bins (normaliser)
+constexpr int SK_PW = 8 * kWave;          // top bins the top-p walk covers with one wave
 // Rows split over several blocks: each part publishes its histogram as u16
 // counts, 8 bins per 16-byte chunk, then a header chunk (its largest bin
 // offset, its count of equal-bin elements before the drafted token).
@@ -403,6 +404,7 @@ struct SkLds {
   uint32_t zq[SK_NW][SK_ZQ];  // per-wave queues of occupied bins for the normaliser
   SkRed red;
   int32_t i32[12];
+  int32_t pw[5];  // top-p walk of wave 0: boundary bin (or -1), its group bins and counts
   uint64_t x64[2];
   uint32_t unit_ctr;  // next 4 KB unit of the row to stream
 };
@@ -790,7 +792,56 @@ rowstream_bf16_kernel(RowStatArgs a) {
     float pb = 0.0f;
     int gtop0 = 0, gbot0 = 0;
     uint32_t above0 = 0, gcnt0 = 0;
-    for (int top = bmax; top >= klo_bin; top -= SK_NT) {
+    // Wave 0 walks the top SK_PW bins first, 64 at a time (one wave scan each,
+    // no barrier): a nucleus of a few hundred values ends there, and the other
+    // blocks on the CU keep their issue slots. Past them the block takes over in
+    // rounds of SK_NT bins.
+    if (tid < kWave) {
+      uint64_t Sw = 0;
+      int fb = -1;
+      uint64_t sb0 = 0;
+      int g0 = 0, g1 = 0;
+      uint32_t ab = 0, gc = 0;
+      for (int top = bmax; top >= klo_bin && top > bmax - SK_PW; top -= kWave) {
+        const int b = top - lane;
+        const uint32_t c = b >= klo_bin ? hist[b] : 0u;
+        const float p = c ? p_of_bin(b) : 0.0f;
+        const uint64_t mi = (uint64_t)c * fixed62(p);
+        const uint64_t incl = wave_incl_scan_u64(mi, lane);
+        const bool fail = c != 0 && !((rn32_u64(Sw + incl) - p) < tp);
+        const uint64_t fm = __ballot(fail);
+        if (fm) {  // the boundary bin is in this chunk (uniform)
+          const int tf = __ffsll((unsigned long long)fm) - 1;
+          fb = top - tf;
+          const float pbw = p_of_bin(fb);
+          const uint64_t ex = incl - mi;
+          sb0 = Sw + (((uint64_t)rdlane((uint32_t)(ex >> 32), tf) << 32) | rdlane((uint32_t)ex, tf));
+          const bool in_g = c != 0 && p == pbw;
+          g0 = (int)wave_max_u32(in_g ? (uint32_t)b : 0u);
+          g1 = (int)~wave_max_u32(~(in_g ? (uint32_t)b : 0xFFFFFFFFu));
+          ab = wave_sum_u32(in_g && b > fb ? c : 0u);
+          gc = wave_sum_u32(in_g ? c : 0u);
+          break;
+        }
+        Sw += ((uint64_t)rdlane((uint32_t)(incl >> 32), kWave - 1) << 32) |
+              rdlane((uint32_t)incl, kWave - 1);
+      }
+      if (tid == 0) {
+        L.pw[0] = fb; L.pw[1] = g0; L.pw[2] = g1; L.pw[3] = (int32_t)ab;
+        L.pw[4] = (int32_t)gc;
+        L.x64[0] = fb >= 0 ? sb0 : Sw;
+      }
+    }
+    __syncthreads();
+    if (L.pw[0] >= 0) {  // uniform
+      bb = L.pw[0];
+      pb = p_of_bin(bb);
+      gtop0 = L.pw[1]; gbot0 = L.pw[2];
+      above0 = (uint32_t)L.pw[3]; gcnt0 = (uint32_t)L.pw[4];
+    } else {
+      S = L.x64[0];
+    }
+    for (int top = bmax - SK_PW; bb < 0 && top >= klo_bin; top -= SK_NT) {
       const int b = top - tid;
       const uint32_t c = b >= klo_bin ? hist[b] : 0u;
       const float p = c ? p_of_bin(b) : 0.0f;

@@ -7,11 +7,18 @@ machine they run on (the fp32 softmax denominator carries ~1e-6 relative
 noise), so "bit-exact" decisions need a rule that every implementation can
 reproduce. The rule used throughout:
 
-* exp_det(d):   fp32 result of exp(d) evaluated in float64 (Cody-Waite
-                reduction + degree-13 Taylor, plain mul/add, no FMA) and
-                rounded once to fp32; 0 for d < -104 (below half the
-                smallest fp32 denormal). Differs from a correctly rounded
-                expf only when exp(d) lies within ~1e-16 of an fp32 midpoint.
+* exp_det(d):   fp32 exp(d) by one fixed sequence of IEEE operations:
+                k = floor(fl64(d / ln2)) and r = fl32(d - k ln2) in float64
+                (r clamped below at 0, so r lies in [0, ln2]); the degree-9
+                Taylor polynomial of exp at r in fp32 Horner form (plain
+                multiply, then add; coefficients fl32(1/n!)), clamped above at
+                2; times 2**k (rounded once when the result is subnormal); 0
+                for d < -104 (below half the smallest fp32 denormal). Within 2
+                ulps of a correctly rounded expf, and non-decreasing in d: the
+                Horner steps are monotone in r because r >= 0 and every
+                coefficient is positive, and at each k -> k+1 step the left
+                value is at most 2 * 2**k (the clamp) while the right one is at
+                least 2**(k+1) (r >= 0 gives p >= 1).
 * fixed62(x):   floor(x * 2**62) as an unsigned integer, for fp32 x in [0, 1].
                 Exact for x >= 2**-39; every mass, cumulative sum and sampling
                 CDF is accumulated in this fixed point, so it is exact and
@@ -25,45 +32,51 @@ exact, so `rn32(fixed62 prefix)` equals the reference's `cum` value bit for bit.
 """
 import numpy as np
 
-# exp_det constants (float64, written in hex so the HIP restatement uses the
-# identical bits).
+# exp_det constants, written in hex so the HIP restatement uses the identical
+# bits: 1/ln2 and ln2 in float64, and fl32(1/n!) for n = 9 .. 0 (Horner order).
 INV_LN2 = float.fromhex("0x1.71547652b82fep+0")
-LN2_HI = float.fromhex("0x1.62e42fee00000p-1")   # 32 significant bits: k*LN2_HI exact
-LN2_LO = float.fromhex("0x1.a39ef35793c76p-33")
-# 1/n! for n = 13 .. 0 (Horner order)
-EXP_TAYLOR = [float.fromhex(h) for h in (
-    "0x1.6124613a86d09p-33",  # 1/13!
-    "0x1.1eed8eff8d898p-29",  # 1/12!
-    "0x1.ae64567f544e4p-26",  # 1/11!
-    "0x1.27e4fb7789f5cp-22",  # 1/10!
-    "0x1.71de3a556c734p-19",  # 1/9!
-    "0x1.a01a01a01a01ap-16",  # 1/8!
-    "0x1.a01a01a01a01ap-13",  # 1/7!
-    "0x1.6c16c16c16c17p-10",  # 1/6!
-    "0x1.1111111111111p-7",   # 1/5!
-    "0x1.5555555555555p-5",   # 1/4!
-    "0x1.5555555555555p-3",   # 1/3!
-    "0x1.0000000000000p-1",   # 1/2!
-    "0x1.0000000000000p+0",   # 1/1!
-    "0x1.0000000000000p+0",   # 1/0!
+LN2 = float.fromhex("0x1.62e42fefa39efp-1")
+EXP_TAYLOR32 = [np.float32(float.fromhex(h)) for h in (
+    "0x1.71de3ap-19",   # 1/9!
+    "0x1.a01a02p-16",   # 1/8!
+    "0x1.a01a02p-13",   # 1/7!
+    "0x1.6c16c2p-10",   # 1/6!
+    "0x1.111112p-7",    # 1/5!
+    "0x1.555556p-5",    # 1/4!
+    "0x1.555556p-3",    # 1/3!
+    "0x1p-1",           # 1/2!
+    "0x1p+0",           # 1/1!
+    "0x1p+0",           # 1/0!
 )]
 EXP_CUTOFF = np.float32(-104.0)
 TWO62 = float(2 ** 62)
 
 
+def exp_det_poly(r):
+    """The fp32 Horner evaluation of exp at r (fp32 array, r >= 0), clamped at 2."""
+    r = np.asarray(r, np.float32)
+    p = np.full(r.shape, EXP_TAYLOR32[0], np.float32)
+    for c in EXP_TAYLOR32[1:]:
+        p = (p * r).astype(np.float32)
+        p = (p + c).astype(np.float32)
+    return np.minimum(p, np.float32(2.0))
+
+
 def exp_det(d):
     """fp32 exp(d) under the deterministic rule above. d: fp32 array."""
     d = np.asarray(d, dtype=np.float32)
-    with np.errstate(all="ignore"):                 # -inf inputs go through the cutoff
+    with np.errstate(all="ignore"):                 # -inf / NaN inputs go through the cutoff
         dd = d.astype(np.float64)
-        k = np.rint(dd * INV_LN2)
-        r = (dd - k * LN2_HI) - k * LN2_LO
-        p = np.full_like(r, EXP_TAYLOR[0])
-        for c in EXP_TAYLOR[1:]:
-            p = p * r + c
-        k_int = np.nan_to_num(np.clip(k, -2000, 2000)).astype(np.int64)
-        out = np.ldexp(p, k_int).astype(np.float32)
-    out = np.where(d < EXP_CUTOFF, np.float32(0.0), out)
+        kf = np.floor(dd * INV_LN2)
+        r = np.maximum((dd - kf * LN2).astype(np.float32), np.float32(0.0))
+        p = exp_det_poly(r)
+        k = np.nan_to_num(np.clip(kf, -200, 200)).astype(np.int64)
+        normal = k >= -126
+        sh = np.where(normal, k, k + 64) + 127
+        scale = (np.clip(sh, 1, 254).astype(np.uint32) << np.uint32(23)).view(np.float32)
+        e = (p * scale).astype(np.float32)
+        e = np.where(normal, e, (e * np.float32(2.0 ** -64)).astype(np.float32))
+    out = np.where(d >= EXP_CUTOFF, e, np.float32(0.0))
     return out.astype(np.float32)
 
 

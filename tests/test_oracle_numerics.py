@@ -1,18 +1,22 @@
 """Pins for the deterministic arithmetic in `oracle/numerics.py`.
 
 exp_det is checked against float64 `math.exp` rounded to fp32 (a library
-routine), for monotonicity (the nucleus order relies on it), and at its
-special points; fixed62 / rn32 / uniform_threshold against exact rational
-arithmetic.
+routine), at its special points, and for monotonicity (the nucleus order
+relies on it): the premises of the argument in `oracle/numerics.py` (Horner
+value 1 at r = 0, at most 2 up to the largest reduced argument, r >= 0), a
+dense sweep around every range-reduction step, and, with SDX_EXHAUSTIVE=1, all
+1,120,927,745 fp32 inputs in [-104, 0]. fixed62 / rn32 / uniform_threshold are
+checked against exact rational arithmetic.
 """
 import math
+import os
 from fractions import Fraction
 
 import numpy as np
 import pytest
 
-from oracle.numerics import (LN2_HI, exp_det, fixed62, fixed62_sum, rn32, rn32_u64,
-                             uniform_threshold)
+from oracle.numerics import (INV_LN2, LN2, exp_det, exp_det_poly, fixed62, fixed62_sum, rn32,
+                             rn32_u64, uniform_threshold)
 
 
 def _rn32_fraction(fr):
@@ -29,35 +33,73 @@ def test_exp_det_matches_rounded_libm():
     got = exp_det(d)
     ref = np.array([math.exp(float(x)) for x in d]).astype(np.float32)
     diff = np.abs(got.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
-    assert diff.max() <= 1
-    assert (diff == 0).mean() > 0.9999
+    assert diff.max() <= 2
+    assert (diff == 0).mean() > 0.8
 
 
 def test_exp_det_special_points():
     assert exp_det(np.float32([0.0]))[0] == np.float32(1.0)
     assert exp_det(np.float32([-104.01]))[0] == 0.0
     assert exp_det(np.float32([-np.inf]))[0] == 0.0
-    # denormal range is produced, not flushed
+    assert exp_det(np.float32([np.nan]))[0] == 0.0
+    # exact powers of two where the reduced argument is 0
+    assert exp_det(np.float32([-np.log(2.0) * 0.0]))[0] == 1.0
+    # denormal range is produced, not flushed, and rounded once
     v = exp_det(np.float32([-100.0]))[0]
     assert 0 < v < np.finfo(np.float32).tiny
+    assert abs(float(v) - math.exp(-100.0)) <= 2.0 ** -150
+
+
+def test_exp_det_monotone_premises():
+    """The three facts the monotonicity argument needs, checked directly."""
+    # Horner value exactly 1 at r = 0, so p >= 1 at the start of every interval
+    assert exp_det_poly(np.float32([0.0]))[0] == np.float32(1.0)
+    # the Horner value never exceeds 2: p is non-decreasing in r >= 0, so the
+    # 2^20 fp32 values up to a few ulps past fl32(ln2) (the largest reduced
+    # argument) cover the top; a sorted sample checks the order below them
+    top = int(np.float32(math.log(2.0)).view(np.int32)) + 8
+    r = np.arange(top - (1 << 20), top + 1, dtype=np.int32).view(np.float32)
+    p = exp_det_poly(r)
+    assert np.all(np.diff(p) >= 0) and p.max() <= 2.0
+    rs = np.random.RandomState(4)
+    r = np.sort(rs.uniform(0, math.log(2.0), 500000).astype(np.float32))
+    assert np.all(np.diff(exp_det_poly(r)) >= 0)
+    # the reduction never leaves r below 0 before the clamp by more than rounding
+    rs = np.random.RandomState(3)
+    d = -rs.uniform(0, 104, 200000)
+    kf = np.floor(d * INV_LN2)
+    assert np.all(d - kf * LN2 > -1e-12) and np.all(d - kf * LN2 < math.log(2.0) + 1e-12)
 
 
 def test_exp_det_monotone():
-    # dense sweep plus every fp32 input within +-64 ulps of each range-reduction
-    # boundary (k + 1/2) * ln2, where a Cody-Waite evaluation could step backwards
+    # dense sweep plus every fp32 input within +-4096 ulps of each range-reduction
+    # step k * ln2, where the interval index changes
     rs = np.random.RandomState(1)
     d = np.sort(-rs.uniform(0, 104, 400000).astype(np.float32))
-    e = exp_det(d)
-    assert np.all(np.diff(e) >= 0)
+    assert np.all(np.diff(exp_det(d)) >= 0)
     pts = []
     for k in range(-151, 1):
-        c = np.float32((k + 0.5) * math.log(2))
+        c = np.float32(k * math.log(2))
         base = c.view(np.int32)
-        pts.append((base + np.arange(-64, 65, dtype=np.int32)).view(np.float32))
-    d = np.sort(np.concatenate(pts))
+        pts.append((base + np.arange(-4096, 4097, dtype=np.int32)).view(np.float32))
+    d = np.unique(np.concatenate(pts))
     d = d[(d <= 0) & (d >= -104)]
     assert np.all(np.diff(exp_det(d)) >= 0)
-    assert LN2_HI * 151 == float(Fraction(LN2_HI) * 151)   # k * LN2_HI is exact
+
+
+@pytest.mark.skipif(os.environ.get("SDX_EXHAUSTIVE") != "1",
+                    reason="all 1.12e9 fp32 inputs in [-104, 0]: about 5 minutes; SDX_EXHAUSTIVE=1")
+def test_exp_det_monotone_exhaustive():
+    """Every fp32 d in [-104, 0], in value order: exp_det never increases as d
+    decreases (negative floats: a larger bit pattern is a smaller value)."""
+    end = int(np.float32(-104.0).view(np.uint32))
+    b, prev, bad = 0x80000000, None, 0
+    while b <= end:
+        e1 = min(b + (1 << 24), end + 1)
+        v = exp_det(np.arange(b, e1, dtype=np.uint64).astype(np.uint32).view(np.float32))
+        bad += int((np.diff(v) > 0).sum()) + int(prev is not None and v[0] > prev)
+        prev, b = v[-1], e1
+    assert bad == 0
 
 
 def test_fixed62_and_rn32_exact():
