@@ -811,6 +811,7 @@ struct Draw16Args {
   int64_t V;
   int32_t nrec;        // records per job, kRec16 ids each
   int32_t nblk;        // blocks per job
+  int32_t xcd;         // jobs a multiple of 8: a job's blocks on one XCD
   ChunkRec* recs;      // [jobs, nrec]
   uint32_t* counters;  // [jobs], zero on entry
   int64_t* y;
@@ -1154,8 +1155,19 @@ draw16_kernel(Draw16Args<FMT> a) {
   __shared__ uint32_t s32w[SM_NW];
   __shared__ uint64_t s64w[SM_NW];
   const Eval16<FMT>& ev = a.ev;
-  const int64_t j = (int64_t)blockIdx.x / a.nblk;
-  const int bi = (int)((int64_t)blockIdx.x % a.nblk);
+  // The blocks of one job share an XCD (consecutive block indices go to the 8
+  // XCDs in turn, so block % 8 picks the XCD): the completing block then finds
+  // the job's records and rows in its own L2.
+  int64_t j;
+  int bi;
+  if (a.xcd) {
+    const int64_t i = (int64_t)blockIdx.x >> 3;
+    j = (int64_t)(blockIdx.x & 7) + 8 * (i / a.nblk);
+    bi = (int)(i % a.nblk);
+  } else {
+    j = (int64_t)blockIdx.x / a.nblk;
+    bi = (int)((int64_t)blockIdx.x % a.nblk);
+  }
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const int64_t V = a.V;
 
@@ -1594,6 +1606,7 @@ static hipError_t launch_draw16_fmt(const RowSource16& src, const RowStat* stats
   a.V = V;
   a.nrec = (int32_t)((V + kRec16 - 1) / kRec16);
   a.nblk = (a.nrec + SM_NW - 1) / SM_NW;
+  a.xcd = njobs % 8 == 0 ? 1 : 0;
   a.recs = recs;
   a.counters = counters;
   a.y = y;
