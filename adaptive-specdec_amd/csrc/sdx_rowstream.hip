@@ -96,6 +96,13 @@ __device__ __forceinline__ uint32_t max2(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(us2, a),
                                                                 __builtin_bit_cast(us2, b)));
 }
+__device__ __forceinline__ uint32_t min2(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(us2, a),
+                                                                __builtin_bit_cast(us2, b)));
+}
+__device__ __forceinline__ uint32_t add2(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(us2, a) + __builtin_bit_cast(us2, b));
+}
 
 // Bin <-> key maps of the two window kinds. Fixed: as tabled above. Anchored:
 // bin b >= 1 holds key lo + b - 1, bin 0 the keys below lo.
@@ -500,6 +507,11 @@ rowstream_bf16_kernel(RowStatArgs a) {
     // the count is used, so equal bins are equal codes)
     const uint32_t u_tok = g_in_groups ? (uint32_t)((gid_l >> 3) / kUnit) : 0u;
     const uint32_t og = 4u * (uint32_t)bin_g;
+    const uint32_t og2 = og | (og << 16);
+    // per half of the packed bin offsets: words of counted units whose offset
+    // differed from the token's (packed 16-bit counts, at most 4 per group and
+    // row, so no half overflows), and the counted words
+    uint32_t neq2 = 0, ncw = 0;
     auto grab = [&]() -> uint32_t {
       uint32_t u = 0;
       if (lane == 0) u = atomicAdd(&L.unit_ctr, 1u);
@@ -521,8 +533,9 @@ rowstream_bf16_kernel(RowStatArgs a) {
         omx = max2(omx, o);
         atomicAdd(reinterpret_cast<uint32_t*>(hb + (o & 0xFFFFu)), 1u);
         atomicAdd(reinterpret_cast<uint32_t*>(hb + (o >> 16)), 1u);
-        if (cnt) pre += ((o & 0xFFFFu) == og ? 1u : 0u) + ((o >> 16) == og ? 1u : 0u);
+        if (cnt) neq2 = add2(neq2, min2(o ^ og2, 0x00010001u));  // 0 per equal half
       }
+      if (cnt) ncw += 4u;
     };
     auto proc_unit = [&](const uint4 (&d)[U], uint32_t u) {
       const bool full = (u + 1) * kUnit <= n4;  // uniform
@@ -563,6 +576,7 @@ rowstream_bf16_kernel(RowStatArgs a) {
         proc_unit(B, ub);
       }
     }
+    pre += 2u * ncw - (neq2 & 0xFFFFu) - (neq2 >> 16);
     if (g_in_tail) {  // the token among the last V % 8 elements
       __syncthreads();
       snap = hist[bin_g];
