@@ -541,6 +541,131 @@ int sdx_verify_greedy(const void* target_logits, int dtype, int64_t batch, int32
       "greedy_accept");
 }
 
+// ------------------------------------------------------------------ draft step
+// workspace: header, the row statistics / tables (dense probabilities for fp32),
+// the draws' jobs, records and counters, the split parts of bf16 rows
+static size_t draft_ws_bytes(int64_t batch, int64_t vocab, int dtype) {
+  Carve c{nullptr};
+  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jb; sdx::ChunkRec* rc; uint32_t* ct;
+  c.take<uint8_t>(sdx::kWsHeaderBytes);
+  transform_ws(c, batch, vocab, dtype, batch, &st, &tb, &dn, &jb, &rc, &ct);
+  c.take<uint8_t>(dtype == SDX_BF16 ? sdx::rowstream_split_bytes(batch, vocab) : 0);
+  return c.used;
+}
+
+size_t sdx_draft_step_workspace(int64_t batch, int64_t vocab, int dtype) {
+  if (batch < 0 || vocab < 1 || !dtype_ok(dtype)) return 0;
+  return draft_ws_bytes(batch, vocab, dtype);
+}
+
+int sdx_draft_step(const void* logits, int dtype, int64_t batch, int64_t vocab, int64_t ld,
+                   float temperature, float top_p, int32_t top_k, const float* u, int64_t* x,
+                   float* qx, float* conf, float tau, int32_t step, int32_t min_k, int32_t* stop,
+                   void* workspace, size_t workspace_bytes, sdx_stream_t stream) {
+  if (!logits || !x || batch < 0 || ld < vocab || !dtype_ok(dtype))
+    return fail(SDX_EINVAL, "sdx_draft_step: bad arguments");
+  const Switches sw = switches(temperature, top_p, top_k, vocab);
+  if (!sw.greedy) {  // the argmax of T <= 0 takes any vocabulary
+    if (int e = check_vocab(dtype, vocab)) return e;
+    if (!u) return fail(SDX_EINVAL, "sdx_draft_step: uniforms required when T > 0");
+  }
+  if (batch == 0) return SDX_OK;
+  const size_t need = draft_ws_bytes(batch, vocab, dtype);
+  if (!workspace || workspace_bytes < need)
+    return fail(SDX_EWORKSPACE, "sdx_draft_step: workspace %zu < %zu", workspace_bytes, need);
+  hipStream_t s = (hipStream_t)stream;
+  Carve c{(uint8_t*)workspace};
+  uint32_t* header = c.take<uint32_t>(sdx::kWsHeaderBytes / 4);
+  sdx::RowStat* st; float* tb; float* dn; sdx::SampleJob* jobs; sdx::ChunkRec* recs;
+  uint32_t* counters;
+  transform_ws(c, batch, vocab, dtype, batch, &st, &tb, &dn, &jobs, &recs, &counters);
+  const size_t split_bytes = dtype == SDX_BF16 ? sdx::rowstream_split_bytes(batch, vocab) : 0;
+  uint8_t* split_ws = c.take<uint8_t>(split_bytes);
+  sdx::DraftEpiArgs e = {};
+  e.B = batch; e.V = vocab; e.x = x; e.qx = qx; e.conf = conf; e.tau = tau;
+  e.step = step; e.min_k = min_k; e.stop = stop; e.T = temperature;
+  if (sw.greedy) {  // sampling.py:43-48: one-hot at the first maximum
+    const bool vec = aligned16(logits) && (ld % (dtype == SDX_F32 ? 4 : 8)) == 0;
+    if (int r = hip_status(sdx::launch_argmax(dtype, logits, batch, vocab, ld, vec, x, s), "argmax"))
+      return r;
+    e.greedy = true;
+    return hip_status(sdx::launch_draft_epilogue(e, s), "draft_epilogue");
+  }
+  hipLaunchKernelGGL(sdx_jobs_from_u, dim3((unsigned)((batch + 255) / 256)), dim3(256), 0, s, jobs,
+                     u, batch, (int64_t)-1, counters);
+  if (int r = hip_status(hipGetLastError(), "jobs")) return r;
+  if (dtype == SDX_F32) {
+    sdx::F32Args a = {};
+    a.base[0] = (const float*)logits; a.nrows[0] = batch; a.ld[0] = ld;
+    a.base[1] = a.base[0]; a.nrows[1] = 0; a.ld[1] = ld;
+    a.V = vocab; a.ids = nullptr; a.k = 0;
+    a.T = temperature; a.top_p = top_p; a.top_k = top_k;
+    a.use_p = sw.use_p; a.use_k = sw.use_k; a.greedy = 0;
+    a.out = dn; a.ld_out = vocab; a.stats = st;
+    if (int r = hip_status(sdx::launch_to_probs_f32(a, batch, s), "to_probs_f32")) return r;
+    sdx::RowSourceF32 src{dn, vocab, dn, vocab, batch, (vocab % 4) == 0};
+    if (int r = hip_status(sdx::launch_draw_probs(src, nullptr, jobs, batch, vocab, recs, counters,
+                                                  x, s),
+                           "draw_probs"))
+      return r;
+    e.probs = dn;
+    e.ldp = vocab;
+    return hip_status(sdx::launch_draft_epilogue(e, s), "draft_epilogue");
+  }
+  if (!aligned16(logits) || (ld % 8) != 0 || (vocab % 8) != 0)
+    return fail(SDX_EINVAL,
+                "sdx_draft_step: 16-bit rows must start 16-byte aligned, ld %% 8 == 0, vocab %% 8 == 0");
+  sdx::RowStatArgs a = {};
+  a.base[0] = (const uint16_t*)logits; a.nrows[0] = batch; a.ld[0] = ld;
+  a.base[1] = a.base[0]; a.nrows[1] = 0; a.ld[1] = ld;
+  a.V = vocab; a.ids = nullptr; a.k = 0;
+  a.T = temperature; a.top_p = top_p; a.top_k = top_k;
+  a.use_p = sw.use_p; a.use_k = sw.use_k; a.greedy = 0;
+  a.stats = st; a.tables = tb;
+  a.split_ws = split_ws; a.split_bytes = split_bytes; a.ws_header = header;
+  if (int r = row_stats16(dtype, a, batch, s)) return r;
+  sdx::RowSource16 src{(const uint16_t*)logits, ld, (const uint16_t*)logits, ld, batch, true};
+  if (int r = hip_status(sdx::launch_draw_rows16(dtype, src, st, tb, temperature, jobs, batch,
+                                                 vocab, recs, counters, x, s),
+                         "draw_rows16"))
+    return r;
+  e.fmt = dtype;
+  e.codes = (const uint16_t*)logits;
+  e.ld = ld;
+  e.stats = st;
+  e.tables = tb;
+  return hip_status(sdx::launch_draft_epilogue(e, s), "draft_epilogue");
+}
+
+// ------------------------------------------------------------------ round bookkeeping
+int sdx_round_commit(int64_t batch, int32_t k, const int64_t* cu_k, const int64_t* n_acc,
+                     const int64_t* y, const int64_t* draft_ids, uint8_t* done,
+                     int64_t* out_tokens, int64_t* out_len, int64_t max_new,
+                     const int64_t* eos_ids, int32_t n_eos, int64_t* lengths0, int64_t* lengths1,
+                     int64_t* pending, sdx_stream_t stream) {
+  if (batch < 0 || !n_acc || !y || !done || !out_tokens || !out_len || max_new < 1 ||
+      n_eos < 0 || (n_eos > 0 && !eos_ids) || (!cu_k && k < 0) || (k > 0 && !draft_ids && !cu_k))
+    return fail(SDX_EINVAL, "sdx_round_commit: bad arguments");
+  if (batch == 0) return SDX_OK;
+  sdx::RoundCommitArgs a{batch, k,       cu_k,   n_acc, y,        draft_ids, done, out_tokens,
+                         out_len, max_new, eos_ids, n_eos, lengths0, lengths1, pending};
+  return hip_status(sdx::launch_round_commit(a, (hipStream_t)stream), "round_commit");
+}
+
+int sdx_controller_update(sdx_ctrl_state* state, int64_t nstate, const int64_t* n_acc,
+                          int64_t batch, const int64_t* k_used, double beta, int32_t k_max,
+                          int32_t k_init, int32_t warmup, int32_t extra_fwd, const float* c_obs,
+                          int64_t* k_next, int64_t* cu_k, sdx_stream_t stream) {
+  if (!state || !n_acc || !k_used || batch < 1 || k_max < 1 || k_init < 1 ||
+      !(nstate == 1 || nstate == batch) || !(beta > 0.0 && beta <= 1.0))
+    return fail(SDX_EINVAL, "sdx_controller_update: bad arguments");
+  if (cu_k && nstate != batch)
+    return fail(SDX_EINVAL, "sdx_controller_update: cu_k needs one state per row");
+  sdx::CtrlArgs a{reinterpret_cast<sdx::CtrlState*>(state), nstate, n_acc, batch, k_used, beta,
+                  k_max, k_init, warmup, extra_fwd, c_obs, k_next, cu_k};
+  return hip_status(sdx::launch_controller(a, (hipStream_t)stream), "controller");
+}
+
 // ------------------------------------------------------------------ proposer
 int sdx_argmax(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
                int64_t* ids, sdx_stream_t stream) {

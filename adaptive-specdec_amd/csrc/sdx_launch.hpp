@@ -196,6 +196,69 @@ hipError_t launch_greedy_accept(const int64_t* am, int64_t batch, int32_t k, con
                                 const float* u_accept, const uint8_t* active, int64_t* n_acc,
                                 int64_t* y, uint8_t* flags, hipStream_t s,
                                 const int64_t* cu_k = nullptr, const uint8_t* bad = nullptr);
+// draw from 16-bit rows with the draws given in `jobs` (no accept chain); the
+// counters must be zero on entry
+hipError_t launch_draw_rows16(int fmt, const RowSource16& src, const RowStat* stats,
+                              const float* tables, float T, SampleJob* jobs, int64_t njobs,
+                              int64_t V, ChunkRec* recs, uint32_t* counters, int64_t* y,
+                              hipStream_t s);
+// sdx_engine.hip: the device-side bookkeeping of a speculative round
+struct DraftEpiArgs {
+  int fmt;                 // SDX_BF16 / SDX_F16 (16-bit rows)
+  bool greedy;             // temperature <= 0: the drafted token has probability 1
+  const uint16_t* codes;   // 16-bit rows [B, ld]
+  int64_t ld;
+  const float* probs;      // fp32 path: dense probabilities [B, ldp] (else null)
+  int64_t ldp;
+  const RowStat* stats;
+  const float* tables;
+  float T;
+  int64_t B, V;
+  const int64_t* x;        // drafted tokens [B]
+  float* qx;               // [B] or null
+  float* conf;             // [B] running product, or null
+  float tau;
+  int32_t step, min_k;
+  int32_t* stop;           // [1] or null
+};
+hipError_t launch_draft_epilogue(const DraftEpiArgs& a, hipStream_t s);
+struct RoundCommitArgs {
+  int64_t B;
+  int32_t k;               // drafts per row (uniform), or with cu_k the rows' own
+  const int64_t* cu_k;     // [B+1] or null
+  const int64_t* n_acc;
+  const int64_t* y;
+  const int64_t* draft_ids;  // [B, k] (or packed at cu_k)
+  uint8_t* done;
+  int64_t* out;            // [B, max_new]
+  int64_t* out_len;        // [B]
+  int64_t max_new;
+  const int64_t* eos;      // [n_eos]
+  int32_t n_eos;
+  int64_t* len0;           // cache lengths rolled back by k - n_acc (nullable)
+  int64_t* len1;
+  int64_t* pending;        // [B] <- y (nullable)
+};
+hipError_t launch_round_commit(const RoundCommitArgs& a, hipStream_t s);
+struct CtrlState {         // one EWMAAnalytic controller, 32 bytes (sdx_ctrl_state)
+  double acc, reached, c;
+  int32_t rounds, last_k;
+};
+static_assert(sizeof(CtrlState) == 32, "CtrlState layout");
+struct CtrlArgs {
+  CtrlState* state;
+  int64_t nstate;          // 1: one controller for the batch; B: one per row
+  const int64_t* n_acc;    // [B]
+  int64_t B;
+  const int64_t* k_used;   // [nstate]: the k each state's rows drafted this round
+  double beta;
+  int32_t k_max, k_init, warmup, extra_fwd;
+  const float* c_obs;      // [1] observed draft / target forward time, or null
+  int64_t* k_next;         // [nstate] or null
+  int64_t* cu_k;           // per row: [B+1] exclusive prefix of k_next, or null
+};
+hipError_t launch_controller(const CtrlArgs& a, hipStream_t s);
+
 // sdx_attn.hip: multi-query verify attention over paged KV (bf16, head_dim 128)
 struct AttnUnit {   // one key chunk of one row (b < 0: no chunk)
   int32_t b, c, n, qb;  // row, chunk index, tokens in the chunk, query positions of the row

@@ -1625,6 +1625,20 @@ hipError_t launch_draw16(int fmt, const RowSource16& src, const RowStat* stats,
   return launch_draw16_fmt<SDX_F16>(src, stats, tables, T, *acc, njobs, V, recs, counters, y, s);
 }
 
+hipError_t launch_draw_rows16(int fmt, const RowSource16& src, const RowStat* stats,
+                              const float* tables, float T, SampleJob* jobs, int64_t njobs,
+                              int64_t V, ChunkRec* recs, uint32_t* counters, int64_t* y,
+                              hipStream_t s) {
+  if (!src.vec || V % 8 != 0) return hipErrorInvalidValue;
+  if (fmt == SDX_BF16)
+    return launch_draw(Eval16<SDX_BF16>{src.base, src.ld, src.base2, src.ld2, src.split, stats,
+                                         tables, T},
+                       nullptr, jobs, njobs, V, recs, counters, y, s);
+  return launch_draw(Eval16<SDX_F16>{src.base, src.ld, src.base2, src.ld2, src.split, stats,
+                                      tables, T},
+                     nullptr, jobs, njobs, V, recs, counters, y, s);
+}
+
 hipError_t launch_draw_probs(const RowSourceF32& src, const AcceptArgs* acc, SampleJob* jobs,
                              int64_t njobs, int64_t V, ChunkRec* recs, uint32_t* counters,
                              int64_t* y, hipStream_t s) {

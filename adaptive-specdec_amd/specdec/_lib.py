@@ -19,6 +19,7 @@ P = ctypes.c_void_p
 I64 = ctypes.c_int64
 I32 = ctypes.c_int32
 F = ctypes.c_float
+D = ctypes.c_double
 SZ = ctypes.c_size_t
 INT = ctypes.c_int
 
@@ -43,6 +44,11 @@ _SIGS = {
     "sdx_verify_stats": (INT, [P, P, INT, I64, I32, I64, P, F, F, I32, P, SZ, P]),
     "sdx_verify_greedy_workspace": (SZ, [I64, I32]),
     "sdx_verify_greedy": (INT, [P, INT, I64, I32, I64, P, P, P, P, P, P, P, SZ, P]),
+    "sdx_draft_step_workspace": (SZ, [I64, I64, INT]),
+    "sdx_draft_step": (INT, [P, INT, I64, I64, I64, F, F, I32, P, P, P, P, F, I32, I32, P, P, SZ,
+                             P]),
+    "sdx_round_commit": (INT, [I64, I32, P, P, P, P, P, P, P, I64, P, I32, P, P, P, P]),
+    "sdx_controller_update": (INT, [P, I64, P, I64, P, D, I32, I32, I32, I32, P, P, P, P]),
     "sdx_argmax": (INT, [P, INT, I64, I64, I64, P, P]),
     "sdx_slot_mapping": (INT, [P, I64, I64, P, I32, I64, I64, P, P, P]),
     "sdx_kv_advance": (INT, [P, I64, I64, P]),

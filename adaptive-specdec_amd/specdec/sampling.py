@@ -25,7 +25,7 @@ import torch
 from . import _lib
 
 __all__ = ["to_probs", "sample_from_probs", "residual_probs", "gather_prob", "rejection_sample",
-           "rejection_sample_ragged", "Verifier"]
+           "rejection_sample_ragged", "Verifier", "draft_step"]
 
 FLAG_ACCEPT_NEAR_TIE = 1
 FLAG_NONFINITE = 2
@@ -334,3 +334,44 @@ class Verifier:
                                      self.V, ids, self.T, self.tp, self.tk,
                                      _lib.ptr(self.ws), self.ws.numel(), _lib.stream_of(target))
         _lib.check(rc, "Verifier.stats")
+
+
+def draft_step(logits, u, temperature=1.0, top_p=1.0, top_k=0, conf=None, tau=None, step=1,
+               min_k=1, out=None, workspace=None):
+    """One draft step of `engine.py:246-258` in one device call.
+
+    logits [B, V] (the draft's last position), u [B] fp32 uniforms of the draw.
+    q = to_probs(logits) (`sampling.py:34-67`); x = the inverse-CDF draw from q
+    on u (the rule of `sample_from_probs`; T <= 0: the first argmax); qx = q(x).
+    conf [B] fp32 (optional) is multiplied by qx in place (`engine.py:256`); with
+    tau given, stop [1] int32 is set on the device to the early-exit test of
+    `controller.py:184-187`: step >= min_k and mean(conf) < tau. Returns
+    (x [B] int64, qx [B] fp32, stop [1] int32 or None); nothing waits for the host.
+    """
+    T, tp, tk = _switch_args(temperature, top_p, top_k)
+    _lib.require_gpu(logits, None if T == 0.0 else u, conf)
+    L = _lib.lib()
+    B, V = logits.shape
+    x_in, ld = _kernel_rows(logits)
+    dt = _lib.dtype_code(x_in)
+    dev = logits.device
+    if out is None:
+        x = torch.empty(B, dtype=torch.int64, device=dev)
+        qx = torch.empty(B, dtype=torch.float32, device=dev)
+        stop = torch.zeros(1, dtype=torch.int32, device=dev) if tau is not None else None
+    else:
+        x, qx, stop = out
+    if B == 0:
+        return x, qx, stop
+    uu = None if T == 0.0 else u.to(torch.float32).contiguous()
+    if conf is not None and (conf.dtype != torch.float32 or not conf.is_contiguous()):
+        raise ValueError("conf must be a contiguous fp32 tensor (updated in place)")
+    need = L.sdx_draft_step_workspace(B, V, dt)
+    if workspace is None or workspace.numel() < need:
+        workspace = _lib.cached_workspace(need, dev, "draft")
+    rc = L.sdx_draft_step(_lib.ptr(x_in), dt, B, V, ld, T, tp, tk, _lib.ptr(uu), _lib.ptr(x),
+                          _lib.ptr(qx), _lib.ptr(conf), float(tau if tau is not None else 0.0),
+                          int(step), int(min_k), _lib.ptr(stop), _lib.ptr(workspace),
+                          workspace.numel(), _lib.stream_of(x_in))
+    _lib.check(rc, "draft_step")
+    return x, qx, stop

@@ -176,6 +176,56 @@ int sdx_verify_greedy(const void* target_logits, int dtype, int64_t batch, int32
                       const uint8_t* active, int64_t* n_acc, int64_t* y, uint8_t* flags,
                       void* workspace, size_t workspace_bytes, sdx_stream_t stream);
 
+/* ---- one speculative round on the device: specdec/engine.py:228-342 ------- */
+
+/* One draft step (engine.py:246-258 with the early exit of controller.py:184-187):
+ * q = to_probs(logits[b]) (sampling.py:34-67); x[b] = the inverse-CDF draw from q on
+ * u[b] (the rule of sdx_sample_probs; temperature <= 0: the first argmax, u unused);
+ * qx[b] = q(x[b]) (nullable); conf[b] *= qx[b] (nullable, the running product of
+ * engine.py:256); *stop (nullable) = 1 if step >= min_k and mean(conf) < tau, the mean
+ * a sequential fp32 sum in row order over batch (ConfidenceEarlyExit.
+ * should_stop_drafting), else 0. logits [batch, ld] (dtype); workspace from
+ * sdx_draft_step_workspace, prepared once by sdx_workspace_init. Every output stays on
+ * the device: the reference's float(conf.mean()) host sync becomes a device flag. */
+size_t sdx_draft_step_workspace(int64_t batch, int64_t vocab, int dtype);
+int sdx_draft_step(const void* logits, int dtype, int64_t batch, int64_t vocab, int64_t ld,
+                   float temperature, float top_p, int32_t top_k, const float* u, int64_t* x,
+                   float* qx, float* conf, float tau, int32_t step, int32_t min_k, int32_t* stop,
+                   void* workspace, size_t workspace_bytes, sdx_stream_t stream);
+
+/* The end of a round (engine.py:305-340) without its n_acc.tolist() host sync:
+ * row b drafted k (or, with cu_k [batch+1], cu_k[b+1] - cu_k[b]) tokens draft_ids
+ * [batch, k] (or packed at cu_k[b]), accepted n_acc[b] and drew y[b]. lengths0 and
+ * lengths1 (the two caches' device lengths, nullable) drop k_b - n_acc[b] positions.
+ * Unless done[b], the accepted drafts and then y[b] are appended to
+ * out_tokens[b, out_len[b]..] (capacity max_new per row); a token in eos_ids
+ * [n_eos], or the row reaching max_new tokens, sets done[b] and ends the row's
+ * emission. pending[b] (nullable) = y[b], the next round's first input. */
+int sdx_round_commit(int64_t batch, int32_t k, const int64_t* cu_k, const int64_t* n_acc,
+                     const int64_t* y, const int64_t* draft_ids, uint8_t* done,
+                     int64_t* out_tokens, int64_t* out_len, int64_t max_new,
+                     const int64_t* eos_ids, int32_t n_eos, int64_t* lengths0, int64_t* lengths1,
+                     int64_t* pending, sdx_stream_t stream);
+
+/* EWMAAnalytic (controller.py:121-154) on the device. One state per batch
+ * (nstate 1: accepted = sum n_acc, reached = sum min(n_acc + 1, k_used[0]), as
+ * update() computes them) or per row (nstate == batch: row b's n_acc[b] and its
+ * own k_used[b]). Each state: w = beta^reached; acc = w acc + accepted; reached =
+ * w reached + reached; c = 0.9 c + 0.1 c_obs when c_obs (nullable, [1]) is > 0;
+ * rounds += 1; then the next k (propose_k): k_init while rounds < warmup, else
+ * best_k(clamp(acc / reached, 0, 0.999) (0.7 before any token), c, k_max,
+ * extra_fwd) (controller.py:47-67) into k_next [nstate] (nullable) and, per row,
+ * its exclusive prefix into cu_k [batch + 1] (nullable: the offsets of the next
+ * sdx_verify_ragged). All in float64, as the host controller computes it. */
+typedef struct {
+  double acc, reached, c;
+  int32_t rounds, last_k;
+} sdx_ctrl_state;
+int sdx_controller_update(sdx_ctrl_state* state, int64_t nstate, const int64_t* n_acc,
+                          int64_t batch, const int64_t* k_used, double beta, int32_t k_max,
+                          int32_t k_init, int32_t warmup, int32_t extra_fwd, const float* c_obs,
+                          int64_t* k_next, int64_t* cu_k, sdx_stream_t stream);
+
 /* ---- proposer-side calls: vllm_draft_spec/proposer.py -------------------- */
 
 /* Greedy draft token, logits.argmax(dim=-1) (proposer.py:262-263,331-332): first index

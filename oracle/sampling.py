@@ -263,3 +263,37 @@ def greedy_verify(target_logits, draft_ids, u_accept=None, active=None):
         n_acc[b], flags[b] = accept_chain(px, qx, ua[b], bool(act[b]))
     y = am[np.arange(B), n_acc]
     return n_acc, y, flags
+
+
+def draft_step(logits, u, temperature=1.0, top_p=1.0, top_k=0, conf=None, tau=None, step=1,
+               min_k=1):
+    """One draft step, `engine.py:250-258` and `controller.py:184-187`: q =
+    to_probs(logits[b]); x[b] drawn from q by `sample_fixed` on u[b] (the first
+    argmax when T <= 0); qx[b] = q[b, x[b]]; conf[b] *= qx[b] in fp32; stop when
+    step >= min_k and the mean of conf (a sequential fp32 sum in row order over
+    B) is below tau. Returns (x, qx, conf, stop) with stop None when tau is None."""
+    x_in = np.asarray(logits, np.float32)
+    B = x_in.shape[0]
+    greedy = temperature is None or temperature <= 0.0
+    x = np.zeros(B, np.int64)
+    qx = np.zeros(B, np.float32)
+    for b in range(B):
+        if greedy:
+            x[b] = int(np.argmax(x_in[b]))
+            qx[b] = np.float32(1.0)
+            continue
+        q = _transform_row(x_in[b], temperature, top_p, top_k)
+        x[b] = sample_fixed(fixed62(q), np.float32(u[b]))
+        qx[b] = q[x[b]] if x[b] >= 0 else np.float32(0.0)
+    conf_out = None
+    if conf is not None:
+        conf_out = (np.asarray(conf, np.float32) * qx).astype(np.float32)
+    stop = None
+    if tau is not None:
+        stop = 0
+        if conf_out is not None and step >= min_k:
+            s = np.float32(0.0)
+            for v in conf_out:
+                s = np.float32(s + v)
+            stop = int(np.float32(s / np.float32(B)) < np.float32(tau))
+    return x, qx, conf_out, stop
