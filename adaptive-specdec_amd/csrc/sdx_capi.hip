@@ -336,6 +336,7 @@ static size_t verify_ws_bytes(int64_t batch, int64_t ntgt, int64_t ndrf, int64_t
     c.take<int64_t>(ntgt);
     c.take<uint8_t>(batch);
   }
+  if (dtype == SDX_F32) c.take<uint32_t>((size_t)rows * sdx::kF32TieWords);  // tie-group bits
   return c.used;
 }
 
@@ -434,6 +435,8 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
                            "ragged_rows"))
       return e;
   }
+  uint32_t* tie_bits =
+      dtype == SDX_F32 ? c.take<uint32_t>((size_t)rows * sdx::kF32TieWords) : nullptr;
   if (sw.greedy) {
     // one-hot p: only the target argmax matters (see sdx_verify_greedy)
     const bool vec = aligned16(target_logits) && (vocab % (dtype == SDX_F32 ? 4 : 8)) == 0;
@@ -454,6 +457,7 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
     a.use_p = sw.use_p; a.use_k = sw.use_k; a.greedy = 0;
     a.out = dn; a.ld_out = vocab; a.stats = st;
     a.zero = counters; a.nzero = batch;
+    a.tie_bits = tie_bits;
     if (int e = hip_status(sdx::launch_to_probs_f32(a, rows, s), "to_probs_f32")) return e;
   } else {
     if (!aligned16(target_logits) || !aligned16(draft_logits) || (vocab % 8) != 0)
@@ -484,7 +488,7 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
   if (dtype == SDX_F32) {
     sdx::RowSourceF32 src{dn, vocab, dn, vocab, rows, (vocab % 4) == 0};
     return hip_status(sdx::launch_draw_probs(src, &aa, jobs, batch, vocab, recs,
-                                             counters, y, s),
+                                             counters, y, s, tie_bits),
                       "draw_probs");
   }
   sdx::RowSource16 src{(const uint16_t*)target_logits, vocab, (const uint16_t*)draft_logits, vocab,

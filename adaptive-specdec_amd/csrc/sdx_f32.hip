@@ -38,6 +38,7 @@ __global__ void __launch_bounds__(F32_NT) to_probs_f32_kernel(F32Args a) {
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   if (tid == 0 && row < a.nzero) a.zero[row] = 0u;
+  if (tid == 0) s_i[1] = 0;  // set when the gathered token is a tie-group member
   const int g = row < a.nrows[0] ? 0 : 1;
   const int64_t r = g ? row - a.nrows[0] : row;
   const float* x = a.base[g] + r * a.ld[g];
@@ -75,6 +76,8 @@ __global__ void __launch_bounds__(F32_NT) to_probs_f32_kernel(F32Args a) {
     for (int w = 0; w < F32_NT / kWave; ++w) b = red[w] > b ? red[w] : b;
     const int64_t am = (int64_t)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFu));
     for (int i = tid; i < V; i += F32_NT) o[i] = i == am ? 1.0f : 0.0f;
+    if (a.tie_bits)  // no tie groups in a one-hot row
+      for (int i = tid; i < (int)kF32TieWords; i += F32_NT) a.tie_bits[row * kF32TieWords + i] = 0u;
     if (tid == 0 && a.stats) {
       RowStat st = {};
       st.flags = kRowGreedy | kRowProbs;
@@ -130,6 +133,10 @@ __global__ void __launch_bounds__(F32_NT) to_probs_f32_kernel(F32Args a) {
   bool mask[F32_PER];
 #pragma unroll
   for (int t = 0; t < F32_PER; ++t) mask[t] = true;
+  // the partially kept boundary tie group: the tokens of the last kept
+  // probability vb (after top-k zeroing) when the first dropped token has it too
+  bool partial = false;
+  float vb = 0.0f, kth_g = 0.0f;
   if (a.use_k || a.use_p) {
     int n2 = 1;
     while (n2 < V) n2 <<= 1;
@@ -196,11 +203,42 @@ __global__ void __launch_bounds__(F32_NT) to_probs_f32_kernel(F32Args a) {
       }
     }
     __syncthreads();
+    uint64_t nkeep = 0;
 #pragma unroll
     for (int t = 0; t < F32_PER; ++t) {
       const int i = tid + t * F32_NT;
       mask[t] = i < V && keep[i] != 0;
+      nkeep += mask[t] ? 1u : 0u;
     }
+    if (a.use_p) {  // keep is a prefix of the sorted order: its last position is nkeep - 1
+      nkeep = block_sum_u64(nkeep, red);
+      const int js = (int)nkeep - 1;
+      auto masked = [&](int i) {
+        const float pv = __uint_as_float(~(uint32_t)(skey[i] >> 32));
+        return (a.use_k && pv < kth) ? 0.0f : pv;
+      };
+      vb = masked(js);
+      partial = js + 1 < V && vb > 0.0f && masked(js + 1) == vb;
+      kth_g = kth;
+    }
+  }
+  bool gtie = false;
+  if (a.tie_bits || gid >= 0) {
+    const int lane = tid & (kWave - 1), wv = tid / kWave;
+#pragma unroll
+    for (int t = 0; t < F32_PER; ++t) {
+      const int i = tid + t * F32_NT;
+      const float pm = (a.use_k && p[t] < kth_g) ? 0.0f : p[t];
+      const bool mem = partial && i < V && pm == vb;
+      if (mem && i == gid) gtie = true;
+      const uint64_t bm = __ballot(mem);
+      if (a.tie_bits && lane == 0) {  // ids t*F32_NT + 64*wv + [0, 64): two words
+        uint32_t* dst = a.tie_bits + row * kF32TieWords + ((t * F32_NT + wv * kWave) >> 5);
+        dst[0] = (uint32_t)bm;
+        dst[1] = (uint32_t)(bm >> 32);
+      }
+    }
+    if (gtie) s_i[1] = 1;
   }
   // ---- renormalise
   uint64_t tot = 0;
@@ -223,7 +261,7 @@ __global__ void __launch_bounds__(F32_NT) to_probs_f32_kernel(F32Args a) {
   __syncthreads();
   if (tid == 0 && a.stats) {
     RowStat st = {};
-    st.flags = kRowProbs;
+    st.flags = kRowProbs | (s_i[1] ? kRowGatherTie : 0u);
     st.m = m; st.zf = zf; st.totf = totf; st.mass = tot;
     st.glo = 1; st.ghi = 0; st.argmax = -1;
     st.pgather = (gid >= 0 && gid < V) ? s_f[2] : 0.0f;

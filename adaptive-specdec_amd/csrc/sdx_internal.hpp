@@ -22,8 +22,10 @@ enum RowFlag : uint32_t {
   kRowProbs = 1u << 4,       // final probabilities stored densely (fp32 path)
   kRowRank = 1u << 5,        // drafted token inside the partial tie group: pgather is
                              // set by the rank kernel from its member rank
-  kRowBadWs = 1u << 6        // split row whose workspace header was not initialised
+  kRowBadWs = 1u << 6,       // split row whose workspace header was not initialised
                              // (sdx_workspace_init): statistics not computed
+  kRowGatherTie = 1u << 7    // the gathered (drafted) token is a member of the row's
+                             // partially kept boundary tie group
 };
 
 // 64 bytes per row. Keys in [glo, ghi] form the tie group that straddles the

@@ -62,6 +62,8 @@ struct F32Args {
   RowStat* stats;  // may be null
   uint32_t* zero;  // words [0, nzero) cleared (block `row` clears word `row`), or null
   int64_t nzero;
+  uint32_t* tie_bits;  // [rows, kF32TieWords]: members of the row's partially kept
+                       // boundary tie group, one bit per id (null: not written)
 };
 
 // One final draw: weights from row `prow` (and `qrow` for a residual).
@@ -158,6 +160,7 @@ hipError_t launch_workspace_init(void* ws, size_t bytes, hipStream_t s);
 hipError_t launch_rank_bf16(const RowStatArgs& a, int64_t rows, hipStream_t s);
 // sdx_f32.hip
 constexpr int64_t kF32MaxVocab = 8192;
+constexpr int64_t kF32TieWords = kF32MaxVocab / 32;  // tie-group bit words per fp32 row
 hipError_t launch_to_probs_f32(const F32Args& a, int64_t rows, hipStream_t s);
 // sdx_sample.hip
 // Draw: chunk records and the per-job select in one launch (with the accept
@@ -172,7 +175,7 @@ hipError_t launch_draw16(int fmt, const RowSource16& src, const RowStat* stats,
                          hipStream_t s);
 hipError_t launch_draw_probs(const RowSourceF32& src, const AcceptArgs* acc, SampleJob* jobs,
                              int64_t njobs, int64_t V, ChunkRec* recs, uint32_t* counters,
-                             int64_t* y, hipStream_t s);
+                             int64_t* y, hipStream_t s, const uint32_t* tie_bits = nullptr);
 hipError_t launch_chunk_mass_probs(const RowSourceF32& src, SampleJob* jobs, int64_t njobs,
                                    int64_t V, ChunkRec* recs, hipStream_t s);
 // to_probs output of 16-bit rows; `counts` holds rows * nchunk words.

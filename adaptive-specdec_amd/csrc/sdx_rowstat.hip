@@ -379,8 +379,10 @@ __global__ void __launch_bounds__(RS_NT) rowstat16_kernel(RowStatArgs a) {
   bool g_kept = true;
   if (gid >= 0 && gid < V && rstar > 0 && rstar < s_i32[4]) {
     const int32_t kg = (int32_t)key_of_code16(ptr[gid]);
-    if (kg >= glo && kg <= ghi)
+    if (kg >= glo && kg <= ghi) {
       g_kept = block_count_members(ptr, gid, glo, ghi, s_u32) < (uint32_t)rstar;
+      rflags |= kRowGatherTie;
+    }
   }
 
   // ---- 7. table of final probabilities for the top keys, gathered token, record

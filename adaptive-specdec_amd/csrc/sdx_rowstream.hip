@@ -998,6 +998,7 @@ rowstream_bf16_kernel(RowStatArgs a) {
       if (rstar <= 0) {
         kept = false;
       } else if (rstar < gcount) {
+        rflags |= kRowGatherTie;
         // a single-value group whose bin holds that value alone: its member rank
         // is the count of equal codes before the token; otherwise the draw ranks it
         const bool one = glo == ghi && bin_g >= 1 && bin_g <= 2 * SK_WIN + 1 && bin_g != SK_BIN_ZERO;

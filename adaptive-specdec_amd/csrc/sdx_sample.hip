@@ -109,6 +109,12 @@ struct Eval16 {
                : 0.0f;
   }
   __device__ static int32_t rstar(const Row& r) { return r.st.rstar; }
+  // Is id a member of the row's partially kept boundary tie group?
+  __device__ static bool in_tie_group(const Row& r, int64_t id) {
+    if (!(r.st.rstar > 0 && r.st.rstar < r.st.gcount)) return false;
+    const int32_t key = (int32_t)key_of_code16(r.ptr[id]);
+    return key >= r.st.glo && key <= r.st.ghi;
+  }
   __device__ Raw fetch(const Row& r, int64_t idx, int64_t lim) const {
     if (idx + 8 <= lim)  // rows start 16-byte aligned and idx is a multiple of 8
       return *reinterpret_cast<const uint4*>(r.ptr + idx);
@@ -168,16 +174,23 @@ struct EvalProb {
   int64_t ld2;
   int64_t split;
   bool vec;
+  const uint32_t* tie_bits;  // per row kF32TieWords words: members of a partial
+                             // boundary tie group (null: no membership known)
   struct Row {
     const float* ptr;
     float vg;
+    const uint32_t* bits;
   };
   __device__ void stage(int64_t, float*) const {}
   __device__ void bind(Row& r, int64_t row, const float*) const {
     r.ptr = row < split ? base + row * ld : base2 + (row - split) * ld2;
     r.vg = 0.0f;
+    r.bits = tie_bits ? tie_bits + row * kF32TieWords : nullptr;
   }
   __device__ static int32_t rstar(const Row&) { return 0; }
+  __device__ static bool in_tie_group(const Row& r, int64_t id) {
+    return r.bits && ((r.bits[id >> 5] >> (id & 31)) & 1u) != 0;
+  }
   __device__ Raw fetch(const Row& r, int64_t idx, int64_t lim) const {
     Raw x;
     if (vec && idx + 8 <= lim) {
@@ -237,6 +250,15 @@ __device__ inline int64_t accept_chain_wave(const AcceptArgs& a, int64_t b, Samp
     const int first = fm ? __ffsll((unsigned long long)fm) - 1 : kWave;
     if (__ballot(near && lane <= first)) fl |= SDX_FLAG_ACCEPT_NEAR_TIE;
     if (fm) n = i0 + first;
+  }
+  // evaluated tests (positions 0..n, at most k - 1) whose drafted token sits in
+  // a partially kept tie group of its target or draft row
+  const int ne = alive ? (n < k ? n + 1 : k) : 0;
+  for (int i0 = 0; i0 < ne; i0 += kWave) {
+    const int i = i0 + lane;
+    uint32_t rf = 0;
+    if (i < ne) rf = a.stats[trow0 + i].flags | a.stats[drow0 + i].flags;
+    if (__ballot((rf & kRowGatherTie) != 0)) fl |= SDX_FLAG_TIE_ORDER;
   }
   for (int i0 = 0; i0 < 2 * k + 1; i0 += kWave) {
     const int i = i0 + lane;
@@ -392,6 +414,7 @@ __global__ void __launch_bounds__(SM_NT) draw_kernel(Ev ev, DrawArgs a) {
   __shared__ uint64_t s_rm2[SM_NW];
   __shared__ int64_t s_pick[3];
   __shared__ int64_t s_found;
+  __shared__ uint32_t s_fl;
   const int64_t j = (int64_t)blockIdx.x / a.nblk;
   const int bi = (int)((int64_t)blockIdx.x % a.nblk);
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
@@ -406,12 +429,13 @@ __global__ void __launch_bounds__(SM_NT) draw_kernel(Ev ev, DrawArgs a) {
         if (bi == 0) {
           a.jobs[j] = jb;
           if (a.acc.n_acc) a.acc.n_acc[j] = n;
-          if (a.acc.flags) a.acc.flags[j] = (uint8_t)fl;
         }
         s_job = jb;
+        s_fl = fl;  // written with y by the block that draws it
       }
     } else if (lane == 0) {
       s_job = a.jobs[j];
+      s_fl = 0;
     }
   }
   __syncthreads();
@@ -739,8 +763,20 @@ __global__ void __launch_bounds__(SM_NT) draw_kernel(Ev ev, DrawArgs a) {
   }
   const bool use_r = hasq && rn32_u64(tot_r) > 1e-9f;
   const uint64_t tot = use_r ? tot_r : tot_p;
+  // y and the row's flags (the accept chain's, plus SDX_FLAG_TIE_ORDER when y
+  // is a member of a partially kept tie group of a row it was drawn from)
+  auto finish = [&](int64_t yv) {
+    if (threadIdx.x != 0) return;
+    a.y[j] = yv;
+    if (a.acc.stats && a.acc.flags) {
+      uint32_t fl = s_fl;
+      if (yv >= 0 && (Ev::in_tie_group(rp, yv) || (use_r && Ev::in_tie_group(rq, yv))))
+        fl |= SDX_FLAG_TIE_ORDER;
+      a.acc.flags[j] = (uint8_t)fl;
+    }
+  };
   if (tot == 0) {
-    if (threadIdx.x == 0) a.y[j] = -1;
+    finish(-1);
     return;
   }
   const uint64_t t = uniform_threshold(job.u, tot);
@@ -770,7 +806,7 @@ __global__ void __launch_bounds__(SM_NT) draw_kernel(Ev ev, DrawArgs a) {
   __syncthreads();
   const int64_t rec_star = s_pick[0];
   if (rec_star < 0) {  // unreachable: record masses sum to tot > t
-    if (threadIdx.x == 0) a.y[j] = -1;
+    finish(-1);
     return;
   }
   if (w == 0) {
@@ -780,7 +816,7 @@ __global__ void __launch_bounds__(SM_NT) draw_kernel(Ev ev, DrawArgs a) {
               (uint32_t)(packed >> 32), (uint64_t)s_pick[2], true, t, &s_found);
   }
   __syncthreads();
-  if (threadIdx.x == 0) a.y[j] = s_found;
+  finish(s_found);
 }
 
 // ---------------------------------------------------------------- verify draw, 16-bit rows
@@ -879,6 +915,11 @@ __device__ inline int64_t chain16_wave(const AcceptArgs& a, const Eval16<FMT>& e
     if (fm) n = first;
   }
   const uint32_t rf = w3.x;  // RowStat::flags
+  {  // evaluated tests (positions 0..n, at most k - 1): drafted token in a partial tie group
+    const int ne = alive ? (n < k ? n + 1 : k) : 0;
+    const int pos = lane < k ? lane : (lane > k && lane < nr ? lane - k - 1 : kWave);
+    if (__ballot(pos < ne && (rf & kRowGatherTie) != 0)) fl |= SDX_FLAG_TIE_ORDER;
+  }
   if (__ballot(lane < nr && (rf & kRowNonfinite) != 0)) fl |= SDX_FLAG_NONFINITE;
   if (__ballot(lane < nr && (rf & kRowUnsupported) != 0)) fl |= SDX_FLAG_UNSUPPORTED;
   if (__ballot(lane < nr && (rf & kRowBadWs) != 0)) fl |= SDX_FLAG_WORKSPACE;
@@ -1154,6 +1195,7 @@ draw16_kernel(Draw16Args<FMT> a) {
   __shared__ int64_t s_found;
   __shared__ uint32_t s32w[SM_NW];
   __shared__ uint64_t s64w[SM_NW];
+  __shared__ uint32_t s_fl;
   const Eval16<FMT>& ev = a.ev;
   // The blocks of one job share an XCD (consecutive block indices go to the 8
   // XCDs in turn, so block % 8 picks the XCD): the completing block then finds
@@ -1192,9 +1234,9 @@ draw16_kernel(Draw16Args<FMT> a) {
       if (bi == 0) {
         a.acc.jobs[j] = jb;
         if (a.acc.n_acc) a.acc.n_acc[j] = n;
-        if (a.acc.flags) a.acc.flags[j] = (uint8_t)fl;
       }
       s_job = jb;
+      s_fl = fl;  // written with y by the block that draws it
     }
   }
   __syncthreads();
@@ -1395,8 +1437,21 @@ draw16_kernel(Draw16Args<FMT> a) {
   }
   const bool use_r = hasq && rn32_u64(tot_r) > 1e-9f;
   const uint64_t tot = use_r ? tot_r : tot_p;
+  // y and the row's flags (the accept chain's, plus SDX_FLAG_TIE_ORDER when y
+  // is a member of a partially kept tie group of a row it was drawn from)
+  auto finish = [&](int64_t yv) {
+    if (threadIdx.x != 0) return;
+    a.y[j] = yv;
+    if (a.acc.flags) {
+      uint32_t fl = s_fl;
+      if (yv >= 0 && (Eval16<FMT>::in_tie_group(rp, yv) ||
+                      (use_r && Eval16<FMT>::in_tie_group(rq, yv))))
+        fl |= SDX_FLAG_TIE_ORDER;
+      a.acc.flags[j] = (uint8_t)fl;
+    }
+  };
   if (tot == 0) {
-    if (threadIdx.x == 0) a.y[j] = -1;
+    finish(-1);
     return;
   }
   const uint64_t t = uniform_threshold(job.u, tot);
@@ -1426,7 +1481,7 @@ draw16_kernel(Draw16Args<FMT> a) {
   __syncthreads();
   const int64_t rec_star = s_pick[0];
   if (rec_star < 0) {  // unreachable: record masses sum to tot > t
-    if (threadIdx.x == 0) a.y[j] = -1;
+    finish(-1);
     return;
   }
   {
@@ -1437,7 +1492,7 @@ draw16_kernel(Draw16Args<FMT> a) {
     block_walk16<FMT, 1>(ev, rp, rq, use_r, i0, i1, bp1, bq1, mm, (uint64_t)s_pick[2], true, t,
                          &s_found, s32w, s64w);
   }
-  if (threadIdx.x == 0) a.y[j] = s_found;
+  finish(s_found);
 }
 
 // ---------------------------------------------------------------- to_probs output
@@ -1641,14 +1696,14 @@ hipError_t launch_draw_rows16(int fmt, const RowSource16& src, const RowStat* st
 
 hipError_t launch_draw_probs(const RowSourceF32& src, const AcceptArgs* acc, SampleJob* jobs,
                              int64_t njobs, int64_t V, ChunkRec* recs, uint32_t* counters,
-                             int64_t* y, hipStream_t s) {
-  EvalProb ev{src.base, src.ld, src.base2, src.ld2, src.split, src.vec};
+                             int64_t* y, hipStream_t s, const uint32_t* tie_bits) {
+  EvalProb ev{src.base, src.ld, src.base2, src.ld2, src.split, src.vec, tie_bits};
   return launch_draw(ev, acc, jobs, njobs, V, recs, counters, y, s);
 }
 
 hipError_t launch_chunk_mass_probs(const RowSourceF32& src, SampleJob* jobs, int64_t njobs,
                                    int64_t V, ChunkRec* recs, hipStream_t s) {
-  EvalProb ev{src.base, src.ld, src.base2, src.ld2, src.split, src.vec};
+  EvalProb ev{src.base, src.ld, src.base2, src.ld2, src.split, src.vec, nullptr};
   return launch_draw(ev, nullptr, jobs, njobs, V, recs, nullptr, nullptr, s);
 }
 

@@ -27,9 +27,13 @@ from . import _lib
 __all__ = ["to_probs", "sample_from_probs", "residual_probs", "gather_prob", "rejection_sample",
            "rejection_sample_ragged", "Verifier", "draft_step"]
 
-FLAG_ACCEPT_NEAR_TIE = 1
-FLAG_NONFINITE = 2
-FLAG_BAD_ROW = 8
+# per-row flags of the verify calls (the SDX_FLAG_* bits of the C ABI)
+FLAG_ACCEPT_NEAR_TIE = 1   # an evaluated accept test had |u - min(p/q, 1)| < 1e-5
+FLAG_NONFINITE = 2         # a logit row held +inf or NaN
+FLAG_UNSUPPORTED = 4       # a row's mass spans more distinct values than the kernels represent
+FLAG_BAD_ROW = 8           # per-row k: inconsistent offsets
+FLAG_WORKSPACE = 16        # the workspace was not prepared by sdx_workspace_init
+FLAG_TIE_ORDER = 32        # a test or the draw touched a partially kept top-p tie group
 
 
 def _switch_args(temperature, top_p, top_k):

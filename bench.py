@@ -182,6 +182,10 @@ def bench_verify(args, torch):
         "graph_per_step_ms_per_step": round(ms_single, 5),
         "row_stats_only_us": None if stat_ms is None else round(stat_ms * 1e3, 2),
         "mean_accepted": round(sum(tokens) / len(tokens) / B - 1, 4),
+        # rows whose accept tests or final draw touched a partially kept top-p tie
+        # group (SDX_FLAG_TIE_ORDER), over every input set
+        "tie_order_rows": int(sum(int(((f & 32) != 0).sum().item()) for _, _, f in eager)),
+        "rows_checked": B * len(eager),
         "roofline": roof, "cpu_baseline": cpu,
     }
     if cpu:

@@ -52,8 +52,15 @@ enum sdx_flag {
                                    spanning over 36 binades of mass): results unspecified */
   SDX_FLAG_BAD_ROW = 8,         /* per-row k: the row offsets (cu_k) were inconsistent with
                                    k_max or the row counts; n_acc 0, y unspecified */
-  SDX_FLAG_WORKSPACE = 16       /* the verify workspace was not prepared by
+  SDX_FLAG_WORKSPACE = 16,      /* the verify workspace was not prepared by
                                    sdx_workspace_init: results of the row unspecified */
+  SDX_FLAG_TIE_ORDER = 32       /* an evaluated accept test's drafted token, or the final
+                                   draw, is a member of a partially kept top-p boundary tie
+                                   group (tokens of equal probability of which the nucleus
+                                   keeps only some, specdec/sampling.py:57-64): the literal
+                                   reference's unstable sort may keep other members, so the
+                                   row's outcome is fixed here by the lowest-ids-first rule
+                                   and may differ from a run of the reference */
 };
 
 const char* sdx_last_error(void);

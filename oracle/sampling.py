@@ -21,6 +21,7 @@ from .numerics import exp_det, fixed62, fixed62_sum, rn32, rn32_u64, uniform_thr
 
 ACCEPT_TIE_EPS = np.float32(1e-5)
 FLAG_ACCEPT_NEAR_TIE = 1
+FLAG_TIE_ORDER = 32
 
 
 def _enabled(temperature, top_p, top_k, V):
@@ -31,6 +32,15 @@ def _enabled(temperature, top_p, top_k, V):
     return greedy, use_p, use_k
 
 
+def _softmax_row(x, temperature):
+    """`sampling.py:50`: softmax(logits / T) of one fp32 row under the exp rule."""
+    s = x / np.float32(temperature)              # logits / T (fp32)
+    d = s - s.max()
+    e = exp_det(d)
+    zf = rn32(fixed62_sum(e))
+    return (e / zf).astype(np.float32)
+
+
 def _transform_row(x, temperature, top_p, top_k):
     """One row of `to_probs` (`sampling.py:34-67`). x: fp32 [V]."""
     V = x.shape[0]
@@ -39,12 +49,39 @@ def _transform_row(x, temperature, top_p, top_k):
         out = np.zeros(V, np.float32)
         out[int(np.argmax(x))] = 1.0             # first index among maxima
         return out
-    s = x / np.float32(temperature)              # sampling.py:50: logits / T (fp32)
-    d = s - s.max()
-    e = exp_det(d)
-    zf = rn32(fixed62_sum(e))
-    p = (e / zf).astype(np.float32)              # softmax
+    p = _softmax_row(x, temperature)
     return filter_renorm(p, top_p if use_p else None, top_k if use_k else None)
+
+
+def boundary_tie_group(x, temperature, top_p, top_k):
+    """Members of the row's partially kept top-p boundary tie group, or None.
+
+    `sampling.py:57-64` keeps a prefix of the descending sort; when the last
+    kept probability v is shared by a token the nucleus drops, the tokens of
+    probability v (after top-k zeroing) form a group of which only some survive,
+    and torch's unstable sort decides which (here: the lowest ids). A token's
+    kept probability inside such a group depends on that order. Returns a bool
+    mask [V] of the group's members (kept and dropped), None when no group is
+    partially kept (greedy rows, top-p off, or the cut between distinct values).
+    """
+    x = np.asarray(x, np.float32)
+    V = x.shape[0]
+    greedy, use_p, use_k = _enabled(temperature, top_p, top_k, V)
+    if greedy or not use_p:
+        return None
+    p = _softmax_row(x, temperature)
+    if use_k:
+        kth = np.sort(p)[-int(top_k)]
+        p = np.where(p < kth, np.float32(0.0), p)
+    srt = p[np.argsort(-p, kind="stable")]
+    cum = rn32_u64(np.cumsum(fixed62(srt), dtype=np.uint64))
+    keep = (cum - srt) < np.float32(top_p)
+    keep[0] = True
+    j = int(np.count_nonzero(keep)) - 1          # keep is a prefix of the sort
+    vb = srt[j]
+    if j + 1 >= V or srt[j + 1] != vb or vb <= 0:
+        return None
+    return p == vb
 
 
 def filter_renorm(p, top_p=None, top_k=None):
@@ -167,6 +204,14 @@ def rejection_sample(target_logits, draft_logits, draft_ids, u_accept, u_final,
     Returns (n_acc [B] int64, y [B] int64, flags [B] uint8). The tokens emitted
     for row b are draft_ids[b, :n_acc[b]] followed by y[b]; the KV drop is
     k - n_acc[b] (`engine.py:310`).
+
+    flags: FLAG_ACCEPT_NEAR_TIE (see accept_chain); FLAG_TIE_ORDER when an
+    evaluated accept test's drafted token, or y, is a member of a partially
+    kept boundary tie group (`boundary_tie_group`) of a distribution it was
+    tested or drawn from (p_i and q_i for test i; p_k for the bonus draw; p_n,
+    and q_n unless the residual is degenerate, for the residual draw): those
+    rows would read other probabilities under another order of equal values
+    in torch's sort.
     """
     tl = np.asarray(target_logits, np.float32)
     dl = np.asarray(draft_logits, np.float32)
@@ -182,15 +227,28 @@ def rejection_sample(target_logits, draft_logits, draft_ids, u_accept, u_final,
     for b in range(B):
         ps = np.stack([_transform_row(tl[b, i], temperature, top_p, top_k) for i in range(k + 1)])
         qs = np.stack([_transform_row(dl[b, i], temperature, top_p, top_k) for i in range(k)])
+        gp = [boundary_tie_group(tl[b, i], temperature, top_p, top_k) for i in range(k + 1)]
+        gq = [boundary_tie_group(dl[b, i], temperature, top_p, top_k) for i in range(k)]
         px = ps[np.arange(k), ids[b]]
         qx = qs[np.arange(k), ids[b]]
         n, f = accept_chain(px, qx, ua[b], bool(act[b]))
-        n_acc[b], flags[b] = n, f
+        if act[b]:
+            for i in range(min(n + 1, k)):           # the evaluated tests
+                t = ids[b, i]
+                if (gp[i] is not None and gp[i][t]) or (gq[i] is not None and gq[i][t]):
+                    f |= FLAG_TIE_ORDER
         if n == k:                                   # bonus draw from p_{k+1}
             w = fixed62(ps[k])
+            groups = [gp[k]]
         else:                                        # residual at the stop position
             w = _residual_weights(ps[n], qs[n])
+            degenerate = rn32(fixed62_sum(np.maximum(ps[n] - qs[n], np.float32(0.0)))) \
+                <= np.float32(1e-9)
+            groups = [gp[n]] if degenerate else [gp[n], gq[n]]
         y[b] = sample_fixed(w, uf[b])
+        if y[b] >= 0 and any(g is not None and g[y[b]] for g in groups):
+            f |= FLAG_TIE_ORDER
+        n_acc[b], flags[b] = n, f
     return n_acc, y, flags
 
 
@@ -220,6 +278,9 @@ def rejection_sample_ragged(target_logits, draft_logits, draft_ids, u_accept, u_
                 y[b] = argmax_first(t[0])
             else:
                 y[b] = sample_fixed(fixed62(_transform_row(t[0], temperature, top_p, top_k)), uf[b])
+                grp = boundary_tie_group(t[0], temperature, top_p, top_k)
+                if y[b] >= 0 and grp is not None and grp[y[b]]:
+                    flags[b] = FLAG_TIE_ORDER
             continue
         if temperature is None or temperature <= 0:
             n, yy, f = greedy_verify(t[None], ids[c0:c0 + kb][None], ua[c0:c0 + kb][None],

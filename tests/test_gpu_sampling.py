@@ -490,3 +490,81 @@ def test_rejection_sample_ragged_random(seed):
     assert np.array_equal(n.cpu().numpy(), rn)
     assert np.array_equal(y.cpu().numpy(), ry)
     assert np.array_equal(f.cpu().numpy(), rf)
+
+
+def _coarse_logits(shape, g, dtype):
+    """Logits on a grid of 0.5 (12 values): every probability is shared by many
+    tokens, so a top-p cut nearly always falls inside a tie group."""
+    x = torch.randint(0, 12, shape, generator=g, device=DEV).float() * 0.5 - 3.0
+    return x.to(dtype)
+
+
+def _ids_in_groups(drf, T, tp, tk, g):
+    """Draft ids: a member of the draft row's partially kept boundary group with
+    probability 0.7, else any id."""
+    d = _np(drf)
+    sh = d.shape[:-1]
+    V = d.shape[-1]
+    pick = torch.rand(sh, generator=g, device=DEV).cpu().numpy()
+    anyid = torch.randint(0, V, sh, generator=g, device=DEV).cpu().numpy()
+    out = np.zeros(sh, np.int64)
+    for idx in np.ndindex(*sh):
+        grp = O.boundary_tie_group(d[idx], T, tp, tk)
+        if grp is not None and pick[idx] < 0.7:
+            mem = np.flatnonzero(grp)
+            out[idx] = mem[int(anyid[idx]) % mem.size]
+        else:
+            out[idx] = anyid[idx]
+    return torch.from_numpy(out).to(DEV)
+
+
+@pytest.mark.parametrize("dtype,V,k", [(torch.bfloat16, 4096, 4), (torch.float16, 4096, 4),
+                                       (torch.float32, 2048, 3), (torch.bfloat16, 151936, 4),
+                                       (torch.bfloat16, 1024, 40)])
+def test_tie_order_flags(dtype, V, k):
+    """SDX_FLAG_TIE_ORDER (32) on rows whose accept tests or final draw touch a
+    partially kept top-p boundary tie group: flags equal the oracle's, bit for
+    bit, with accept-side and draw-side cases both present."""
+    B, T, tp, tk = 16, 0.9, 0.8, 0
+    g = torch.Generator(device=DEV).manual_seed(V + k)
+    tgt = _coarse_logits((B, k + 1, V), g, dtype)
+    drf = (tgt[:, :k].float() + 0.5 * torch.randint(0, 2, (B, k, V), generator=g,
+                                                     device=DEV).float()).to(dtype)
+    ids = _ids_in_groups(drf, T, tp, tk, g)
+    ua = uniforms((B, k), g, DEV)
+    uf = uniforms((B,), g, DEV)
+    n, y, f = S.rejection_sample(tgt, drf, ids, ua, uf, temperature=T, top_p=tp, top_k=tk)
+    rn, ry, rf = O.rejection_sample(_np(tgt), _np(drf), ids.cpu().numpy(), _np(ua), _np(uf),
+                                    T, tp, tk)
+    assert np.array_equal(n.cpu().numpy(), rn)
+    assert np.array_equal(y.cpu().numpy(), ry)
+    assert np.array_equal(f.cpu().numpy(), rf)
+    tied = (rf & O.FLAG_TIE_ORDER) != 0
+    assert tied.any() and not tied.all()
+    # with top_p off nothing is flagged
+    n, y, f = S.rejection_sample(tgt, drf, ids, ua, uf, temperature=T, top_p=1.0, top_k=tk)
+    assert not (f.cpu().numpy() & O.FLAG_TIE_ORDER).any()
+
+
+def test_tie_order_flags_ragged():
+    """The flag through the per-row-k verify (rows with k_b = 0 included)."""
+    B, V, T, tp = 12, 4096, 0.9, 0.8
+    g = torch.Generator(device=DEV).manual_seed(77)
+    kb = torch.randint(0, 6, (B,), generator=g, device=DEV).cpu().numpy()
+    cu = np.concatenate([[0], np.cumsum(kb)]).astype(np.int64)
+    nt = int(cu[-1]) + B
+    tgt = _coarse_logits((nt, V), g, torch.bfloat16)
+    tidx = np.concatenate([np.arange(cu[b] + b, cu[b] + b + kb[b]) for b in range(B)])
+    drf = (tgt[torch.from_numpy(tidx).to(DEV)].float() + 0.5 * torch.randint(
+        0, 2, (int(cu[-1]), V), generator=g, device=DEV).float()).to(torch.bfloat16)
+    ids = _ids_in_groups(drf, T, tp, 0, g)
+    ua = uniforms((int(cu[-1]),), g, DEV)
+    uf = uniforms((B,), g, DEV)
+    cu_t = torch.from_numpy(cu).to(DEV)
+    n, y, f = S.rejection_sample_ragged(tgt, drf, ids, ua, uf, cu_t, temperature=T, top_p=tp)
+    rn, ry, rf = O.rejection_sample_ragged(_np(tgt), _np(drf), ids.cpu().numpy(), _np(ua),
+                                           _np(uf), cu, T, tp, 0)
+    assert np.array_equal(n.cpu().numpy(), rn)
+    assert np.array_equal(y.cpu().numpy(), ry)
+    assert np.array_equal(f.cpu().numpy(), rf)
+    assert ((rf & O.FLAG_TIE_ORDER) != 0).any()

@@ -295,3 +295,128 @@ def test_ragged_rows_use_their_own_slices():
                                         ids[None, c0:c0 + kb], ua[None, c0:c0 + kb], uf[b:b + 1],
                                         0.9, 0.9, 0)
         assert (n[b], y[b], f[b]) == (rn[0], ry[0], rf[0])
+
+
+# ---------------------------------------------------------------- tie-order flag
+def _kept_under_order(p, top_p, rank):
+    """The nucleus of `sampling.py:57-64` when equal probabilities are sorted by
+    `rank` (any tie order the unstable sort may produce): the kept ids."""
+    order = sorted(range(p.size), key=lambda i: (-float(p[i]), rank[i]))
+    srt = p[order]
+    cum = np.cumsum(fixed62(srt), dtype=np.uint64)
+    kept = set()
+    for j, i in enumerate(order):
+        excl = rn32(int(cum[j])) - srt[j]
+        if j == 0 or excl < np.float32(top_p):
+            kept.add(i)
+    return kept
+
+
+def _softmax_topk(x, T, tk):
+    p = S._softmax_row(np.asarray(x, np.float32), T)
+    if tk:
+        kth = np.sort(p)[-tk]
+        p = np.where(p < kth, np.float32(0.0), p)
+    return p
+
+
+def test_kat_boundary_tie_group():
+    """A planted group of four equal logits with the cut after two of them is
+    the group; a cut after all four (or top_p off, or greedy) gives none."""
+    x = np.array([3.0, 2.0, 1.0, 2.0, 0.5, 2.0, 2.0, -1.0], np.float32)
+    p = S._softmax_row(x, 1.0)
+    m3, p2 = float(p[0]), float(p[1])
+    g = S.boundary_tie_group(x, 1.0, m3 + 1.5 * p2, 0)
+    assert g is not None and g.tolist() == (x == 2.0).tolist()
+    assert S.boundary_tie_group(x, 1.0, m3 + 3.5 * p2, 0) is None
+    assert S.boundary_tie_group(x, 1.0, 1.0, 0) is None
+    assert S.boundary_tie_group(x, 0.0, m3 + 1.5 * p2, 0) is None
+
+
+def test_boundary_tie_group_is_what_the_tie_order_decides():
+    """Brute force on tie-heavy rows: the group is exactly the set of ids whose
+    membership in the nucleus changes with the order of equal probabilities."""
+    rng = np.random.default_rng(12)
+    n_partial = 0
+    for trial in range(150):
+        V = int(rng.integers(4, 24))
+        x = rng.integers(0, 5, V).astype(np.float32) * np.float32(0.75)
+        T = float(rng.choice([0.5, 1.0, 1.7]))
+        tp = float(rng.uniform(0.2, 0.97))
+        tk = int(rng.integers(0, V)) if trial % 3 == 0 else 0
+        p = _softmax_topk(x, T, tk)
+        kept = [_kept_under_order(p, tp, rng.permutation(V)) for _ in range(120)]
+        kept.append(_kept_under_order(p, tp, np.arange(V)))
+        varies = np.array([len({i in k for k in kept}) == 2 for i in range(V)])
+        g = S.boundary_tie_group(x, T, tp, tk)
+        if g is None:
+            assert not varies.any(), trial
+        else:
+            n_partial += 1
+            assert np.array_equal(g, varies), trial
+            # the oracle's own nucleus is the lowest-ids-first order
+            probs = S._transform_row(x, T, tp, tk)
+            assert set(np.nonzero(probs > 0)[0].tolist()) == kept[-1]
+    assert n_partial > 20
+
+
+def _rs_with_order(tl, dl, ids, ua, uf, T, tp, tk, rank_of):
+    """rejection_sample with the nucleus taken under tie orders rank_of(row)."""
+    def probs(x, r):
+        p = _softmax_topk(x, T, tk)
+        keep = _kept_under_order(p, tp, r)
+        q = np.array([p[i] if i in keep else 0.0 for i in range(p.size)], np.float32)
+        tot = max(rn32(sum(int(v) for v in fixed62(q))), np.float32(1e-12))
+        return (q / tot).astype(np.float32)
+    B, k1, V = tl.shape
+    k = k1 - 1
+    n_acc = np.zeros(B, np.int64)
+    for b in range(B):
+        px = [probs(tl[b, i], rank_of(b, i))[ids[b, i]] for i in range(k)]
+        qx = [probs(dl[b, i], rank_of(b, 100 + i))[ids[b, i]] for i in range(k)]
+        n_acc[b], _ = S.accept_chain(np.array(px, np.float32), np.array(qx, np.float32), ua[b], True)
+    return n_acc
+
+
+def test_tie_order_flag_covers_every_order_dependent_accept():
+    """Rows whose accepted count changes under another order of equal values in
+    the sort are flagged; rows without partial groups never are."""
+    rng = np.random.default_rng(5)
+    B, k, V = 24, 3, 16
+    T, tp, tk = 1.0, 0.6, 0
+    tl = (rng.integers(0, 4, (B, k + 1, V)) * 0.5).astype(np.float32)
+    dl = (tl[:, :k] + (rng.integers(0, 2, (B, k, V)) * 0.5)).astype(np.float32)
+    ids = np.zeros((B, k), np.int64)
+    for b in range(B):
+        for i in range(k):
+            g = S.boundary_tie_group(dl[b, i], T, tp, tk)
+            pool = np.nonzero(g)[0] if g is not None and rng.random() < 0.7 else np.arange(V)
+            ids[b, i] = int(rng.choice(pool))
+    ua = rng.random((B, k)).astype(np.float32)
+    uf = rng.random(B).astype(np.float32)
+    n, y, fl = S.rejection_sample(tl, dl, ids, ua, uf, T, tp, tk)
+    tied = (fl & S.FLAG_TIE_ORDER) != 0
+    assert tied.any() and not tied.all()
+    for seed in range(25):
+        r = np.random.default_rng(100 + seed)
+        perms = {}
+
+        def rank_of(b, i):
+            return perms.setdefault((b, i), r.permutation(V))
+        n2 = _rs_with_order(tl, dl, ids, ua, uf, T, tp, tk, rank_of)
+        assert np.all(tied | (n2 == n)), seed
+    _, _, fl1 = S.rejection_sample(tl, dl, ids, ua, uf, T, 1.0, tk)   # top_p off
+    assert not ((fl1 & S.FLAG_TIE_ORDER) != 0).any()
+    # an inactive row evaluates no test: only its final draw can flag it
+    act = np.zeros(B, bool)
+    n3, y3, fl3 = S.rejection_sample(tl, dl, ids, ua, uf, T, tp, tk, active=act)
+    assert not n3.any()
+    for b in range(B):
+        g = S.boundary_tie_group(tl[b, 0], T, tp, tk)
+        gq = S.boundary_tie_group(dl[b, 0], T, tp, tk)
+        p0 = S.to_probs(tl[b, 0], T, tp, tk)
+        q0 = S.to_probs(dl[b, 0], T, tp, tk)
+        r = np.maximum(p0 - q0, np.float32(0.0))
+        degenerate = rn32(sum(int(v) for v in fixed62(r))) <= np.float32(1e-9)
+        in_g = (g is not None and g[y3[b]]) or (not degenerate and gq is not None and gq[y3[b]])
+        assert bool(fl3[b] & S.FLAG_TIE_ORDER) == bool(in_g), b
