@@ -6,6 +6,8 @@
 
 #include <mutex>
 
+#include <cstdlib>
+
 #include "sdx_launch.hpp"
 
 namespace {
@@ -340,6 +342,17 @@ static size_t verify_ws_bytes(int64_t batch, int64_t ntgt, int64_t ndrf, int64_t
   return c.used;
 }
 
+// The fused verify kernel (row statistics and draw in one launch) serves bf16
+// logits at one k per batch row; SDX_VERIFY_FUSED=0 in the environment selects
+// the two-launch path instead.
+static bool fused_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("SDX_VERIFY_FUSED");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
 size_t sdx_verify_workspace(int64_t batch, int32_t k, int64_t vocab, int dtype) {
   return verify_ws_bytes(batch, batch * ((int64_t)k + 1), batch * (int64_t)k, vocab, dtype, false);
 }
@@ -437,6 +450,7 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
   }
   uint32_t* tie_bits =
       dtype == SDX_F32 ? c.take<uint32_t>((size_t)rows * sdx::kF32TieWords) : nullptr;
+
   if (sw.greedy) {
     // one-hot p: only the target argmax matters (see sdx_verify_greedy)
     const bool vec = aligned16(target_logits) && (vocab % (dtype == SDX_F32 ? 4 : 8)) == 0;
@@ -475,6 +489,21 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
     a.split_ws = split_ws;
     a.split_bytes = split_bytes;
     a.ws_header = header;
+    if (dtype == SDX_BF16 && !cu_k && !stats_only && 2 * (int64_t)k + 1 <= 64 &&
+        batch <= sdx::kWsFusedMaxJobs && fused_enabled()) {
+      // one launch: the draw of each batch row starts as soon as its rows are in.
+      // Its counters sit at fixed header offsets (every call leaves them at zero),
+      // so a workspace reused across shapes never hands it stale counts.
+      sdx::AcceptArgs aa{st,    batch, k,         u_accept, u_final, active, jobs,
+                         n_acc, flags, draft_ids, cu_k,     bad,     ntgt};
+      sdx::RowSource16 src{(const uint16_t*)target_logits, vocab, (const uint16_t*)draft_logits,
+                           vocab, ntgt, true};
+      return hip_status(
+          sdx::launch_verify_fused_bf16(a, rows, src, aa, batch, vocab, temperature, recs,
+                                        header + sdx::kWsFusedDrawWord,
+                                        header + sdx::kWsFusedJobWord, y, s),
+          "verify_fused_bf16");
+    }
     if (int e = row_stats16(dtype, a, rows, s)) return e;
     // bf16: drafted tokens the row kernel could not rank (a tie group of several
     // values) are ranked by the draw's accept chain; the statistics-only call

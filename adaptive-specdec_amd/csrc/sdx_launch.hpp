@@ -10,10 +10,14 @@ namespace sdx {
 // word that sdx_workspace_init writes, then the arrival counters of rows split
 // over several blocks. The counters sit at fixed offsets, so a workspace reused
 // for other shapes finds them where the last call left them, at zero.
-constexpr size_t kWsHeaderBytes = 4096;
+constexpr size_t kWsHeaderBytes = 16384;
 constexpr uint32_t kWsMagic = 0x53445857u;
-constexpr int kWsCounterWord = 64;  // first counter word (256-byte aligned)
-constexpr int kWsMaxCounters = (int)(kWsHeaderBytes / 4) - kWsCounterWord;
+constexpr int kWsCounterWord = 64;  // split-row arrival counters (256-byte aligned)
+constexpr int kWsMaxCounters = 1024 - kWsCounterWord;
+constexpr int kWsFusedJobWord = 1024;   // fused verify: row arrivals per batch row
+constexpr int kWsFusedDrawWord = 2048;  // fused verify: the draw's counters per batch row
+constexpr int kWsFusedMaxJobs = 1024;   // batch rows the fused verify serves
+static_assert(kWsFusedDrawWord + kWsFusedMaxJobs <= (int)(kWsHeaderBytes / 4), "header words");
 
 struct RowStatArgs {
   const uint16_t* base[2];  // group 0: target rows, group 1: draft rows
@@ -45,6 +49,7 @@ struct RowStatArgs {
   int32_t xcd_group;  // a row's parts on blocks of one XCD (block index mod 8)
   uint32_t* split_cnt;  // the header's counters (set by launch_rowstream_bf16)
   uint8_t* split_parts;
+  int32_t jm_k;  // fused verify kernel: rows are taken in batch-row order at this k
 };
 
 struct F32Args {
@@ -151,6 +156,16 @@ int rowstat16_nslot(int64_t V);
 hipError_t launch_rowstat16(int fmt, const RowStatArgs& a, int64_t rows, hipStream_t s);
 // sdx_rowstream.hip
 hipError_t launch_rowstream_bf16(const RowStatArgs& a, int64_t rows, hipStream_t s);
+// The verify at one k per batch row over bf16 logits (2k + 1 <= 64) in one launch:
+// row statistics and the draw (see sdx_rowstream.hip). `job_cnt` ([njobs] words)
+// and `counters` must be zero on entry; the launch leaves them at zero.
+struct AcceptArgs;
+struct RowSource16;
+struct ChunkRec;
+hipError_t launch_verify_fused_bf16(const RowStatArgs& rs, int64_t rows, const RowSource16& src,
+                                    const AcceptArgs& acc, int64_t njobs, int64_t V, float T,
+                                    ChunkRec* recs, uint32_t* counters, uint32_t* job_cnt,
+                                    int64_t* y, hipStream_t s);
 // bytes of RowStatArgs::split_ws that let launch_rowstream_bf16 split rows over
 // several blocks on the current device (0: it would not split)
 size_t rowstream_split_bytes(int64_t rows, int64_t V);

@@ -42,7 +42,7 @@
 // values of different probability) are re-streamed into a histogram anchored
 // at the row maximum (keys [kmax - 10242, kmax]). A decision that needs the
 // order of elements below either window marks the row unsupported.
-#include "sdx_launch.hpp"
+#include "sdx_draw16.hpp"
 
 namespace sdx {
 
@@ -416,15 +416,45 @@ struct SkLds {
   uint32_t unit_ctr;  // next 4 KB unit of the row to stream
 };
 
-__global__ void __launch_bounds__(SK_NT) __attribute__((amdgpu_waves_per_eu(6)))
-rowstream_bf16_kernel(RowStatArgs a) {
-  __shared__ SkLds L;
+// Outputs of a row: plain stores, or device-coherent ones (agent-scope atomic
+// stores, which no XCD's L2 keeps back) when the draw that reads them runs in
+// the same launch.
+__device__ __forceinline__ void st_rowstat(RowStat* dst, const RowStat& st, bool coh) {
+  if (coh) {
+    const uint64_t* s = reinterpret_cast<const uint64_t*>(&st);
+    uint64_t* d = reinterpret_cast<uint64_t*>(dst);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) __hip_atomic_store(d + i, s[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    *dst = st;
+  }
+}
+__device__ __forceinline__ void st_f32(float* dst, float v, bool coh) {
+  if (coh)
+    __hip_atomic_store(reinterpret_cast<uint32_t*>(dst), __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *dst = v;
+}
+
+// Rows in batch-row order (jm_k = k > 0): the q-th row taken is position
+// q % (2k + 1) of batch row q / (2k + 1), target positions first, so the rows of
+// one batch row finish close together.
+__device__ __forceinline__ int64_t jm_row(int64_t q, int32_t k, int64_t ntgt) {
+  const int64_t b = q / (2 * k + 1), i = q % (2 * k + 1);
+  return i <= k ? b * (k + 1) + i : ntgt + b * k + (i - k - 1);
+}
+
+// One block's share of the row statistics (block blk of the launch). Returns
+// the row whose statistics this block completed (written), or -1 (a split
+// row's part that did not merge).
+template <bool FUSED>
+__device__ __forceinline__ int64_t rowstream_body(const RowStatArgs& a, SkLds& L, int64_t blk) {
   uint32_t* const hist = L.hist;
   int rs = 0;
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   // the row, and the part of it when rows after nwhole are split over nparts blocks
-  const int64_t blk = blockIdx.x;
   const int P = a.nparts;
   int64_t row = blk, sidx = -1;
   int part = -1;
@@ -440,6 +470,7 @@ rowstream_bf16_kernel(RowStatArgs a) {
     }
     row = a.nwhole + sidx;
   }
+  if (FUSED) row = jm_row(row, a.jm_k, a.nrows[0]);
   const int g = row < a.nrows[0] ? 0 : 1;
   const int64_t r = g ? row - a.nrows[0] : row;
   const uint16_t* __restrict__ ptr = a.base[g] + r * a.ld[g];
@@ -604,9 +635,9 @@ rowstream_bf16_kernel(RowStatArgs a) {
       RowStat st = {};
       st.flags = kRowBadWs | kRowUnsupported;
       st.zf = 1.0f; st.totf = 1.0f; st.klo = 0x7FFFFFFF; st.glo = 1; st.ghi = 0; st.argmax = -1;
-      *st_out = st;
+      st_rowstat(st_out, st, FUSED);
     }
-    if (mg != 1) return;
+    if (mg != 1) return mg == 2 && part == 0 ? row : -1;
     snap = cp;  // every part's count, this one's included
     pre = 0;
   }
@@ -624,9 +655,9 @@ rowstream_bf16_kernel(RowStatArgs a) {
       RowStat st = {};
       st.flags = kRowNonfinite;
       st.zf = 1.0f; st.totf = 1.0f; st.klo = 0x7FFFFFFF; st.glo = 1; st.ghi = 0; st.argmax = -1;
-      *st_out = st;
+      st_rowstat(st_out, st, FUSED);
     }
-    return;
+    return row;
   }
   const float T = a.T;
   const double invT = 1.0 / (double)T;
@@ -806,35 +837,72 @@ rowstream_bf16_kernel(RowStatArgs a) {
     float pb = 0.0f;
     int gtop0 = 0, gbot0 = 0;
     uint32_t above0 = 0, gcnt0 = 0;
-    // Wave 0 walks the top SK_PW bins first, 64 at a time (one wave scan each,
-    // no barrier): a nucleus of a few hundred values ends there, and the other
-    // blocks on the CU keep their issue slots. Past them the block takes over in
-    // rounds of SK_NT bins.
+    // Wave 0 walks the top SK_PW bins first, in chunks of 256: lane l holds bins
+    // top - 4l - j (j = 0..3) of a chunk, sums them in order, one wave scan gives
+    // every lane the mass above its bins, and every bin's keep test follows with
+    // no further dependence. A nucleus of a few hundred values ends here in one
+    // or two scans, and the other blocks on the CU keep their issue slots. Past
+    // them the block takes over in rounds of SK_NT bins.
+    constexpr int PJ = 4;  // bins per lane and chunk (more spills at this register budget)
+    static_assert(SK_PW % (PJ * kWave) == 0, "whole chunks");
     if (tid < kWave) {
       uint64_t Sw = 0;
       int fb = -1;
       uint64_t sb0 = 0;
       int g0 = 0, g1 = 0;
       uint32_t ab = 0, gc = 0;
-      for (int top = bmax; top >= klo_bin && top > bmax - SK_PW; top -= kWave) {
-        const int b = top - lane;
-        const uint32_t c = b >= klo_bin ? hist[b] : 0u;
-        const float p = c ? p_of_bin(b) : 0.0f;
-        const uint64_t mi = (uint64_t)c * fixed62(p);
-        const uint64_t incl = wave_incl_scan_u64(mi, lane);
-        const bool fail = c != 0 && !((rn32_u64(Sw + incl) - p) < tp);
-        const uint64_t fm = __ballot(fail);
+      for (int top = bmax; top >= klo_bin && top > bmax - SK_PW; top -= PJ * kWave) {
+        uint32_t c[PJ];
+        float p[PJ];
+        uint64_t f[PJ];
+        uint64_t run = 0;
+#pragma unroll
+        for (int j = 0; j < PJ; ++j) {
+          const int b = top - PJ * lane - j;
+          c[j] = b >= klo_bin ? hist[b] : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < PJ; ++j) {
+          const int b = top - PJ * lane - j;
+          p[j] = c[j] ? p_of_bin(b) : 0.0f;
+          f[j] = (uint64_t)c[j] * fixed62(p[j]);
+          run += f[j];
+        }
+        const uint64_t incl = wave_incl_scan_u64(run, lane);
+        uint32_t fmask = 0;
+        {
+          uint64_t acc = Sw + incl - run;  // mass above this lane's bins
+#pragma unroll
+          for (int j = 0; j < PJ; ++j) {
+            acc += f[j];
+            const bool fail = c[j] != 0 && !((rn32_u64(acc) - p[j]) < tp);
+            fmask |= (fail ? 1u : 0u) << j;
+          }
+        }
+        const uint64_t fm = __ballot(fmask != 0);
         if (fm) {  // the boundary bin is in this chunk (uniform)
           const int tf = __ffsll((unsigned long long)fm) - 1;
-          fb = top - tf;
+          const int jf = __ffs((int)rdlane(fmask, tf)) - 1;
+          fb = top - PJ * tf - jf;
           const float pbw = p_of_bin(fb);
-          const uint64_t ex = incl - mi;
-          sb0 = Sw + (((uint64_t)rdlane((uint32_t)(ex >> 32), tf) << 32) | rdlane((uint32_t)ex, tf));
-          const bool in_g = c != 0 && p == pbw;
-          g0 = (int)wave_max_u32(in_g ? (uint32_t)b : 0u);
-          g1 = (int)~wave_max_u32(~(in_g ? (uint32_t)b : 0xFFFFFFFFu));
-          ab = wave_sum_u32(in_g && b > fb ? c : 0u);
-          gc = wave_sum_u32(in_g ? c : 0u);
+          uint64_t acc = Sw + incl - run, exf = 0;
+          uint32_t gmax = 0, gmin = 0xFFFFFFFFu, a1 = 0, a2 = 0;
+#pragma unroll
+          for (int j = 0; j < PJ; ++j) {
+            const int b = top - PJ * lane - j;
+            if (j == jf) exf = acc;  // mass before the boundary bin (on lane tf)
+            acc += f[j];
+            const bool in_g = c[j] != 0 && p[j] == pbw;
+            gmax = in_g ? max(gmax, (uint32_t)b) : gmax;
+            gmin = in_g ? min(gmin, (uint32_t)b) : gmin;
+            a1 += in_g && b > fb ? c[j] : 0u;
+            a2 += in_g ? c[j] : 0u;
+          }
+          sb0 = ((uint64_t)rdlane((uint32_t)(exf >> 32), tf) << 32) | rdlane((uint32_t)exf, tf);
+          g0 = (int)wave_max_u32(gmax);
+          g1 = (int)~wave_max_u32(~gmin);
+          ab = wave_sum_u32(a1);
+          gc = wave_sum_u32(a2);
           break;
         }
         Sw += ((uint64_t)rdlane((uint32_t)(incl >> 32), kWave - 1) << 32) |
@@ -984,7 +1052,7 @@ rowstream_bf16_kernel(RowStatArgs a) {
     } else {  // below the window: exact per key (zero in the fixed window)
       v = exp_det(sk_d(kk, invT, m)) / zf / totf;
     }
-    tbl_out[t] = v;
+    st_f32(tbl_out + t, v, FUSED);
   }
 
   // ---- 7. probability of the drafted token. Inside a partial tie group it
@@ -1024,8 +1092,15 @@ rowstream_bf16_kernel(RowStatArgs a) {
     st.flags = rflags;
     st.ntbl = ntbl;
     st.argmax = -1;
-    *st_out = st;
+    st_rowstat(st_out, st, FUSED);
   }
+  return row;
+}
+
+__global__ void __launch_bounds__(SK_NT) __attribute__((amdgpu_waves_per_eu(6)))
+rowstream_bf16_kernel(RowStatArgs a) {
+  __shared__ SkLds L;
+  rowstream_body<false>(a, L, blockIdx.x);
 }
 
 // Compute units of the current device (cached per device; 0 if unknown).
@@ -1072,8 +1147,9 @@ size_t rowstream_split_bytes(int64_t rows, int64_t V) {
   return split_need(rows, nwhole, p);
 }
 
-hipError_t launch_rowstream_bf16(const RowStatArgs& args, int64_t rows, hipStream_t s) {
-  RowStatArgs a = args;
+// The launch shape of the row statistics: sets late_block and the split layout
+// of `a` and returns the number of blocks.
+static int64_t rowstream_setup(RowStatArgs& a, int64_t rows) {
   const int cus = device_cus();
   a.late_block = cus > 0 ? 2 * (int64_t)cus : INT64_MAX;
   int64_t nwhole;
@@ -1096,7 +1172,133 @@ hipError_t launch_rowstream_bf16(const RowStatArgs& args, int64_t rows, hipStrea
     a.split_cnt = nullptr;
     a.split_parts = nullptr;
   }
+  return grid;
+}
+
+hipError_t launch_rowstream_bf16(const RowStatArgs& args, int64_t rows, hipStream_t s) {
+  RowStatArgs a = args;
+  const int64_t grid = rowstream_setup(a, rows);
   hipLaunchKernelGGL(rowstream_bf16_kernel, dim3((unsigned)grid), dim3(SK_NT), 0, s, a);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- fused verify
+// Row statistics and the draw in one launch, for bf16 logits at one k per batch
+// row (2k + 1 <= 64 rows). Blocks [0, nrow) are row blocks, taking rows in
+// batch-row order; each publishes its row's statistics and table with
+// device-coherent stores, waits for them, and counts the row in on its batch
+// row (job_cnt). Blocks from nrow_pad on are draw blocks (draw16_body on
+// SM_NT threads; the block's other waves retire at once, and a barrier waits
+// only for the waves that have not): each waits until its batch row's 2k + 1
+// rows are in, then draws. So the draw of the batch rows whose rows finish
+// first overlaps the row statistics of the others.
+//
+// The wait ends: row blocks never wait, and on every XCD all row blocks are
+// dispatched before any draw block (workgroups are dispatched in index order),
+// so a draw block never holds a slot a row block still needs. It is bounded all
+// the same: after kFusedWaitTicks of the 100 MHz real-time counter (20 ms, some
+// 400 times the whole launch) the block gives up and flags its batch row
+// (SDX_FLAG_WORKSPACE), with n_acc 0 and y -1.
+constexpr uint64_t kFusedWaitTicks = 2000000;
+
+struct FusedArgs {
+  RowStatArgs rs;
+  int64_t nrow;      // row blocks
+  int64_t nrow_pad;  // the first draw block (a multiple of 8: block % 8 keeps the XCD)
+  Draw16Args<SDX_BF16> d;
+  uint32_t need;     // rows per batch row
+};
+
+__global__ void __launch_bounds__(SK_NT) __attribute__((amdgpu_waves_per_eu(6)))
+verify_fused_bf16_kernel(FusedArgs a) {
+  __shared__ union FusedLds {
+    SkLds row;
+    Draw16Lds draw;
+  } U;
+  const int64_t blk = blockIdx.x;
+  if (blk < a.nrow_pad) {
+    if (blk >= a.nrow) return;
+    const int64_t row = rowstream_body<true>(a.rs, U.row, blk);
+    if (row < 0) return;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // gfx9 encoding: vmcnt(0) (the row's stores done)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int64_t nt = a.rs.nrows[0];
+      const int64_t b = row < nt ? row / (a.rs.k + 1) : (row - nt) / a.rs.k;
+      __hip_atomic_fetch_add(&a.d.job_cnt[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
+  if (threadIdx.x >= SM_NT) return;
+  const int64_t t = blk - a.nrow_pad;
+  int64_t j;
+  int bi;
+  if (a.d.xcd) {  // a job's blocks on one XCD, as in draw16_kernel
+    const int64_t i = t >> 3;
+    j = (t & 7) + 8 * (i / a.d.nblk);
+    bi = (int)(i % a.d.nblk);
+  } else {
+    j = t / a.d.nblk;
+    bi = (int)(t % a.d.nblk);
+  }
+  if (threadIdx.x == 0) {
+    int ok = 0;
+    if (__hip_atomic_load(a.rs.ws_header, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == kWsMagic) {
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      for (;;) {
+        if (__hip_atomic_load(&a.d.job_cnt[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= a.need) {
+          ok = 1;
+          break;
+        }
+        if (__builtin_amdgcn_s_memrealtime() - t0 > kFusedWaitTicks) break;
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    U.draw.last = ok;
+  }
+  __syncthreads();
+  if (!U.draw.last) {
+    if (threadIdx.x == 0 && bi == 0) {
+      if (a.d.acc.n_acc) a.d.acc.n_acc[j] = 0;
+      if (a.d.acc.flags) a.d.acc.flags[j] = (uint8_t)SDX_FLAG_WORKSPACE;
+      a.d.y[j] = -1;
+    }
+    return;
+  }
+  draw16_body<SDX_BF16, true>(a.d, U.draw, j, bi);
+}
+
+hipError_t launch_verify_fused_bf16(const RowStatArgs& rs, int64_t rows, const RowSource16& src,
+                                    const AcceptArgs& acc, int64_t njobs, int64_t V, float T,
+                                    ChunkRec* recs, uint32_t* counters, uint32_t* job_cnt,
+                                    int64_t* y, hipStream_t s) {
+  if (!src.vec || !y || !job_cnt || !rs.ws_header || V % 8 != 0 || rs.k < 1 ||
+      2 * rs.k + 1 > kWave || rows != njobs * (2 * (int64_t)rs.k + 1))
+    return hipErrorInvalidValue;
+  FusedArgs a = {};
+  a.rs = rs;
+  a.rs.jm_k = rs.k;
+  a.rs.zero = nullptr;  // the draw counters reset themselves (a row block could clear one late)
+  a.rs.nzero = 0;
+  a.nrow = rowstream_setup(a.rs, rows);
+  a.nrow_pad = (a.nrow + 7) / 8 * 8;
+  Draw16Args<SDX_BF16>& d = a.d;
+  d.acc = acc;
+  d.ev = Eval16<SDX_BF16>{src.base, src.ld, src.base2, src.ld2, src.split, rs.stats, rs.tables, T};
+  d.V = V;
+  d.nrec = (int32_t)((V + kRec16 - 1) / kRec16);
+  if (d.nrec > kMaxRec16) return hipErrorInvalidValue;
+  d.nblk = (d.nrec + SM_NW - 1) / SM_NW;
+  d.xcd = njobs % 8 == 0 ? 1 : 0;
+  d.recs = recs;
+  d.counters = counters;
+  d.job_cnt = job_cnt;
+  d.y = y;
+  a.need = (uint32_t)(2 * rs.k + 1);
+  const int64_t grid = a.nrow_pad + njobs * d.nblk;
+  hipLaunchKernelGGL(verify_fused_bf16_kernel, dim3((unsigned)grid), dim3(SK_NT), 0, s, a);
   return hipGetLastError();
 }
 

@@ -242,9 +242,11 @@ def test_split_rows_graph_replays():
 
 
 def test_unprepared_workspace_flags_split_rows():
-    """A zero-filled workspace that sdx_workspace_init never prepared: the rows
-    split over blocks do not trust its counters and their batch rows come back
-    with FLAG_WORKSPACE; every other batch row equals the oracle."""
+    """A zero-filled workspace that sdx_workspace_init never prepared: no batch
+    row whose result depends on the workspace's counters comes back silently
+    wrong. The rows split over blocks do not trust them, so their batch rows
+    carry FLAG_WORKSPACE; the one-launch verify (whose draws wait on counters)
+    flags every batch row; every batch row not flagged equals the oracle."""
     cus = _cus()
     B, k, T, tp = 64, 4, 0.8, 0.95
     inp = verify_inputs(B, k, V, seed=1000, device=DEV, temperature=T, top_p=tp)
@@ -262,14 +264,16 @@ def test_unprepared_workspace_flags_split_rows():
     cu = np.arange(B + 1, dtype=np.int64) * k
     split, _ = _split_batch_rows(cu, cus)
     fl = f.cpu().numpy()
-    flagged = np.flatnonzero(fl & 16)
-    assert set(flagged.tolist()) == set(split)
+    flagged = set(np.flatnonzero(fl & 16).tolist())
+    assert set(split) <= flagged
     if cus == 256:
         assert len(split) > 0
-    ok = [b for b in range(B) if b not in set(split)][:6]
-    rn, ry, rf = O.rejection_sample(_np(inp["target"][ok]), _np(inp["draft"][ok]),
-                                    inp["draft_ids"][ok].cpu().numpy(), _np(inp["u_accept"][ok]),
-                                    _np(inp["u_final"][ok]), T, tp, 0)
-    assert np.array_equal(n.cpu().numpy()[ok], rn)
-    assert np.array_equal(y.cpu().numpy()[ok], ry)
-    assert np.array_equal(fl[ok], rf)
+    ok = [b for b in range(B) if b not in flagged][:6]
+    if ok:
+        rn, ry, rf = O.rejection_sample(_np(inp["target"][ok]), _np(inp["draft"][ok]),
+                                        inp["draft_ids"][ok].cpu().numpy(),
+                                        _np(inp["u_accept"][ok]), _np(inp["u_final"][ok]), T, tp,
+                                        0)
+        assert np.array_equal(n.cpu().numpy()[ok], rn)
+        assert np.array_equal(y.cpu().numpy()[ok], ry)
+        assert np.array_equal(fl[ok], rf)
