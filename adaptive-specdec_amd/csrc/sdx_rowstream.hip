@@ -1197,7 +1197,7 @@ hipError_t launch_rowstream_bf16(const RowStatArgs& args, int64_t rows, hipStrea
 // dispatched before any draw block (workgroups are dispatched in index order),
 // so a draw block never holds a slot a row block still needs. It is bounded all
 // the same: after kFusedWaitTicks of the 100 MHz real-time counter (20 ms, some
-// 400 times the whole launch) the block gives up and flags its batch row
+// 250 times the whole launch) the block gives up and flags its batch row
 // (SDX_FLAG_WORKSPACE), with n_acc 0 and y -1.
 constexpr uint64_t kFusedWaitTicks = 2000000;
 

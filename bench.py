@@ -158,13 +158,18 @@ def bench_verify(args, torch):
     rows = B * (2 * k + 1)
     alg_bytes = rows * V * 2                     # every bf16 logit read once
     out_bytes = B * (8 + 8 + 1)
-    # the roofline is the whole fused verify step (one C-ABI call: the row
-    # statistics kernel and the accept/draw kernel), timed over the timed region
+    # the roofline is the whole verify step (one C-ABI call: one fused launch of
+    # row statistics and draw, or the two kernels when SDX_VERIFY_FUSED=0),
+    # timed over the timed region
     achieved = alg_bytes / (ms / 1e3) / 1e9
+    fused = os.environ.get("SDX_VERIFY_FUSED", "1") != "0"
     roof = {"bound": "hbm",
-            "kernel": "fused verify step (rowstream_bf16_kernel + draw16_kernel, one call)",
+            "kernel": ("verify_fused_bf16_kernel (row statistics + accept/draw, one launch)"
+                       if fused else
+                       "verify step: rowstream_bf16_kernel + draw16_kernel (two launches)"),
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_per_launch(),
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic_per_launch() if fused else None,
             "algorithmic_bytes": alg_bytes, "avg_launch_us": round(ms * 1e3, 2)}
     cpu = None if args.skip_cpu else cpu_baseline(sets[0], eager[0], args, T, tp, np, torch)
     result = {

@@ -69,7 +69,7 @@ int sdx_version(void);
 /* Prepare a workspace for the entry points below: zero-fill `bytes` and write the
  * header word the verify kernels check. Required once for a workspace of
  * sdx_verify / sdx_verify_ragged / sdx_verify_stats (which keep arrival counters
- * at fixed offsets of its first 4 KB and leave them at zero after every call);
+ * at fixed offsets of its first 16 KB and leave them at zero after every call);
  * harmless for the others. Asynchronous on `stream`; no memset, so it may be
  * captured in a graph. A verify call on a workspace that was never prepared does
  * not trust its counters: the rows that would use them get SDX_FLAG_WORKSPACE.
