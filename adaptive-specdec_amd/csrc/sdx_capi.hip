@@ -60,13 +60,8 @@ Switches switches(float T, float top_p, int32_t top_k, int64_t V) {
 // multiple of 8 ids, at most 2048 ids (one block round) where the chunk count
 // allows, at most 128 per row.
 void chunking(int64_t V, int64_t* chunk, int* nchunk) {
-  int64_t n = (V + 2047) / 2048;
-  if (n > 128) n = 128;
-  if (n < 1) n = 1;
-  int64_t c = (V + n - 1) / n;
-  c = (c + 7) / 8 * 8;
-  *chunk = c;
-  *nchunk = (int)((V + c - 1) / c);
+  *chunk = sdx::kMatChunk;
+  *nchunk = (int)((V + sdx::kMatChunk - 1) / sdx::kMatChunk);
 }
 
 constexpr int64_t kMaxVocab16 = 16 * 20 * 512;  // register capacity of the row kernel
@@ -189,13 +184,8 @@ int sdx_to_probs(const void* logits, int dtype, int64_t rows, int64_t vocab, int
 
 // ------------------------------------------------------------------ sample_from_probs
 size_t sdx_sample_probs_workspace(int64_t rows, int64_t vocab) {
-  int64_t rec_ids;
-  int nrec;
-  sdx::draw_layout(vocab, &rec_ids, &nrec);
   Carve c{nullptr};
-  c.take<sdx::SampleJob>(rows);
-  c.take<sdx::ChunkRec>((size_t)rows * nrec);
-  c.take<uint32_t>((size_t)rows);  // draw counters
+  c.take<uint64_t>((size_t)rows * sdx::dense_nrec(vocab));  // record masses
   return c.used;
 }
 
@@ -220,27 +210,29 @@ int sdx_sample_probs(const float* probs, int64_t rows, int64_t vocab, int64_t ld
   const size_t need = sdx_sample_probs_workspace(rows, vocab);
   if (!workspace || workspace_bytes < need)
     return fail(SDX_EWORKSPACE, "sdx_sample_probs: workspace %zu < %zu", workspace_bytes, need);
-  hipStream_t s = (hipStream_t)stream;
-  int64_t rec_ids;
-  int nrec;
-  sdx::draw_layout(vocab, &rec_ids, &nrec);
   Carve c{(uint8_t*)workspace};
-  sdx::SampleJob* jobs = c.take<sdx::SampleJob>(rows);
-  sdx::ChunkRec* recs = c.take<sdx::ChunkRec>((size_t)rows * nrec);
-  uint32_t* counters = c.take<uint32_t>((size_t)rows);
-  hipLaunchKernelGGL(sdx_jobs_from_u, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, jobs,
-                     u, rows, (int64_t)-1, counters);
-  if (int e = hip_status(hipGetLastError(), "jobs")) return e;
-  const bool vec = aligned16(probs) && (ld % 4) == 0;
-  sdx::RowSourceF32 src{probs, ld, probs, ld, rows, vec};
-  return hip_status(
-      sdx::launch_draw_probs(src, nullptr, jobs, rows, vocab, recs, counters, ids, s),
-      "draw_probs");
+  sdx::DenseArgs a = {};
+  a.p = probs;
+  a.ld = ld;
+  a.rows = rows;
+  a.V = vocab;
+  a.nrec = sdx::dense_nrec(vocab);
+  a.vec = aligned16(probs) && (ld % 4) == 0;
+  a.mass = c.take<uint64_t>((size_t)rows * a.nrec);
+  a.u = u;
+  a.y = ids;
+  return hip_status(sdx::launch_sample_dense(a, (hipStream_t)stream), "sample_dense");
 }
 
 // ------------------------------------------------------------------ residual_probs
 size_t sdx_residual_probs_workspace(int64_t rows, int64_t vocab) {
-  return sdx_sample_probs_workspace(rows, vocab);
+  int64_t rec_ids;
+  int nrec;
+  sdx::draw_layout(vocab, &rec_ids, &nrec);
+  Carve c{nullptr};
+  c.take<sdx::SampleJob>(rows);
+  c.take<sdx::ChunkRec>((size_t)rows * nrec);
+  return c.used;
 }
 
 int sdx_residual_probs(const float* p, const float* q, int64_t rows, int64_t vocab, int64_t ld,

@@ -193,7 +193,27 @@ hipError_t launch_draw_probs(const RowSourceF32& src, const AcceptArgs* acc, Sam
                              int64_t* y, hipStream_t s, const uint32_t* tie_bits = nullptr);
 hipError_t launch_chunk_mass_probs(const RowSourceF32& src, SampleJob* jobs, int64_t njobs,
                                    int64_t V, ChunkRec* recs, hipStream_t s);
-// to_probs output of 16-bit rows; `counts` holds rows * nchunk words.
+// to_probs output of 16-bit rows: ids per chunk (one workgroup each).
+constexpr int64_t kMatChunk = 16384;
+
+// sample_from_probs over dense fp32 rows: record masses (mass[rows * nrec]
+// words, nrec = dense_nrec(V)), then one workgroup per row draws y.
+constexpr int kDenseRec = 2048;
+inline int32_t dense_nrec(int64_t V) { return (int32_t)((V + kDenseRec - 1) / kDenseRec); }
+struct DenseArgs {
+  const float* p;
+  int64_t ld;
+  int64_t rows;
+  int64_t V;
+  int32_t nrec;
+  bool vec;        // p 16-byte aligned and ld % 4 == 0
+  uint64_t* mass;  // [rows, nrec]
+  const float* u;  // [rows]
+  int64_t* y;      // [rows]
+};
+hipError_t launch_sample_dense(const DenseArgs& a, hipStream_t s);
+// to_probs output of 16-bit rows: the group members per chunk of partial rows
+// into `counts` (rows * nchunk words), then the output.
 hipError_t launch_materialize16(int fmt, const RowSource16& src, const RowStat* stats,
                                 const float* tables, float T, int64_t rows, int64_t V,
                                 int64_t chunk, int nchunk, uint32_t* counts, float* out,

@@ -613,13 +613,22 @@ draw16_kernel(Draw16Args<FMT> a) {
 }
 
 // ---------------------------------------------------------------- to_probs output
+// Rows are cut into chunks of kMatRounds block rounds (SM_ROUND ids each), one
+// workgroup each. A row whose boundary tie group is partially kept needs, in
+// every chunk, the number of group members before it (members are kept lowest
+// ids first): one pass counts them per chunk, then the output pass writes the
+// chunk.
+constexpr int kMatRounds = (int)(kMatChunk / SM_ROUND);
+static_assert(kMatChunk % SM_ROUND == 0, "whole block rounds per chunk");
+
 struct MaterializeArgs {
   int64_t V;
-  int64_t chunk;
+  int64_t chunk;     // ids per chunk, kMatRounds * SM_ROUND
   int32_t nchunk;
   uint32_t* counts;  // [rows, nchunk] group members per chunk (partial rows only)
   float* out;
   int64_t ld_out;
+  bool vec_out;      // out 16-byte aligned and ld_out % 4 == 0
 };
 
 __device__ __forceinline__ bool partial_group(const RowStat& st) {
@@ -636,10 +645,29 @@ __global__ void __launch_bounds__(SM_NT) member_count_kernel(Eval16<FMT> ev, Mat
   const uint16_t* ptr = row < ev.split ? ev.base + row * ev.ld : ev.base2 + (row - ev.split) * ev.ld2;
   const int64_t c0 = cidx * a.chunk;
   const int64_t c1 = min(a.V, c0 + a.chunk);
+  uint4 raw[kMatRounds];
+#pragma unroll
+  for (int u = 0; u < kMatRounds; ++u) {  // every load in flight before any count
+    const int64_t idx = c0 + (int64_t)u * SM_ROUND + (int64_t)threadIdx.x * 8;
+    raw[u] = idx + 8 <= c1 ? *reinterpret_cast<const uint4*>(ptr + idx) : make_uint4(0, 0, 0, 0);
+  }
   uint32_t cnt = 0;
-  for (int64_t i = c0 + threadIdx.x; i < c1; i += SM_NT) {
-    const int32_t kk = (int32_t)key_of_code16(ptr[i]);
-    cnt += (kk >= st.glo && kk <= st.ghi) ? 1u : 0u;
+#pragma unroll
+  for (int u = 0; u < kMatRounds; ++u) {
+    const int64_t idx = c0 + (int64_t)u * SM_ROUND + (int64_t)threadIdx.x * 8;
+    const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+    if (idx + 8 <= c1) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int32_t kk = (int32_t)key_of_code16((t & 1) ? w[t >> 1] >> 16 : w[t >> 1] & 0xFFFFu);
+        cnt += (kk >= st.glo && kk <= st.ghi) ? 1u : 0u;
+      }
+    } else {
+      for (int64_t i = idx; i < c1; ++i) {  // the row's last ids (V % 8)
+        const int32_t kk = (int32_t)key_of_code16(ptr[i]);
+        cnt += (kk >= st.glo && kk <= st.ghi) ? 1u : 0u;
+      }
+    }
   }
   cnt = wave_sum_u32(cnt);
   if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = cnt;
@@ -657,14 +685,23 @@ __global__ void __launch_bounds__(SM_NT) materialize16_kernel(Eval16<FMT> ev, Ma
   __shared__ uint32_t s32[SM_NW];
   const int64_t row = (int64_t)blockIdx.x / a.nchunk;
   const int64_t cidx = (int64_t)blockIdx.x % a.nchunk;
+  const int64_t c0 = cidx * a.chunk;
+  const int64_t c1 = min(a.V, c0 + a.chunk);
+  typename Eval16<FMT>::Row r;
+  r.ptr = row < ev.split ? ev.base + row * ev.ld : ev.base2 + (row - ev.split) * ev.ld2;
+  // the chunk's loads first, then the table
+  uint4 raw[kMatRounds];
+#pragma unroll
+  for (int u = 0; u < kMatRounds; ++u) {
+    const int64_t idx = c0 + (int64_t)u * SM_ROUND + (int64_t)threadIdx.x * 8;
+    raw[u] = idx < c1 ? ev.fetch(r, idx, c1) : make_uint4(0, 0, 0, 0);
+  }
   ev.stage(row, tbl);
   __syncthreads();
-  typename Eval16<FMT>::Row r;
   ev.bind(r, row, tbl);
+  float* o = a.out + row * a.ld_out;
   if (r.st.flags & kRowUnsupported) {  // outside the row kernel's windows: mark, don't guess
-    float* o = a.out + row * a.ld_out;
-    for (int64_t i = cidx * a.chunk + threadIdx.x; i < min(a.V, (cidx + 1) * a.chunk); i += SM_NT)
-      o[i] = __builtin_nanf("");
+    for (int64_t i = c0 + threadIdx.x; i < c1; i += SM_NT) o[i] = __builtin_nanf("");
     return;
   }
   const bool part = partial_group(r.st);
@@ -674,31 +711,146 @@ __global__ void __launch_bounds__(SM_NT) materialize16_kernel(Eval16<FMT> ev, Ma
     for (int64_t c = threadIdx.x; c < cidx; c += SM_NT) v += a.counts[row * a.nchunk + c];
     block_excl_u32(v, s32, &rank);
   }
-  const int64_t c0 = cidx * a.chunk;
-  const int64_t c1 = min(a.V, c0 + a.chunk);
-  float* o = a.out + row * a.ld_out;
-  for (int64_t r0 = c0; r0 < c1; r0 += SM_ROUND) {
+#pragma unroll
+  for (int u = 0; u < kMatRounds; ++u) {
+    const int64_t r0 = c0 + (int64_t)u * SM_ROUND;
+    if (r0 >= c1) break;  // uniform
     const int64_t idx = r0 + (int64_t)threadIdx.x * 8;
     float p[8];
     uint32_t m = 0;
-    if (idx < c1) m = ev.load8(r, idx, c1, p);
-    if (part) {
+    if (idx < c1) {
+      m = ev.eval(r, idx, c1, raw[u], p) & 0xFFu;
+    } else {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) p[t] = 0.0f;
+    }
+    if (part) {  // member ranks: a block scan per round (members kept lowest ids first)
       uint32_t tot;
       uint32_t rk = rank + block_excl_u32((uint32_t)__popc(m), s32, &tot);
       rank += tot;
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if ((m >> u) & 1u) { if ((int32_t)rk >= r.st.rstar) p[u] = 0.0f; ++rk; }
+      for (int t = 0; t < 8; ++t)
+        if ((m >> t) & 1u) { if ((int32_t)rk >= r.st.rstar) p[t] = 0.0f; ++rk; }
     } else if (r.st.rstar <= 0) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if ((m >> u) & 1u) p[u] = 0.0f;
+      for (int t = 0; t < 8; ++t)
+        if ((m >> t) & 1u) p[t] = 0.0f;
     }
-    if (idx < c1) {
+    if (a.vec_out && idx + 8 <= c1) {
+      *reinterpret_cast<float4*>(o + idx) = make_float4(p[0], p[1], p[2], p[3]);
+      *reinterpret_cast<float4*>(o + idx + 4) = make_float4(p[4], p[5], p[6], p[7]);
+    } else if (idx < c1) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (idx + u < c1) o[idx + u] = p[u];
+      for (int t = 0; t < 8; ++t)
+        if (idx + t < c1) o[idx + t] = p[t];
     }
+  }
+}
+
+// ---------------------------------------------------------------- sample_from_probs
+// Inverse-CDF draws from dense fp32 probability rows (no tie groups, no q), in
+// two launches and with no counters: every wave sums the fixed62 weights of one
+// record of kDenseRec ids (8 float4 loads per lane, all in flight at once);
+// then one workgroup per row scans the row's record masses, takes the record
+// holding floor(u * total) and walks its ids to the draw. A weight is
+// fixed62(p) for p > 0 and 0 otherwise, in both passes, so the walked record's
+// ids sum to the mass the first pass gave it.
+constexpr int kDenseNT = 256;
+
+__device__ __forceinline__ uint64_t dense_w(float v) { return v > 0.0f ? fixed62(v) : 0ull; }
+
+__global__ void __launch_bounds__(kDenseNT) dense_mass_kernel(DenseArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t g = (int64_t)blockIdx.x * (kDenseNT / kWave) + threadIdx.x / kWave;
+  if (g >= a.rows * a.nrec) return;  // whole waves (no block barrier below)
+  const int64_t row = g / a.nrec;
+  const int64_t x0 = (g % a.nrec) * kDenseRec;
+  const int64_t x1 = min(a.V, x0 + kDenseRec);
+  const float* src = a.p + row * a.ld;
+  uint64_t s = 0;
+  if (a.vec && x1 - x0 == kDenseRec) {
+    float4 v[kDenseRec / (4 * kWave)];
+#pragma unroll
+    for (int i = 0; i < kDenseRec / (4 * kWave); ++i)
+      v[i] = *reinterpret_cast<const float4*>(src + x0 + ((int64_t)i * kWave + lane) * 4);
+#pragma unroll
+    for (int i = 0; i < kDenseRec / (4 * kWave); ++i)
+      s += dense_w(v[i].x) + dense_w(v[i].y) + dense_w(v[i].z) + dense_w(v[i].w);
+  } else {
+    for (int64_t i = x0 + lane; i < x1; i += kWave) s += dense_w(src[i]);
+  }
+  s = wave_sum_u64(s);
+  if (lane == 0) a.mass[g] = s;
+}
+
+__global__ void __launch_bounds__(kDenseNT) dense_pick_kernel(DenseArgs a) {
+  static_assert(kDenseNT == SM_NT, "the block scans span SM_NT threads");
+  __shared__ uint64_t s64[SM_NW];
+  __shared__ int64_t s_rec;
+  __shared__ uint64_t s_base;
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  if (tid == 0) s_rec = -1;
+  // ---- the record holding t: thread tid sums records [r0, r1)
+  const int per = (a.nrec + kDenseNT - 1) / kDenseNT;
+  const int r0 = min(a.nrec, tid * per), r1 = min(a.nrec, r0 + per);
+  const uint64_t* m = a.mass + row * a.nrec;
+  uint64_t mine = 0;
+  for (int r = r0; r < r1; ++r) mine += m[r];
+  uint64_t total;
+  const uint64_t ex = block_excl_u64(mine, s64, &total);
+  if (total == 0) {  // uniform: an all-zero row
+    if (tid == 0) a.y[row] = -1;
+    return;
+  }
+  const uint64_t t = uniform_threshold(a.u[row], total);  // < total
+  if (ex <= t && t - ex < mine) {  // exactly one thread
+    uint64_t run = ex;
+    for (int r = r0; r < r1; ++r) {
+      if (t - run < m[r]) {
+        s_rec = r;
+        s_base = run;
+        break;
+      }
+      run += m[r];
+    }
+  }
+  __syncthreads();
+  // ---- walk it: thread tid takes 16 consecutive ids
+  constexpr int kPer = kDenseRec / kDenseNT;
+  const int64_t rs = s_rec;  // >= 0 for u in [0, 1): the record masses sum to total > t
+  if (rs < 0) {              // uniform: u outside [0, 1) (a caller error) draws nothing
+    if (tid == 0) a.y[row] = -1;
+    return;
+  }
+  const int64_t e1 = min(a.V, rs * kDenseRec + kDenseRec);
+  const int64_t i0 = rs * kDenseRec + (int64_t)tid * kPer;
+  const float* src = a.p + row * a.ld;
+  float v[kPer];
+  if (a.vec && i0 + kPer <= e1) {
+#pragma unroll
+    for (int i = 0; i < kPer / 4; ++i) {
+      const float4 x = *reinterpret_cast<const float4*>(src + i0 + 4 * i);
+      v[4 * i] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) v[i] = i0 + i < e1 ? src[i0 + i] : 0.0f;
+  }
+  uint64_t sum = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) sum += dense_w(v[i]);
+  uint64_t tot2;
+  const uint64_t st = s_base + block_excl_u64(sum, s64, &tot2);
+  if (st <= t && t - st < sum) {  // exactly one thread
+    uint64_t acc = st;
+    int64_t f = -1;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      acc += dense_w(v[i]);
+      if (f < 0 && acc > t) f = i0 + i;
+    }
+    a.y[row] = f;
   }
 }
 
@@ -830,7 +982,9 @@ hipError_t launch_materialize16(int fmt, const RowSource16& src, const RowStat* 
                                 int64_t chunk, int nchunk, uint32_t* counts, float* out,
                                 int64_t ld_out, hipStream_t s) {
   if (!src.vec) return hipErrorInvalidValue;
-  MaterializeArgs ma{V, chunk, nchunk, counts, out, ld_out};
+  if (chunk != (int64_t)kMatRounds * SM_ROUND) return hipErrorInvalidValue;
+  MaterializeArgs ma{V, chunk, nchunk, counts, out, ld_out,
+                     ((uintptr_t)out & 15u) == 0 && (ld_out % 4) == 0};
   const dim3 grid((unsigned)(nchunk * rows));
   if (fmt == SDX_BF16) {
     Eval16<SDX_BF16> ev{src.base, src.ld, src.base2, src.ld2, src.split, stats, tables, T};
@@ -841,6 +995,19 @@ hipError_t launch_materialize16(int fmt, const RowSource16& src, const RowStat* 
     hipLaunchKernelGGL((member_count_kernel<SDX_F16>), grid, dim3(SM_NT), 0, s, ev, ma);
     hipLaunchKernelGGL((materialize16_kernel<SDX_F16>), grid, dim3(SM_NT), 0, s, ev, ma);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_sample_dense(const DenseArgs& a, hipStream_t s) {
+  if (a.rows <= 0) return hipSuccess;
+  if (!a.p || !a.mass || !a.u || !a.y || a.V < 1 || a.ld < a.V ||
+      a.nrec != dense_nrec(a.V))
+    return hipErrorInvalidValue;
+  const int64_t waves = a.rows * a.nrec;
+  const int64_t wpb = kDenseNT / kWave;
+  hipLaunchKernelGGL(dense_mass_kernel, dim3((unsigned)((waves + wpb - 1) / wpb)), dim3(kDenseNT),
+                     0, s, a);
+  hipLaunchKernelGGL(dense_pick_kernel, dim3((unsigned)a.rows), dim3(kDenseNT), 0, s, a);
   return hipGetLastError();
 }
 

@@ -120,17 +120,22 @@ def stream_of(t):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
-def workspace(nbytes, device):
-    """A new workspace of at least `nbytes`, prepared by sdx_workspace_init on the
-    current stream (zero-filled, header word set: the verify entry points keep
-    arrival counters in it that every call leaves at zero)."""
+def workspace(nbytes, device, prepare=True):
+    """A new workspace of at least `nbytes`; with `prepare`, prepared by
+    sdx_workspace_init on the current stream (zero-filled, header word set: the
+    verify entry points keep arrival counters in it that every call leaves at
+    zero)."""
     n = (max(int(nbytes), 1) + 255) // 256 * 256
     ws = torch.empty(n, dtype=torch.uint8, device=device)
-    check(lib().sdx_workspace_init(ptr(ws), n, stream_of(ws)), "sdx_workspace_init")
+    if prepare:
+        check(lib().sdx_workspace_init(ptr(ws), n, stream_of(ws)), "sdx_workspace_init")
     return ws
 
 
 _WS_CACHE = {}
+# entry points whose workspace must be prepared (they keep arrival counters or
+# per-row state in it); the others use theirs as plain scratch
+_PREPARED_KINDS = {"verify", "draft", "greedy"}
 
 
 def cached_workspace(nbytes, device, kind):
@@ -141,11 +146,12 @@ def cached_workspace(nbytes, device, kind):
     offsets that other entry points would overwrite. Under graph capture a new
     workspace is allocated (from the graph's pool) and not kept."""
     dev = torch.device(device)
+    prepare = kind in _PREPARED_KINDS
     if torch.cuda.is_current_stream_capturing():
-        return workspace(nbytes, dev)
+        return workspace(nbytes, dev, prepare)
     key = (dev.index, torch.cuda.current_stream(dev).cuda_stream, kind)
     ws = _WS_CACHE.get(key)
     if ws is None or ws.numel() < int(nbytes):
-        ws = workspace(nbytes, dev)
+        ws = workspace(nbytes, dev, prepare)
         _WS_CACHE[key] = ws
     return ws

@@ -334,6 +334,68 @@ def bench_kv(args, torch):
             "cpu_baseline": None}
 
 
+def bench_probs(args, torch):
+    """The standalone drop-ins the reference engine calls most (`engine.py:250,282`
+    `to_probs`, `engine.py:301-302` `sample_from_probs`): 256 rows of V=151936
+    bf16 logits (B=64 x k=4 draft positions), T=0.8, top-p 0.95 -> fp32
+    probabilities, then one inverse-CDF draw per row from them. Each call is
+    timed on its own, replayed from graphs over three rotating input sets."""
+    from specdec.sampling import sample_from_probs, to_probs
+    from specdec.workloads import uniforms, zipf_logits
+    rows, V, T, tp = 256, 151936, 0.8, 0.95
+    dev = "cuda:0"
+    sets = []
+    for i in range(3):
+        g = torch.Generator(device=dev).manual_seed(2000 + i)
+        sets.append((zipf_logits(rows, V, g, dev), uniforms((rows,), g, dev)))
+    probs = [None] * 3
+
+    def tp_step(i):  # captured: probs[i] is the graph's static output
+        probs[i] = to_probs(sets[i][0], T, tp)
+
+    def sp_step(i):
+        sample_from_probs(probs[i], u=sets[i][1])
+
+    for _ in range(max(1, args.warmup)):
+        for i in range(3):
+            tp_step(i)
+            sp_step(i)
+    gt = [capture(lambda i=i: tp_step(i), torch) for i in range(3)]
+    gs = [capture(lambda i=i: sp_step(i), torch) for i in range(3)]
+    ms_tp_call = timed_graphs(gt, args.steps, torch)
+    ms_sp = timed_graphs(gs, args.steps, torch)
+    # for reference: a plain fill of the same fp32 output (pure writes, torch's kernel)
+    fills = [torch.empty(rows, V, dtype=torch.float32, device=dev) for _ in range(3)]
+    gf = [capture(lambda f=f: f.fill_(0.5), torch) for f in fills]
+    ms_fill = timed_graphs(gf, args.steps, torch)
+    alg_tp = rows * V * (2 + 4)                     # bf16 logits in, fp32 probs out
+    alg_sp = rows * V * 4                           # fp32 probs in
+    ach_tp = alg_tp / (ms_tp_call / 1e3) / 1e9
+    ach_sp = alg_sp / (ms_sp / 1e3) / 1e9
+    return {"metric": "to_probs + sample_from_probs, 256 x 151936 bf16 logits, GB/s",
+            "value": round((alg_tp + alg_sp) / ((ms_tp_call + ms_sp) / 1e3) / 1e9, 1),
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(ms_tp_call + ms_sp, 5), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "to_probs 256 x 151936 bf16 (T=0.8, top-p 0.95) -> fp32, "
+                                   "then sample_from_probs on it", "rows": rows, "vocab": V},
+            "to_probs_us": round(ms_tp_call * 1e3, 2),
+            "sample_from_probs_us": round(ms_sp * 1e3, 2),
+            "fill_output_us": round(ms_fill * 1e3, 2),
+            "roofline": {"bound": "hbm",
+                         "kernel": "to_probs (rowstream + member_count + materialize16)",
+                         "achieved": round(ach_tp, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(ach_tp / HBM_PEAK_GBS, 4), "traffic": None,
+                         "algorithmic_bytes": alg_tp, "avg_launch_us": round(ms_tp_call * 1e3, 2)},
+            "roofline_sample": {"bound": "hbm", "kernel": "sample_from_probs "
+                                "(dense_mass + dense_pick)", "achieved": round(ach_sp, 1),
+                                "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": round(ach_sp / HBM_PEAK_GBS, 4), "traffic": None,
+                                "algorithmic_bytes": alg_sp,
+                                "avg_launch_us": round(ms_sp * 1e3, 2)},
+            "cpu_baseline": None}
+
+
 def bench_ragged(args, torch):
     """Config 5's sampler: B=128 rows with per-row k_b = best_k(alpha_b, 0.1),
     alpha_b ~ U(0.4, 0.9), V=151936 bf16 logits as in the fused verify, T=0.7,
@@ -458,7 +520,7 @@ def main():
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="verify",
-                    choices=["verify", "greedy", "kv", "attn", "ragged"])
+                    choices=["verify", "greedy", "kv", "attn", "ragged", "probs"])
     ap.add_argument("--sets", type=int, default=3)
     ap.add_argument("--attn-chunk", type=int, default=0,
                     help="attn workload: keys per chunk (0: the library default)")
@@ -478,7 +540,7 @@ def main():
         print("bench.py: no ROCm device visible", file=sys.stderr)
         sys.exit(1)
     fn = {"verify": bench_verify, "greedy": bench_greedy, "kv": bench_kv,
-          "attn": bench_attn, "ragged": bench_ragged}[args.workload]
+          "attn": bench_attn, "ragged": bench_ragged, "probs": bench_probs}[args.workload]
     result = fn(args, torch)
     if args.calibrate_copy:
         # a device-to-device copy of known size: its FETCH_SIZE / WRITE_SIZE per

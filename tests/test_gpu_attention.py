@@ -154,3 +154,34 @@ def test_verify_attention_long_rows_unstaged_merge():
     nch = (int(inp["kv_len"].max()) + 63) // 64
     assert nch * inp["max_q"] * 4 > 4096
     _check(inp, 32, 8, chunk_tokens=64)
+
+
+def test_verify_attention_bench_shape_sampled_rows():
+    """The bench shape: B=128 rows of contexts U[1024, 8192], k_b from the
+    controller's best_k (alpha ~ U(0.4, 0.9), k_max 8), 32/8 heads x 128, block
+    16, the library's default chunking, in one launch. Eight rows (the longest,
+    the shortest and six others) are checked against the float64 oracle, each
+    on its own pages."""
+    inp = attn_inputs(128, seed=2024, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = verify_attention_paged(inp["q"], inp["cu_q"], inp["k_pool"], inp["v_pool"],
+                                 inp["block_table"], inp["kv_len"], inp["max_q"], error=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    kv = inp["kv_len"].cpu().numpy()
+    cu = inp["cu_q"].cpu().numpy()
+    g = np.random.default_rng(7)
+    rows = sorted({int(kv.argmax()), int(kv.argmin()), *g.choice(128, 6, replace=False).tolist()})
+    d, bs = inp["d"], inp["k_pool"].shape[1]
+    for b in rows:
+        pages = (int(kv[b]) + bs - 1) // bs
+        ids = inp["block_table"][b, :pages].long()
+        kp = inp["k_pool"][ids].float().cpu().numpy()
+        vp = inp["v_pool"][ids].float().cpu().numpy()
+        q = inp["q"][int(cu[b]):int(cu[b + 1])].float().cpu().numpy()
+        ref = OA.verify_attention_paged(q, np.array([0, q.shape[0]]), kp, vp,
+                                        np.arange(pages)[None], kv[b:b + 1], 32, 8,
+                                        1.0 / np.sqrt(d))
+        got = out[int(cu[b]):int(cu[b + 1])].float().cpu().numpy()
+        bad = np.abs(got - ref) > 2e-2 + 2e-2 * np.abs(ref)
+        assert not bad.any(), (b, np.abs(got - ref).max())

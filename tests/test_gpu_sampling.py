@@ -190,6 +190,46 @@ def test_sample_from_probs_and_residual():
     assert np.array_equal(_np(S.gather_prob(p, gi)), O.gather_prob(_np(p), gi.cpu().numpy()))
 
 
+@pytest.mark.parametrize("V,pad", [(1, 0), (3000, 0), (4096, 0), (4097, 3), (12288, 0),
+                                   (12288, 1), (151936, 0), (151936, 5)])
+def test_sample_from_probs_records_and_edges(V, pad):
+    """Draws over whole 4096-id records, a partial last record and rows whose
+    stride is not a multiple of 4 (unaligned, scalar loads), with hand-placed
+    rows: all-zero (-1), a single mass at the last id, masses on both sides of
+    a record boundary, u = 0 and the largest u below 1, next to random rows."""
+    g = torch.Generator(device=DEV).manual_seed(4000 + V + pad)
+    rows = 12
+    base = torch.zeros(rows, V + pad, device=DEV, dtype=torch.float32)
+    p = base[:, :V]
+    p[:6] = S.to_probs(zipf_logits(6, V, g, DEV), 0.9, 0.95)
+    p[6] = torch.rand(V, generator=g, device=DEV) / V        # dense, unnormalised
+    p[7] = 0.0                                                 # all zero
+    p[8, V - 1] = 0.25                                         # one mass at the end
+    if V > 4096:
+        p[9, 4095], p[9, 4096] = 0.5, 0.5                      # across a boundary
+    else:
+        p[9, 0], p[9, V - 1] = 0.5, 0.5
+    p[10] = p[0]
+    p[11] = p[1]
+    u = uniforms((rows,), g, DEV)
+    u[10] = 0.0
+    u[11] = float(np.nextafter(np.float32(1.0), np.float32(0.0)))
+    if pad:  # straight through the C ABI on the padded rows (stride V + pad)
+        from specdec import _lib
+        L = _lib.lib()
+        out = torch.empty(rows, dtype=torch.int64, device=DEV)
+        ws = _lib.workspace(L.sdx_sample_probs_workspace(rows, V), DEV)
+        rc = L.sdx_sample_probs(_lib.ptr(base), rows, V, V + pad, _lib.ptr(u), _lib.ptr(out),
+                                _lib.ptr(ws), ws.numel(), _lib.stream_of(base))
+        _lib.check(rc, "sample_from_probs")
+        ids = out.cpu().numpy()
+    else:
+        ids = S.sample_from_probs(p, u=u).cpu().numpy()
+    want = O.sample_from_probs(_np(p), _np(u))
+    assert np.array_equal(ids, want), (ids, want)
+    assert ids[7] == -1 and ids[8] == V - 1
+
+
 def test_g1_config1_on_gpu():
     """G1 gate on the HIP path: B=1, k=4, V=64, target N(0, 2^2), draft = target +
     N(0, 0.8^2), T=1, 100,000 trials; first-token TV vs the exact target marginal
