@@ -270,14 +270,15 @@ verify_attn_kernel(AttnArgs a) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) o[j] = (va_f4){0.0f, 0.0f, 0.0f, 0.0f};
   float m_run[4], l_run[4];
-  int lim[4];  // last visible key of the lane's rows, relative to the chunk (-1: none)
+  int lim[4];  // last visible key of the lane's rows, relative to the chunk (-1: none;
+               // at most n - 1, so a tile past the chunk's end is all masked)
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     m_run[r] = -INFINITY;
     l_run[r] = 0.0f;
     const int i = r0 + lr + r;
     const int64_t l = i < M ? base + i / a.group - c0 : -1;
-    lim[r] = (int)max((int64_t)-1, min(l, (int64_t)a.chunk));
+    lim[r] = (int)max((int64_t)-1, min(l, (int64_t)n - 1));
   }
 
   // the wave's query operands, in registers: lane holds row r0 + lc, dims
