@@ -554,14 +554,17 @@ __device__ __forceinline__ void rec16_entry(const Rec16Rows& R, Rec16Acc& A, uin
   A.cnt += (ip && iq ? 1u : 0u) + (ip ? 0x10000u : 0u);
 }
 // Common case: p-live ids by a signed 16-bit compare of the code with the cut
-// (thp = klo_p - 0x8000 >= 0), q members (one code, cqg) by a code compare; the
-// p-live ids go through the wave's LDS list L, evaluated one per lane once 64
-// have gathered. TAIL: the record runs past V (ids past V are skipped).
+// (thp = klo_p - 0x8000 >= 0), q members (one code, cqg) counted per lane from
+// the packed codes into nq_l (in the last record, TAIL, by a wave vote per id
+// into nq_s); the p-live ids go through the wave's LDS list L, evaluated one per
+// lane once 64 have gathered. TAIL: the record runs past V (ids past V are skipped).
 template <int FMT, bool TAIL>
 __device__ __forceinline__ void rec16_fast(const Quad4& P, const Quad4& Q, int64_t x0, int64_t V,
                                            int lane, int32_t thp, bool hasgq, uint32_t cqg,
                                            uint32_t* L, const Rec16Rows& R, Rec16Acc& A,
-                                           uint32_t& nq_s) {
+                                           uint32_t& nq_s, uint32_t& nq_l) {
+  typedef unsigned short pq_us2 __attribute__((ext_vector_type(2)));
+  const uint32_t cqg2 = cqg | (cqg << 16);
   uint32_t off = 0;  // uniform
 #pragma unroll
   for (int u = 0; u < kRec16Rounds; ++u) {
@@ -569,6 +572,13 @@ __device__ __forceinline__ void rec16_fast(const Quad4& P, const Quad4& Q, int64
     const uint32_t pw[4] = {pu.x, pu.y, pu.z, pu.w};
     const uint32_t qw[4] = {qu.x, qu.y, qu.z, qu.w};
     const int64_t nv = TAIL ? V - (x0 + u * kDrawSub + (int64_t)lane * 8) : 8;
+    if (!TAIL && hasgq) {  // q group members: equal halves of the packed codes
+      pq_us2 ne = {0, 0};
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        ne += __builtin_elementwise_min(__builtin_bit_cast(pq_us2, qw[k] ^ cqg2), (pq_us2){1, 1});
+      nq_l += 8u - (uint32_t)ne[0] - (uint32_t)ne[1];
+    }
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       const uint32_t cp = (t & 1) ? pw[t >> 1] >> 16 : pw[t >> 1] & 0xFFFFu;
@@ -576,7 +586,7 @@ __device__ __forceinline__ void rec16_fast(const Quad4& P, const Quad4& Q, int64
       const bool in = !TAIL || t < nv;
       const bool live = (int32_t)(int16_t)cp >= thp && in;
       const uint64_t m = __ballot(live);
-      if (hasgq) nq_s += (uint32_t)__popcll(__ballot(cq == cqg && in));
+      if (TAIL && hasgq) nq_s += (uint32_t)__popcll(__ballot(cq == cqg && in));
       if (m) {
         if (live)
           L[off + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
@@ -770,16 +780,16 @@ __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a, Draw16Lds&
     R.totf_q = rq.st.totf;
     const int32_t klo_p = rp.st.klo;
     Rec16Acc A = {0, 0, 0, 0, 0, 0};
-    uint32_t nqv = 0;   // per lane: q group members (in-place path)
+    uint32_t nqv = 0;   // per lane: q group members (in-place path, packed counts)
     uint32_t nq_s = 0;  // per wave: q group members (listed path)
     if (klo_p >= 0x8000 && (!hasq || R.glo_q >= R.ghi_q)) {
       const int32_t thp = klo_p - 0x8000;  // p-live: positive code >= this
       const bool hasgq = hasq && R.glo_q == R.ghi_q;
       const uint32_t cqg = hasgq ? code_of_key16((uint32_t)R.glo_q) : 0u;
       if (x0 + kRec16 <= V)
-        rec16_fast<FMT, false>(P, Q, x0, V, lane, thp, hasgq, cqg, lst[w], R, A, nq_s);
+        rec16_fast<FMT, false>(P, Q, x0, V, lane, thp, hasgq, cqg, lst[w], R, A, nq_s, nqv);
       else
-        rec16_fast<FMT, true>(P, Q, x0, V, lane, thp, hasgq, cqg, lst[w], R, A, nq_s);
+        rec16_fast<FMT, true>(P, Q, x0, V, lane, thp, hasgq, cqg, lst[w], R, A, nq_s, nqv);
     } else {
       rec16_general<FMT>(P, Q, x0, V, lane, klo_p, R, A, nqv);
     }
