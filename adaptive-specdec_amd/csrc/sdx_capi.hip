@@ -329,14 +329,16 @@ static size_t verify_ws_bytes(int64_t batch, int64_t ntgt, int64_t ndrf, int64_t
   if (ragged) {
     c.take<int64_t>(ntgt);
     c.take<uint8_t>(batch);
+    c.take<int32_t>(rows);  // the rows in batch-row order (fused kernel)
+    c.take<int32_t>(rows);  // each row's batch row
   }
   if (dtype == SDX_F32) c.take<uint32_t>((size_t)rows * sdx::kF32TieWords);  // tie-group bits
   return c.used;
 }
 
 // The fused verify kernel (row statistics and draw in one launch) serves bf16
-// logits at one k per batch row; SDX_VERIFY_FUSED=0 in the environment selects
-// the two-launch path instead.
+// logits, at one k or per-row k (2 k_max + 1 <= 64, batch <= 1024);
+// SDX_VERIFY_FUSED=0 in the environment selects the two-launch path instead.
 static bool fused_enabled() {
   static const bool on = [] {
     const char* e = getenv("SDX_VERIFY_FUSED");
@@ -433,10 +435,15 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
   uint8_t* split_ws = c.take<uint8_t>(split_bytes);
   int64_t* tgt_idx = nullptr;
   uint8_t* bad = nullptr;
+  int32_t* order = nullptr;
+  int32_t* rowjob = nullptr;
   if (cu_k) {
     tgt_idx = c.take<int64_t>(ntgt);
     bad = c.take<uint8_t>(batch);
-    if (int e = hip_status(sdx::launch_ragged_rows(cu_k, batch, k, ntgt, ndrf, tgt_idx, bad, s),
+    order = c.take<int32_t>(rows);
+    rowjob = c.take<int32_t>(rows);
+    if (int e = hip_status(sdx::launch_ragged_rows(cu_k, batch, k, ntgt, ndrf, tgt_idx, bad, s,
+                                                   order, rowjob),
                            "ragged_rows"))
       return e;
   }
@@ -481,19 +488,21 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
     a.split_ws = split_ws;
     a.split_bytes = split_bytes;
     a.ws_header = header;
-    if (dtype == SDX_BF16 && !cu_k && !stats_only && 2 * (int64_t)k + 1 <= 64 &&
+    if (dtype == SDX_BF16 && !stats_only && 2 * (int64_t)k + 1 <= 64 &&
         batch <= sdx::kWsFusedMaxJobs && fused_enabled()) {
       // one launch: the draw of each batch row starts as soon as its rows are in.
       // Its counters sit at fixed header offsets (every call leaves them at zero),
-      // so a workspace reused across shapes never hands it stale counts.
+      // so a workspace reused across shapes never hands it stale counts. Per-row
+      // k takes the rows in the batch-row order ragged_rows_kernel listed.
       sdx::AcceptArgs aa{st,    batch, k,         u_accept, u_final, active, jobs,
                          n_acc, flags, draft_ids, cu_k,     bad,     ntgt};
       sdx::RowSource16 src{(const uint16_t*)target_logits, vocab, (const uint16_t*)draft_logits,
                            vocab, ntgt, true};
+      a.jm_order = order;
       return hip_status(
           sdx::launch_verify_fused_bf16(a, rows, src, aa, batch, vocab, temperature, recs,
                                         header + sdx::kWsFusedDrawWord,
-                                        header + sdx::kWsFusedJobWord, y, s),
+                                        header + sdx::kWsFusedJobWord, y, s, rowjob),
           "verify_fused_bf16");
     }
     if (int e = row_stats16(dtype, a, rows, s)) return e;

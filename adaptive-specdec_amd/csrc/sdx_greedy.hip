@@ -165,29 +165,51 @@ hipError_t launch_greedy_accept(const int64_t* am, int64_t batch, int32_t k, con
 // Per-row k: one workgroup checks cu_k (cu_k[0] = 0, cu_k[batch] = ndrf, non-
 // decreasing, every k_b <= k_max) and maps each target row to the drafted id
 // it gathers. Inconsistent offsets mark every row bad: rows then overlap, so
-// none of their row sets can be trusted.
+// none of their row sets can be trusted. With `order` / `rowjob` (the fused
+// verify kernel) it also lists the rows in batch-row order (batch row b's
+// k_b + 1 target rows then its k_b draft rows, from q = 2 cu_k[b] + b) and gives
+// each row its batch row; bad offsets: the identity order and no batch row (-1).
 __global__ void __launch_bounds__(1024) ragged_rows_kernel(const int64_t* cu_k, int64_t batch,
                                                           int32_t k_max, int64_t ntgt,
                                                           int64_t ndrf, int64_t* tgt_idx,
-                                                          uint8_t* bad) {
+                                                          uint8_t* bad, int32_t* order,
+                                                          int32_t* rowjob) {
   int ok = cu_k[0] == 0 && cu_k[batch] == ndrf && ndrf + batch == ntgt;
   for (int64_t b = threadIdx.x; b < batch; b += blockDim.x) {
     const int64_t kb = cu_k[b + 1] - cu_k[b];
     ok &= kb >= 0 && kb <= k_max;
   }
   ok = __syncthreads_and(ok);
+  if (!ok && order) {
+    for (int64_t q = threadIdx.x; q < ntgt + ndrf; q += blockDim.x) {
+      order[q] = (int32_t)q;
+      rowjob[q] = -1;
+    }
+  }
   for (int64_t b = threadIdx.x; b < batch; b += blockDim.x) {
     bad[b] = ok ? 0 : 1;
     if (!ok) continue;
     const int64_t c0 = cu_k[b], kb = cu_k[b + 1] - c0;
     for (int64_t i = 0; i <= kb; ++i) tgt_idx[c0 + b + i] = i < kb ? c0 + i : -1;
+    if (order) {
+      const int64_t q0 = 2 * c0 + b;
+      for (int64_t i = 0; i <= kb; ++i) {
+        order[q0 + i] = (int32_t)(c0 + b + i);
+        rowjob[c0 + b + i] = (int32_t)b;
+      }
+      for (int64_t i = 0; i < kb; ++i) {
+        order[q0 + kb + 1 + i] = (int32_t)(ntgt + c0 + i);
+        rowjob[ntgt + c0 + i] = (int32_t)b;
+      }
+    }
   }
 }
 
 hipError_t launch_ragged_rows(const int64_t* cu_k, int64_t batch, int32_t k_max, int64_t ntgt,
-                              int64_t ndrf, int64_t* tgt_idx, uint8_t* bad, hipStream_t s) {
+                              int64_t ndrf, int64_t* tgt_idx, uint8_t* bad, hipStream_t s,
+                              int32_t* order, int32_t* rowjob) {
   hipLaunchKernelGGL(ragged_rows_kernel, dim3(1), dim3(1024), 0, s, cu_k, batch, k_max, ntgt, ndrf,
-                     tgt_idx, bad);
+                     tgt_idx, bad, order, rowjob);
   return hipGetLastError();
 }
 

@@ -50,6 +50,7 @@ struct RowStatArgs {
   uint32_t* split_cnt;  // the header's counters (set by launch_rowstream_bf16)
   uint8_t* split_parts;
   int32_t jm_k;  // fused verify kernel: rows are taken in batch-row order at this k
+  const int32_t* jm_order;  // ... or, at per-row k, in this order (block's q -> row)
 };
 
 struct F32Args {
@@ -162,10 +163,12 @@ hipError_t launch_rowstream_bf16(const RowStatArgs& a, int64_t rows, hipStream_t
 struct AcceptArgs;
 struct RowSource16;
 struct ChunkRec;
+// per-row k (acc.cu_k): `rowjob` gives each row its batch row (-1: none) and
+// rs.jm_order the rows' batch-row order, both from launch_ragged_rows
 hipError_t launch_verify_fused_bf16(const RowStatArgs& rs, int64_t rows, const RowSource16& src,
                                     const AcceptArgs& acc, int64_t njobs, int64_t V, float T,
                                     ChunkRec* recs, uint32_t* counters, uint32_t* job_cnt,
-                                    int64_t* y, hipStream_t s);
+                                    int64_t* y, hipStream_t s, const int32_t* rowjob = nullptr);
 // bytes of RowStatArgs::split_ws that let launch_rowstream_bf16 split rows over
 // several blocks on the current device (0: it would not split)
 size_t rowstream_split_bytes(int64_t rows, int64_t V);
@@ -229,7 +232,8 @@ hipError_t launch_onehot(const int64_t* am, int64_t rows, int64_t V, float* out,
 // per-row k: validates cu_k [batch+1] against k_max and the row counts; writes
 // tgt_idx [ntgt] (target row -> index into the drafted ids, -1: bonus) and bad [batch]
 hipError_t launch_ragged_rows(const int64_t* cu_k, int64_t batch, int32_t k_max, int64_t ntgt,
-                              int64_t ndrf, int64_t* tgt_idx, uint8_t* bad, hipStream_t s);
+                              int64_t ndrf, int64_t* tgt_idx, uint8_t* bad, hipStream_t s,
+                              int32_t* order = nullptr, int32_t* rowjob = nullptr);
 hipError_t launch_greedy_accept(const int64_t* am, int64_t batch, int32_t k, const int64_t* ids,
                                 const float* u_accept, const uint8_t* active, int64_t* n_acc,
                                 int64_t* y, uint8_t* flags, hipStream_t s,

@@ -470,7 +470,7 @@ __device__ __forceinline__ int64_t rowstream_body(const RowStatArgs& a, SkLds& L
     }
     row = a.nwhole + sidx;
   }
-  if (FUSED) row = jm_row(row, a.jm_k, a.nrows[0]);
+  if (FUSED) row = a.jm_order ? (int64_t)a.jm_order[row] : jm_row(row, a.jm_k, a.nrows[0]);
   const int g = row < a.nrows[0] ? 0 : 1;
   const int64_t r = g ? row - a.nrows[0] : row;
   const uint16_t* __restrict__ ptr = a.base[g] + r * a.ld[g];
@@ -1206,7 +1206,8 @@ struct FusedArgs {
   int64_t nrow;      // row blocks
   int64_t nrow_pad;  // the first draw block (a multiple of 8: block % 8 keeps the XCD)
   Draw16Args<SDX_BF16> d;
-  uint32_t need;     // rows per batch row
+  uint32_t need;     // rows per batch row (per-row k: 2 k_b + 1, from acc.cu_k)
+  const int32_t* rowjob;  // per-row k: each row's batch row (-1: offsets inconsistent)
 };
 
 __global__ void __launch_bounds__(SK_NT) __attribute__((amdgpu_waves_per_eu(6)))
@@ -1226,8 +1227,10 @@ verify_fused_bf16_kernel(FusedArgs a) {
     __syncthreads();
     if (threadIdx.x == 0) {
       const int64_t nt = a.rs.nrows[0];
-      const int64_t b = row < nt ? row / (a.rs.k + 1) : (row - nt) / a.rs.k;
-      __hip_atomic_fetch_add(&a.d.job_cnt[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int64_t b = a.rowjob ? (int64_t)a.rowjob[row]
+                                 : (row < nt ? row / (a.rs.k + 1) : (row - nt) / a.rs.k);
+      if (b >= 0)
+        __hip_atomic_fetch_add(&a.d.job_cnt[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     return;
   }
@@ -1243,12 +1246,25 @@ verify_fused_bf16_kernel(FusedArgs a) {
     j = t / a.d.nblk;
     bi = (int)(t % a.d.nblk);
   }
+  // per-row k: a batch row with inconsistent offsets draws nothing (its rows
+  // were not counted in); it gets n_acc 0 and SDX_FLAG_BAD_ROW
+  const AcceptArgs& acc = a.d.acc;
+  if (acc.cu_k && acc.bad[j]) {
+    if (threadIdx.x == 0 && bi == 0) {
+      if (acc.n_acc) acc.n_acc[j] = 0;
+      if (acc.flags) acc.flags[j] = (uint8_t)SDX_FLAG_BAD_ROW;
+      a.d.y[j] = -1;
+    }
+    return;
+  }
   if (threadIdx.x == 0) {
     int ok = 0;
+    const uint32_t need =
+        acc.cu_k ? (uint32_t)(2 * (acc.cu_k[j + 1] - acc.cu_k[j]) + 1) : a.need;
     if (__hip_atomic_load(a.rs.ws_header, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == kWsMagic) {
       const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
       for (;;) {
-        if (__hip_atomic_load(&a.d.job_cnt[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= a.need) {
+        if (__hip_atomic_load(&a.d.job_cnt[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= need) {
           ok = 1;
           break;
         }
@@ -1273,13 +1289,18 @@ verify_fused_bf16_kernel(FusedArgs a) {
 hipError_t launch_verify_fused_bf16(const RowStatArgs& rs, int64_t rows, const RowSource16& src,
                                     const AcceptArgs& acc, int64_t njobs, int64_t V, float T,
                                     ChunkRec* recs, uint32_t* counters, uint32_t* job_cnt,
-                                    int64_t* y, hipStream_t s) {
+                                    int64_t* y, hipStream_t s, const int32_t* rowjob) {
+  const bool ragged = acc.cu_k != nullptr;
   if (!src.vec || !y || !job_cnt || !rs.ws_header || V % 8 != 0 || rs.k < 1 ||
-      2 * rs.k + 1 > kWave || rows != njobs * (2 * (int64_t)rs.k + 1))
+      2 * rs.k + 1 > kWave ||
+      (ragged ? (!rowjob || !rs.jm_order || !acc.bad)
+              : rows != njobs * (2 * (int64_t)rs.k + 1)))
     return hipErrorInvalidValue;
   FusedArgs a = {};
   a.rs = rs;
   a.rs.jm_k = rs.k;
+  if (!ragged) a.rs.jm_order = nullptr;
+  a.rowjob = ragged ? rowjob : nullptr;
   a.rs.zero = nullptr;  // the draw counters reset themselves (a row block could clear one late)
   a.rs.nzero = 0;
   a.nrow = rowstream_setup(a.rs, rows);
