@@ -11,6 +11,7 @@
 namespace sdx {
 
 constexpr int AM_NT = 512;
+typedef unsigned short am_us2 __attribute__((ext_vector_type(2)));
 
 template <int DT>
 __device__ __forceinline__ uint64_t pack_best(uint32_t key, int64_t idx) {
@@ -42,6 +43,58 @@ __global__ void __launch_bounds__(AM_NT) argmax_kernel(const void* data, int64_t
           best = c > best ? c : best;
         }
       }
+    }
+  } else if (vec && V / ((int64_t)AM_NT * 8) < 0xFFF0) {
+    // Whole 8-element chunks with packed 16-bit work: both keys of a word at
+    // once (-0 folded onto +0), and per element slot e of the chunk a running
+    // best (key << 16) | (0xFFFF - round), whose max keeps the largest key and,
+    // among equal keys, the earliest round. Four rounds of loads in flight; the
+    // last V % 8 elements go through the per-element form below.
+    const uint16_t* p = static_cast<const uint16_t*>(data) + row * ld;
+    constexpr int64_t kStep = (int64_t)AM_NT * 8;  // ids per block round
+    const int64_t nround = (V + kStep - 1) / kStep;
+    uint32_t bk[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) bk[e] = 0u;
+    for (int64_t r0 = 0; r0 < nround; r0 += 4) {
+      uint4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t i0 = (r0 + u) * kStep + (int64_t)threadIdx.x * 8;
+        // past the whole chunks: all-ones codes (key 0, later rounds lose ties)
+        v[u] = i0 + 8 <= V ? *reinterpret_cast<const uint4*>(p + i0)
+                           : make_uint4(0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t inv = 0xFFFFu - (uint32_t)(r0 + u);
+        const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          uint32_t k2 = keys2_of_codes2(w[t]);
+          // -0 (key 0x7FFF) -> +0 (0x8000): add 1 to exactly those halves
+          const uint32_t x = k2 ^ 0x7FFF7FFFu;
+          const uint32_t nz = __builtin_bit_cast(
+              uint32_t, __builtin_elementwise_min(__builtin_bit_cast(am_us2, x), (am_us2){1, 1}));
+          k2 += 0x00010001u - nz;
+          bk[2 * t] = max(bk[2 * t], (k2 << 16) | inv);
+          bk[2 * t + 1] = max(bk[2 * t + 1], (k2 & 0xFFFF0000u) | inv);
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (bk[e] != 0u) {
+        const int64_t rr = (int64_t)(0xFFFFu - (bk[e] & 0xFFFFu));
+        const uint64_t c = pack_best<DT>(bk[e] >> 16, rr * kStep + (int64_t)threadIdx.x * 8 + e);
+        best = c > best ? c : best;
+      }
+    }
+    for (int64_t i = V / 8 * 8 + threadIdx.x; i < V; i += AM_NT) {  // the last V % 8
+      uint32_t k = key_of_code16(p[i]);
+      if (k == 0x7FFFu) k = 0x8000u;  // -0 == +0
+      const uint64_t c = pack_best<DT>(k, i);
+      best = c > best ? c : best;
     }
   } else {
     const uint16_t* p = static_cast<const uint16_t*>(data) + row * ld;

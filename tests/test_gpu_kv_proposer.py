@@ -203,3 +203,34 @@ def test_slot_mapping_and_argmax():
         y = x[:, :4096].to(dt)
         assert np.array_equal(greedy_draft_tokens(y).cpu().numpy(),
                               OS.argmax_first(y.float().cpu().numpy()))
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("V", [8, 4099, 4096 * 4 + 13, 151936])
+def test_argmax_strided_rows_edges(dt, V):
+    """sdx_argmax on rows with a padded stride (16-byte aligned, so the packed
+    whole-chunk path runs and the last V % 8 elements take the per-element one):
+    zeros with a -0, all-equal rows, the maximum in the last element, ties across
+    rounds and chunk slots, -inf rows; first index among equal maxima."""
+    from specdec import _lib
+    ld = (V + 7) // 8 * 8 + 8
+    g = torch.Generator(device=DEV).manual_seed(V)
+    base = torch.randn((10, ld), generator=g, device=DEV).to(dt)
+    x = base[:, :V]
+    x[0] = 0.0
+    x[0, V // 2] = -0.0
+    x[1] = -3.0
+    x[2, V - 1] = 100.0
+    x[3, [1, V - 2]] = 100.0
+    x[4] = -float("inf")
+    x[4, V - 1] = -1000.0
+    x[5, [V - 1, V // 3, (V // 3) + 4097 if (V // 3) + 4097 < V else 0]] = 50.0
+    x[6] = -0.0
+    x[7] = -float("inf")
+    x[8, [0, V - 1]] = 60.0
+    out = torch.empty(10, dtype=torch.int64, device=DEV)
+    rc = _lib.lib().sdx_argmax(_lib.ptr(base), _lib.dtype_code(base), 10, V, ld, _lib.ptr(out),
+                               _lib.stream_of(base))
+    _lib.check(rc, "sdx_argmax")
+    want = OS.argmax_first(x.float().cpu().numpy())
+    assert np.array_equal(out.cpu().numpy(), want), (out.cpu().numpy(), want)
