@@ -9,7 +9,7 @@ logits with a Zipf head, draft = target + N(0,1), draft ids drawn from q) are
 resident in HBM; three input sets (525 MB, more than the 256 MB MALL) rotate so
 no step reads another step's bytes from cache.
 
-    python bench.py [--steps K] [--warmup W] [--workload verify|greedy|kv|attn]
+    python bench.py [--steps K] [--warmup W] [--workload verify|greedy|kv|attn|ragged|probs]
 
 Prints one JSON line: verified tokens/s (sum over rows of n_acc + 1 per
 step), the roofline of the fused verify step (algorithmic bytes = every logit
