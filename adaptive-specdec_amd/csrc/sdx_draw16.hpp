@@ -116,12 +116,15 @@ struct Eval16 {
     const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
     const int32_t klo = r.st.klo, glo = r.st.glo, ghi = r.st.ghi, kmax = r.st.kmax;
     const int32_t tmax = max(r.st.ntbl - 1, 0);
+    // ids in range: idx + t < lim exactly when t < nv (a 32-bit count of at most 8)
+    const int32_t nv = (int32_t)min(max(lim - idx, (int64_t)0), (int64_t)8);
+    const uint32_t kw[4] = {keys2_of_codes2(w[0]), keys2_of_codes2(w[1]), keys2_of_codes2(w[2]),
+                            keys2_of_codes2(w[3])};
     uint32_t mask = 0, slow = 0;
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-      const uint32_t code = (t & 1) ? (w[t >> 1] >> 16) : (w[t >> 1] & 0xFFFFu);
-      const int32_t key = (int32_t)key_of_code16(code);
-      const bool live = idx + t < lim && key >= klo;
+      const int32_t key = (int32_t)((t & 1) ? (kw[t >> 1] >> 16) : (kw[t >> 1] & 0xFFFFu));
+      const bool live = t < nv && key >= klo;
       const bool mem = live && key >= glo && key <= ghi;
       const int32_t tt = kmax - key;
       const float tv = r.tbl[min(max(tt, 0), tmax)];
