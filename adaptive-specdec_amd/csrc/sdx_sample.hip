@@ -651,6 +651,13 @@ __global__ void __launch_bounds__(SM_NT) member_count_kernel(Eval16<FMT> ev, Mat
     const int64_t idx = c0 + (int64_t)u * SM_ROUND + (int64_t)threadIdx.x * 8;
     raw[u] = idx + 8 <= c1 ? *reinterpret_cast<const uint4*>(ptr + idx) : make_uint4(0, 0, 0, 0);
   }
+  // whole 8-id groups on packed keys: key - glo (mod 2^16) is at most ghi - glo
+  // exactly for a member (a partial group is not empty), so the saturating
+  // (ghi - glo + 1) - (key - glo), capped at 1, is 1 for a member and 0 otherwise
+  typedef unsigned short mc_us2 __attribute__((ext_vector_type(2)));
+  const mc_us2 glo2 = {(unsigned short)st.glo, (unsigned short)st.glo};
+  const mc_us2 span2 = {(unsigned short)(st.ghi - st.glo + 1), (unsigned short)(st.ghi - st.glo + 1)};
+  mc_us2 pk = {0, 0};  // per half at most 4 x 8 members
   uint32_t cnt = 0;
 #pragma unroll
   for (int u = 0; u < kMatRounds; ++u) {
@@ -658,9 +665,9 @@ __global__ void __launch_bounds__(SM_NT) member_count_kernel(Eval16<FMT> ev, Mat
     const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
     if (idx + 8 <= c1) {
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const int32_t kk = (int32_t)key_of_code16((t & 1) ? w[t >> 1] >> 16 : w[t >> 1] & 0xFFFFu);
-        cnt += (kk >= st.glo && kk <= st.ghi) ? 1u : 0u;
+      for (int t = 0; t < 4; ++t) {
+        const mc_us2 d = __builtin_bit_cast(mc_us2, keys2_of_codes2(w[t])) - glo2;
+        pk += __builtin_elementwise_min(__builtin_elementwise_sub_sat(span2, d), (mc_us2){1, 1});
       }
     } else {
       for (int64_t i = idx; i < c1; ++i) {  // the row's last ids (V % 8)
@@ -669,6 +676,7 @@ __global__ void __launch_bounds__(SM_NT) member_count_kernel(Eval16<FMT> ev, Mat
       }
     }
   }
+  cnt += (uint32_t)pk[0] + (uint32_t)pk[1];
   cnt = wave_sum_u32(cnt);
   if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = cnt;
   __syncthreads();
