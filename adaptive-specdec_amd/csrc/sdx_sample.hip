@@ -736,10 +736,12 @@ __global__ void __launch_bounds__(SM_NT) materialize16_kernel(Eval16<FMT> ev, Ma
       uint32_t tot;
       uint32_t rk = rank + block_excl_u32((uint32_t)__popc(m), s32, &tot);
       rank += tot;
+      if (m != 0u) {  // few lanes hold members: the others (usually the whole wave) skip
 #pragma unroll
-      for (int t = 0; t < 8; ++t)
-        if ((m >> t) & 1u) { if ((int32_t)rk >= r.st.rstar) p[t] = 0.0f; ++rk; }
-    } else if (r.st.rstar <= 0) {
+        for (int t = 0; t < 8; ++t)
+          if ((m >> t) & 1u) { if ((int32_t)rk >= r.st.rstar) p[t] = 0.0f; ++rk; }
+      }
+    } else if (r.st.rstar <= 0 && m != 0u) {
 #pragma unroll
       for (int t = 0; t < 8; ++t)
         if ((m >> t) & 1u) p[t] = 0.0f;
