@@ -64,8 +64,6 @@ void chunking(int64_t V, int64_t* chunk, int* nchunk) {
   *nchunk = (int)((V + sdx::kMatChunk - 1) / sdx::kMatChunk);
 }
 
-constexpr int64_t kMaxVocab16 = 16 * 20 * 512;  // register capacity of the row kernel
-
 // Workspace of the transform + draw pipeline over `rows` rows and `njobs` draws.
 size_t transform_ws(Carve& c, int64_t rows, int64_t V, int dtype, int64_t njobs,
                     sdx::RowStat** stats, float** tables, float** dense, sdx::SampleJob** jobs,
@@ -96,9 +94,10 @@ int check_vocab(int dtype, int64_t V) {
   if (dtype == SDX_F32 && V > sdx::kF32MaxVocab)
     return fail(SDX_EUNSUPPORTED, "fp32 logits support vocab <= %lld (got %lld)",
                 (long long)sdx::kF32MaxVocab, (long long)V);
-  if (dtype != SDX_F32 && V > kMaxVocab16)
-    return fail(SDX_EUNSUPPORTED, "16-bit logits support vocab <= %lld (got %lld)",
-                (long long)kMaxVocab16, (long long)V);
+  const int64_t max16 = dtype == SDX_BF16 ? sdx::kMaxVocabBf16 : sdx::kMaxVocabF16;
+  if (dtype != SDX_F32 && V > max16)
+    return fail(SDX_EUNSUPPORTED, "%s logits support vocab <= %lld (got %lld)",
+                dtype == SDX_BF16 ? "bf16" : "fp16", (long long)max16, (long long)V);
   return SDX_OK;
 }
 

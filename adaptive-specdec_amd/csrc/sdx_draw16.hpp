@@ -292,7 +292,7 @@ __device__ __forceinline__ float ld_f32(const float* p) {
 // walks that issue a record's loads before scanning it.
 constexpr int kRec16 = 4 * kDrawSub;
 constexpr int kRec16Rounds = kRec16 / kDrawSub;
-constexpr int kMaxRec16 = (int)((16 * 20 * 512 + kRec16 - 1) / kRec16);  // 16-bit vocab <= 163,840
+constexpr int kMaxRec16 = (int)((kMaxVocabBf16 + kRec16 - 1) / kRec16);  // records of the largest row
 constexpr int kLst16 = kDrawSub + kWave;  // one round of ids plus a leftover below 64
 
 template <int FMT>

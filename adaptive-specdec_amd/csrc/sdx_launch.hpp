@@ -177,6 +177,13 @@ hipError_t launch_workspace_init(void* ws, size_t bytes, hipStream_t s);
 // sdx_rank.hip: pgather of drafted tokens inside a partial tie group (after rowstream)
 hipError_t launch_rank_bf16(const RowStatArgs& a, int64_t rows, hipStream_t s);
 // sdx_f32.hip
+// Largest vocabularies of 16-bit rows. bf16 rows stream through the histogram
+// kernel, whose normaliser queues a bin as (bin << 18 | count): counts, so the
+// vocabulary, stay below 2^18 (the largest multiple of 8 below it, as rows are
+// read in 16-byte groups). fp16 rows are held in the registers of one 1024-thread
+// workgroup: 16 x 20 x 512 values.
+constexpr int64_t kMaxVocabBf16 = (1 << 18) - 8;
+constexpr int64_t kMaxVocabF16 = 16 * 20 * 512;
 constexpr int64_t kF32MaxVocab = 8192;
 constexpr int64_t kF32TieWords = kF32MaxVocab / 32;  // tie-group bit words per fp32 row
 hipError_t launch_to_probs_f32(const F32Args& a, int64_t rows, hipStream_t s);

@@ -79,7 +79,10 @@ int sdx_workspace_init(void* workspace, size_t bytes, sdx_stream_t stream);
 /* ---- sampling transforms: specdec/sampling.py ---------------------------
  * Switches follow sampling.py:43,52,56: temperature <= 0 -> greedy one-hot
  * (first index among maxima); top_p outside (0, 1) -> no nucleus; top_k <= 0
- * or >= vocab -> no top-k. */
+ * or >= vocab -> no top-k.
+ * Vocabularies: bf16 rows up to 262,136 (2^18 - 8), fp16 up to 163,840, fp32 up
+ * to 8,192; larger ones return SDX_EUNSUPPORTED (here and in the verify entry
+ * points) before anything is launched. */
 
 /* to_probs (sampling.py:34-67): logits [rows, vocab] (dtype) -> probs [rows, vocab] fp32. */
 size_t sdx_to_probs_workspace(int64_t rows, int64_t vocab, int dtype);

@@ -108,7 +108,11 @@ def test_c_abi_argument_errors():
 
     assert verify(B, k, V, need - 1) == EWS
     assert b"workspace" in L.sdx_last_error()
-    assert verify(B, k, 163840 + 8, 1 << 40) == EUNSUP
+    assert verify(B, k, (1 << 18), 1 << 40) == EUNSUP  # bf16 rows: vocab <= 2^18 - 8
+    assert b"vocab" in L.sdx_last_error()
+    F16 = 2
+    assert L.sdx_to_probs(fake, F16, 1, 163840 + 8, 163840 + 8, ctypes.c_float(0.8),
+                          ctypes.c_float(0.95), 0, fake, 163840 + 8, fake, 1 << 40, None) == EUNSUP
     assert verify(B, 0, V, need) == EINVAL
     assert verify(B, k, V, need, draft_ids=None) == EINVAL
     assert verify(0, k, V, need) == OK  # an empty batch is a no-op
