@@ -90,7 +90,7 @@ def bench_verify(args, torch):
     from specdec.sampling import Verifier
     from specdec.workloads import verify_inputs
 
-    B, k, V, T, tp = 64, 4, 151936, 0.8, 0.95
+    B, k, V, T, tp = 64, 4, args.vocab, 0.8, 0.95
     dev = "cuda:0"
     log(f"generating {args.sets} input sets B={B} k={k} V={V}")
     sets = [verify_inputs(B, k, V, seed=1000 + i, device=dev, temperature=T, top_p=tp)
@@ -169,15 +169,17 @@ def bench_verify(args, torch):
                        "verify step: rowstream_bf16_kernel + draw16_kernel (two launches)"),
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic_per_launch() if fused else None,
+            # the committed traffic figures were measured at V = 151936
+            "traffic": traffic_per_launch() if fused and V == 151936 else None,
             "algorithmic_bytes": alg_bytes, "avg_launch_us": round(ms * 1e3, 2)}
     cpu = None if args.skip_cpu else cpu_baseline(sets[0], eager[0], args, T, tp, np, torch)
     result = {
-        "metric": METRIC, "value": round(value, 1), "unit": "verified tokens/s", "n_gpus": 1,
+        "metric": METRIC.replace("V=151936", f"V={V}"), "value": round(value, 1),
+        "unit": "verified tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "fused verify B=64 k=4 V=151936 bf16 T=0.8 top-p 0.95",
+        "config": {"workload": f"fused verify B=64 k=4 V={V} bf16 T=0.8 top-p 0.95",
                    "batch": B, "k": k, "vocab": V, "logits": "bf16", "temperature": T,
                    "top_p": tp, "input_sets": len(sets), "hip_graph": not args.no_graph},
         "rows_per_s": round(rows / (ms / 1e3), 1),
@@ -522,6 +524,8 @@ def main():
     ap.add_argument("--workload", default="verify",
                     choices=["verify", "greedy", "kv", "attn", "ragged", "probs"])
     ap.add_argument("--sets", type=int, default=3)
+    ap.add_argument("--vocab", type=int, default=151936,
+                    help="verify workload: vocabulary of the bf16 rows (151936: the headline)")
     ap.add_argument("--attn-chunk", type=int, default=0,
                     help="attn workload: keys per chunk (0: the library default)")
     ap.add_argument("--no-graph", action="store_true")
