@@ -296,6 +296,15 @@ int scratch_for_current_device(hipStream_t s, void** out) {
                 kMaxDevices);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    // preparing the scratch queues a kernel: under graph capture it would be
+    // recorded into the graph instead of run, and every replay would redo it
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (int e = hip_status(hipStreamIsCapturing(s, &cs), "sdx_verify_noalloc: hipStreamIsCapturing"))
+      return e;
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(SDX_EINVAL,
+                  "sdx_verify_noalloc: the first call on device %d is being captured; make one "
+                  "call outside graph capture first (it prepares the device's scratch)", dev);
     void* p = nullptr;
     if (int e = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
                            "sdx_verify_noalloc: hipGetSymbolAddress"))
@@ -500,8 +509,8 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
       a.jm_order = order;
       return hip_status(
           sdx::launch_verify_fused_bf16(a, rows, src, aa, batch, vocab, temperature, recs,
-                                        header + sdx::kWsFusedDrawWord,
-                                        header + sdx::kWsFusedJobWord, y, s, rowjob),
+                                        sdx::fused_draw_words(header),
+                                        sdx::fused_job_words(header), y, s, rowjob),
           "verify_fused_bf16");
     }
     if (int e = row_stats16(dtype, a, rows, s)) return e;
@@ -527,6 +536,42 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
                     "draw16");
 }
 
+int sdx_verify_counter_layout(int64_t batch, int64_t target_rows, int32_t k, int64_t vocab,
+                              int dtype, int32_t cus, int64_t* ranges, int32_t max_ranges) {
+  if (batch < 1 || k < 1 || vocab < 1 || cus < 0 || !dtype_ok(dtype) || !ranges ||
+      max_ranges < 4)
+    return fail(SDX_EINVAL, "sdx_verify_counter_layout: bad arguments");
+  const bool ragged = target_rows > 0;
+  const int64_t ntgt = ragged ? target_rows : batch * ((int64_t)k + 1);
+  const int64_t ndrf = ragged ? target_rows - batch : batch * (int64_t)k;
+  const int64_t rows = ntgt + ndrf;
+  // the carve of verify_impl: the header comes first
+  Carve c{(uint8_t*)nullptr};
+  c.take<uint8_t>(0);
+  const size_t header_at = c.used;
+  c.take<uint32_t>(sdx::kWsHeaderBytes / 4);
+  uint32_t* const h = reinterpret_cast<uint32_t*>((uintptr_t)4096);  // a stand-in base
+  auto off = [&](const uint32_t* p) {
+    return (int64_t)header_at + (int64_t)((const uint8_t*)p - (const uint8_t*)h);
+  };
+  int n = 0;
+  const int64_t nsplit = dtype == SDX_BF16 ? sdx::rowstream_split_rows(rows, vocab, cus) : 0;
+  ranges[2 * n] = off(sdx::split_counter_words(h));
+  ranges[2 * n + 1] = off(sdx::split_counter_words(h) + nsplit);
+  ++n;
+  const bool fused = dtype == SDX_BF16 && 2 * (int64_t)k + 1 <= 64 && batch <= sdx::kWsFusedMaxJobs;
+  ranges[2 * n] = off(sdx::fused_job_words(h));
+  ranges[2 * n + 1] = off(sdx::fused_job_words(h) + (fused ? batch : 0));
+  ++n;
+  ranges[2 * n] = off(sdx::fused_draw_words(h));
+  ranges[2 * n + 1] = off(sdx::fused_draw_words(h) + (fused ? batch : 0));
+  ++n;
+  ranges[2 * n] = (int64_t)header_at;
+  ranges[2 * n + 1] = (int64_t)(header_at + sdx::kWsHeaderBytes);
+  ++n;
+  return n;
+}
+
 int sdx_verify_noalloc(const void* target_logits, const void* draft_logits, int dtype,
                        int64_t batch, int32_t k, int64_t vocab, const int64_t* draft_ids,
                        const float* u_accept, const float* u_final, const uint8_t* active,
@@ -542,6 +587,11 @@ int sdx_verify_noalloc(const void* target_logits, const void* draft_logits, int 
                 (long long)batch, k, (long long)vocab, need, kScratchBytes);
   void* ws = nullptr;
   if (int e = scratch_for_current_device((hipStream_t)stream, &ws)) return e;
+  // a draw whose wait gave up in an earlier call left the header marked: prepare
+  // it again (a one-block kernel that returns at once when the header is intact)
+  if (int e = hip_status(sdx::launch_workspace_rearm(ws, (hipStream_t)stream),
+                         "sdx_verify_noalloc: scratch re-arm"))
+    return e;
   return sdx_verify(target_logits, draft_logits, dtype, batch, k, vocab, draft_ids, u_accept,
                     u_final, active, temperature, top_p, top_k, n_acc, y, flags, ws,
                     kScratchBytes, stream);
@@ -675,13 +725,15 @@ int sdx_round_commit(int64_t batch, int32_t k, const int64_t* cu_k, const int64_
                      const int64_t* y, const int64_t* draft_ids, uint8_t* done,
                      int64_t* out_tokens, int64_t* out_len, int64_t max_new,
                      const int64_t* eos_ids, int32_t n_eos, int64_t* lengths0, int64_t* lengths1,
-                     int64_t* pending, sdx_stream_t stream) {
+                     int64_t* pending, const uint8_t* flags, int32_t* error,
+                     sdx_stream_t stream) {
   if (batch < 0 || !n_acc || !y || !done || !out_tokens || !out_len || max_new < 1 ||
-      n_eos < 0 || (n_eos > 0 && !eos_ids) || (!cu_k && k < 0) || (k > 0 && !draft_ids && !cu_k))
+      n_eos < 0 || (n_eos > 0 && !eos_ids) || (!cu_k && k < 0) || (!draft_ids && (cu_k || k > 0)))
     return fail(SDX_EINVAL, "sdx_round_commit: bad arguments");
   if (batch == 0) return SDX_OK;
   sdx::RoundCommitArgs a{batch, k,       cu_k,   n_acc, y,        draft_ids, done, out_tokens,
-                         out_len, max_new, eos_ids, n_eos, lengths0, lengths1, pending};
+                         out_len, max_new, eos_ids, n_eos, lengths0, lengths1, pending,
+                         flags,   error};
   return hip_status(sdx::launch_round_commit(a, (hipStream_t)stream), "round_commit");
 }
 

@@ -73,6 +73,10 @@ hipError_t launch_draft_epilogue(const DraftEpiArgs& a, hipStream_t s) {
 // are appended to out[b, len..] while they fit: a token equal to an EOS id, or
 // the row reaching max_new tokens, marks it done and stops the row
 // (engine.py:321-339). pending[b] = y[b] for every row (engine.py:340).
+// Verify flags that leave a row's outcome unspecified.
+constexpr uint32_t kCommitBadFlags =
+    SDX_FLAG_NONFINITE | SDX_FLAG_UNSUPPORTED | SDX_FLAG_BAD_ROW | SDX_FLAG_WORKSPACE;
+
 __global__ void round_commit_kernel(RoundCommitArgs a) {
   const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= a.B) return;
@@ -91,9 +95,22 @@ __global__ void round_commit_kernel(RoundCommitArgs a) {
   const int64_t drop = kb - n;
   if (a.len0) a.len0[b] -= drop;
   if (a.len1) a.len1[b] -= drop;
-  const int64_t yb = a.y[b];
+  int64_t yb = a.y[b];
+  if (a.done[b]) {
+    if (a.pending) a.pending[b] = yb;
+    return;
+  }
+  // a live row the verify could not decide (its flags, or no token drawn) emits
+  // nothing, ends, and raises the round's error word
+  const uint32_t fl = a.flags ? (uint32_t)a.flags[b] : 0u;
+  const uint32_t err = ((fl & kCommitBadFlags) ? 1u : 0u) | (yb < 0 ? 2u : 0u);
+  if (err) {
+    if (a.error) atomicOr(reinterpret_cast<uint32_t*>(a.error), err);
+    if (a.pending) a.pending[b] = 0;
+    a.done[b] = 1;
+    return;
+  }
   if (a.pending) a.pending[b] = yb;
-  if (a.done[b]) return;
   auto is_eos = [&](int64_t t) {
     for (int32_t i = 0; i < a.n_eos; ++i)
       if (a.eos[i] == t) return true;

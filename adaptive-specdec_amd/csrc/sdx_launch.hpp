@@ -12,6 +12,10 @@ namespace sdx {
 // for other shapes finds them where the last call left them, at zero.
 constexpr size_t kWsHeaderBytes = 16384;
 constexpr uint32_t kWsMagic = 0x53445857u;
+// Written over the magic word by a fused-verify draw whose bounded wait gave up:
+// the header's counters may then hold counts of that call, so every later call
+// flags its rows (SDX_FLAG_WORKSPACE) until sdx_workspace_init prepares it again.
+constexpr uint32_t kWsDirty = 0x44495254u;
 constexpr int kWsCounterWord = 64;  // split-row arrival counters (256-byte aligned)
 constexpr int kWsMaxCounters = 1024 - kWsCounterWord;
 constexpr int kWsFusedJobWord = 1024;   // fused verify: row arrivals per batch row
@@ -172,8 +176,22 @@ hipError_t launch_verify_fused_bf16(const RowStatArgs& rs, int64_t rows, const R
 // bytes of RowStatArgs::split_ws that let launch_rowstream_bf16 split rows over
 // several blocks on the current device (0: it would not split)
 size_t rowstream_split_bytes(int64_t rows, int64_t V);
+// Rows of a launch over `rows` rows split over several blocks on a device of `cus`
+// compute units (each has an arrival counter at header word kWsCounterWord + its
+// index; split_layout keeps them below kWsMaxCounters).
+int64_t rowstream_split_rows(int64_t rows, int64_t V, int cus);
+// The header words the fused verify's per-batch-row counters start at: the row
+// arrivals (job_cnt) and the draw counters, one word per batch row each.
+inline uint32_t* fused_job_words(uint32_t* header) { return header + kWsFusedJobWord; }
+inline uint32_t* fused_draw_words(uint32_t* header) { return header + kWsFusedDrawWord; }
+inline uint32_t* split_counter_words(uint32_t* header) { return header + kWsCounterWord; }
 // zero `bytes` of a workspace and write the header's magic word
 hipError_t launch_workspace_init(void* ws, size_t bytes, hipStream_t s);
+// One block: if the header's magic word is not kWsMagic (a draw's wait gave up,
+// kWsDirty), zero the header's counter words and write the magic word again.
+// Stream order makes it safe: every kernel of earlier calls on the stream has
+// ended, so no late arrival can still land in the counters.
+hipError_t launch_workspace_rearm(void* ws, hipStream_t s);
 // sdx_rank.hip: pgather of drafted tokens inside a partial tie group (after rowstream)
 hipError_t launch_rank_bf16(const RowStatArgs& a, int64_t rows, hipStream_t s);
 // sdx_f32.hip
@@ -287,6 +305,9 @@ struct RoundCommitArgs {
   int64_t* len0;           // cache lengths rolled back by k - n_acc (nullable)
   int64_t* len1;
   int64_t* pending;        // [B] <- y (nullable)
+  const uint8_t* flags;    // [B] the verify's flags (nullable)
+  int32_t* error;          // OR-ed: 1 a live row flagged NONFINITE / UNSUPPORTED /
+                           // BAD_ROW / WORKSPACE, 2 a live row with y < 0 (nullable)
 };
 hipError_t launch_round_commit(const RoundCommitArgs& a, hipStream_t s);
 struct CtrlState {         // one EWMAAnalytic controller, 32 bytes (sdx_ctrl_state)

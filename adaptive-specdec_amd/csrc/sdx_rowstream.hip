@@ -42,6 +42,8 @@
 // values of different probability) are re-streamed into a histogram anchored
 // at the row maximum (keys [kmax - 10242, kmax]). A decision that needs the
 // order of elements below either window marks the row unsupported.
+#include <stdlib.h>
+
 #include "sdx_draw16.hpp"
 
 namespace sdx {
@@ -1141,6 +1143,12 @@ static size_t split_need(int64_t rows, int64_t nwhole, int p) {
   return (size_t)rest * p * SK_SPLIT_BYTES;
 }
 
+int64_t rowstream_split_rows(int64_t rows, int64_t V, int cus) {
+  int64_t nwhole;
+  const int p = split_layout(rows, V, cus, &nwhole);
+  return p >= 2 ? rows - nwhole : 0;
+}
+
 size_t rowstream_split_bytes(int64_t rows, int64_t V) {
   int64_t nwhole;
   const int p = split_layout(rows, V, device_cus(), &nwhole);
@@ -1162,7 +1170,7 @@ static int64_t rowstream_setup(RowStatArgs& a, int64_t rows) {
     a.nwhole = nwhole;
     a.nparts = p;
     a.xcd_group = (nwhole % 8 == 0 && rest % 8 == 0) ? 1 : 0;
-    a.split_cnt = a.ws_header + kWsCounterWord;
+    a.split_cnt = split_counter_words(a.ws_header);
     a.split_parts = a.split_ws;
     grid = nwhole + rest * p;
   } else {
@@ -1196,9 +1204,13 @@ hipError_t launch_rowstream_bf16(const RowStatArgs& args, int64_t rows, hipStrea
 // The wait ends: row blocks never wait, and on every XCD all row blocks are
 // dispatched before any draw block (workgroups are dispatched in index order),
 // so a draw block never holds a slot a row block still needs. It is bounded all
-// the same: after kFusedWaitTicks of the 100 MHz real-time counter (20 ms, some
-// 250 times the whole launch) the block gives up and flags its batch row
-// (SDX_FLAG_WORKSPACE), with n_acc 0 and y -1.
+// the same: after wait_ticks of the 100 MHz real-time counter (by default 20 ms,
+// some 250 times the whole launch) the block gives up. A block that gives up
+// flags its batch row (SDX_FLAG_WORKSPACE, y -1; n_acc unspecified) and never
+// counts in on the draw counter, so no block of that batch row draws. Its row
+// arrivals may still land after it left, so the header's counters can no longer
+// be trusted: the block overwrites the magic word with kWsDirty, and every later
+// call on the workspace flags its rows until sdx_workspace_init runs again.
 constexpr uint64_t kFusedWaitTicks = 2000000;
 
 struct FusedArgs {
@@ -1208,6 +1220,7 @@ struct FusedArgs {
   Draw16Args<SDX_BF16> d;
   uint32_t need;     // rows per batch row (per-row k: 2 k_b + 1, from acc.cu_k)
   const int32_t* rowjob;  // per-row k: each row's batch row (-1: offsets inconsistent)
+  uint64_t wait_ticks;    // a draw block's bound on its wait for the rows (100 MHz ticks)
 };
 
 __global__ void __launch_bounds__(SK_NT) __attribute__((amdgpu_waves_per_eu(6)))
@@ -1268,7 +1281,11 @@ verify_fused_bf16_kernel(FusedArgs a) {
           ok = 1;
           break;
         }
-        if (__builtin_amdgcn_s_memrealtime() - t0 > kFusedWaitTicks) break;
+        if (__builtin_amdgcn_s_memrealtime() - t0 > a.wait_ticks) {
+          // the counters of this call may now be left behind: mark the header
+          __hip_atomic_store(a.rs.ws_header, kWsDirty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
         __builtin_amdgcn_s_sleep(2);
       }
     }
@@ -1276,7 +1293,9 @@ verify_fused_bf16_kernel(FusedArgs a) {
   }
   __syncthreads();
   if (!U.draw.last) {
-    if (threadIdx.x == 0 && bi == 0) {
+    // every block that gives up flags its batch row; none of them counts in, so
+    // no block of the row draws and these are the row's outputs
+    if (threadIdx.x == 0) {
       if (a.d.acc.n_acc) a.d.acc.n_acc[j] = 0;
       if (a.d.acc.flags) a.d.acc.flags[j] = (uint8_t)SDX_FLAG_WORKSPACE;
       a.d.y[j] = -1;
@@ -1284,6 +1303,18 @@ verify_fused_bf16_kernel(FusedArgs a) {
     return;
   }
   draw16_body<SDX_BF16, true>(a.d, U.draw, j, bi);
+}
+
+// The draw blocks' wait bound: kFusedWaitTicks, or a smaller bound from
+// SDX_VERIFY_WAIT_TICKS (read at every launch; tests set 0 to make every wait give
+// up from the host, so that the give-up path runs while every kernel exits normally).
+static uint64_t fused_wait_ticks() {
+  const char* e = getenv("SDX_VERIFY_WAIT_TICKS");
+  if (!e || !*e) return kFusedWaitTicks;
+  char* end = nullptr;
+  const unsigned long long v = strtoull(e, &end, 10);
+  if (!end || *end != '\0') return kFusedWaitTicks;
+  return v < kFusedWaitTicks ? (uint64_t)v : kFusedWaitTicks;
 }
 
 hipError_t launch_verify_fused_bf16(const RowStatArgs& rs, int64_t rows, const RowSource16& src,
@@ -1318,6 +1349,7 @@ hipError_t launch_verify_fused_bf16(const RowStatArgs& rs, int64_t rows, const R
   d.job_cnt = job_cnt;
   d.y = y;
   a.need = (uint32_t)(2 * rs.k + 1);
+  a.wait_ticks = fused_wait_ticks();
   const int64_t grid = a.nrow_pad + njobs * d.nblk;
   hipLaunchKernelGGL(verify_fused_bf16_kernel, dim3((unsigned)grid), dim3(SK_NT), 0, s, a);
   return hipGetLastError();
@@ -1329,6 +1361,24 @@ __global__ void workspace_init_kernel(uint32_t* ws, int64_t words) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += stride)
     ws[i] = i == 0 ? kWsMagic : 0u;
+}
+
+__global__ void __launch_bounds__(256) workspace_rearm_kernel(uint32_t* hdr) {
+  __shared__ int dirty;
+  if (threadIdx.x == 0) dirty = hdr[0] != kWsMagic;
+  __syncthreads();
+  if (!dirty) return;
+  for (int i = 1 + (int)threadIdx.x; i < (int)(kWsHeaderBytes / 4); i += 256) hdr[i] = 0u;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    hdr[0] = kWsMagic;
+  }
+}
+
+hipError_t launch_workspace_rearm(void* ws, hipStream_t s) {
+  hipLaunchKernelGGL(workspace_rearm_kernel, dim3(1), dim3(256), 0, s, (uint32_t*)ws);
+  return hipGetLastError();
 }
 
 hipError_t launch_workspace_init(void* ws, size_t bytes, hipStream_t s) {

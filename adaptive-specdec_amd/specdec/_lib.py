@@ -41,13 +41,14 @@ _SIGS = {
     "sdx_verify_ragged_workspace": (SZ, [I64, I64, I64, INT]),
     "sdx_verify_ragged": (INT, [P, P, INT, I64, I32, I64, I64, P, P, P, P, P, F, F, I32, P, P, P, P,
                                 SZ, P]),
+    "sdx_verify_counter_layout": (INT, [I64, I64, I32, I64, INT, I32, P, I32]),
     "sdx_verify_stats": (INT, [P, P, INT, I64, I32, I64, P, F, F, I32, P, SZ, P]),
     "sdx_verify_greedy_workspace": (SZ, [I64, I32]),
     "sdx_verify_greedy": (INT, [P, INT, I64, I32, I64, P, P, P, P, P, P, P, SZ, P]),
     "sdx_draft_step_workspace": (SZ, [I64, I64, INT]),
     "sdx_draft_step": (INT, [P, INT, I64, I64, I64, F, F, I32, P, P, P, P, F, I32, I32, P, P, SZ,
                              P]),
-    "sdx_round_commit": (INT, [I64, I32, P, P, P, P, P, P, P, I64, P, I32, P, P, P, P]),
+    "sdx_round_commit": (INT, [I64, I32, P, P, P, P, P, P, P, I64, P, I32, P, P, P, P, P, P]),
     "sdx_controller_update": (INT, [P, I64, P, I64, P, D, I32, I32, I32, I32, P, P, P, P]),
     "sdx_argmax": (INT, [P, INT, I64, I64, I64, P, P]),
     "sdx_slot_mapping": (INT, [P, I64, I64, P, I32, I64, I64, P, P, P]),
@@ -155,3 +156,17 @@ def cached_workspace(nbytes, device, kind):
         ws = workspace(nbytes, dev, prepare)
         _WS_CACHE[key] = ws
     return ws
+
+
+def prepare(ws):
+    """Prepare an existing workspace again (sdx_workspace_init on the current
+    stream): needed after a verify call flagged rows SDX_FLAG_WORKSPACE because a
+    draw's bounded wait gave up, which marks the workspace header."""
+    check(lib().sdx_workspace_init(ptr(ws), ws.numel(), stream_of(ws)), "sdx_workspace_init")
+
+
+def reset_workspaces():
+    """Prepare every cached workspace of the prepared kinds again (see `prepare`)."""
+    for (_, _, kind), ws in _WS_CACHE.items():
+        if kind in _PREPARED_KINDS:
+            prepare(ws)

@@ -17,16 +17,32 @@ condition (`all_done`, `engine.py:232`), the controller's k for the next round
 and the early-exit decision (`controller.py:184-187`, one read per draft step,
 as the reference's `float(conf.mean())`), and `outputs()`.
 
-Models follow `specdec.tinylm.TinyLM`: `forward(tokens [B, q], cache)` returns
-logits [B, q, V] and appends the positions' K/V at the cache's device lengths;
-the engine commits the lengths (`cache.commit(q)`, `kvcache.py:165-168`).
-Every draw takes the caller's uniforms from static buffers (u_draft [k, B],
-u_acc [B, k], u_fin [B]) filled before each round; `generate` fills them from
-one device generator.
+Models follow `specdec.tinylm.TinyLM` (paged cache, graph-capturable) or
+`specdec.hfmodel.HFCausalLM` (a transformers causal LM over `RaggedCache`, the
+reference's own model path, `engine.py:166-183`): `forward(tokens [B, q], cache)`
+returns logits [B, q, V] (of the model's `dtype`) and appends the positions' K/V
+at the cache's device lengths; `prefill(prompt, cache, plen)` takes right-padded
+prompts with per-row lengths and leaves each row's cache at its own length
+(`engine.py:189-195`); the engine commits the lengths (`cache.commit(q)`,
+`kvcache.py:165-168`). Every draw takes the caller's uniforms from static
+buffers (u_draft [k, B], u_acc [B, k], u_fin [B]) filled before each round;
+`generate` fills them from one device generator.
+
+The one host read per round (`sync`, where the reference reads `n_acc.tolist()`)
+also brings back an error word: the round commit raises it for a live row the
+verify flagged (NONFINITE / UNSUPPORTED / BAD_ROW / WORKSPACE) or left without
+a token, and the caches' kernels raise theirs on overflow or a rollback below
+zero. `sync` raises `RuntimeError` then, as the reference fails loudly there
+(torch.multinomial on NaN probabilities). Caches that keep host lengths
+(`RaggedCache`) get them from the same read.
 
 Differences from the reference, by design: a row stops at max_new tokens also
-when max_new is 1 (the reference's first token ignores the limit), and one
-uniform u_fin serves the residual or the bonus draw, whichever the row takes.
+when max_new is 1 (the reference's first token ignores the limit); one uniform
+u_fin serves the residual or the bonus draw, whichever the row takes; the
+controller's observed cost ratio c_obs (draft over target forward time,
+`engine.py:344-346`) comes from device event timings of the eager rounds,
+reaches the controller one round later than in the reference, and keeps its
+last value while rounds replay from graphs.
 """
 import torch
 
@@ -48,7 +64,7 @@ class SpecEngine:
 
     def __init__(self, target, draft, batch, k, temperature=0.0, top_p=1.0, top_k=0,
                  eos_ids=(), max_new=64, capacity=None, prompt_len=0, device="cuda", seed=0,
-                 controller=None, tau=None, min_k=1):
+                 controller=None, tau=None, min_k=1, observe_cost=True):
         if controller is not None and getattr(controller, "mode", "batch") != "batch":
             raise ValueError("SpecEngine drafts one k per round: use a batch-mode controller")
         self.target, self.draft = target, draft
@@ -57,7 +73,11 @@ class SpecEngine:
             raise ValueError("k must be >= 1")
         self.V = target.V
         if draft.V != self.V:
-            raise ValueError("target and draft vocabularies differ")
+            raise ValueError(f"target vocab {self.V} != draft vocab {draft.V}; speculative "
+                             "decoding requires a shared tokenizer")
+        self.dtype = getattr(target, "dtype", torch.bfloat16)
+        if getattr(draft, "dtype", torch.bfloat16) != self.dtype:
+            raise ValueError("target and draft logits must share a dtype")
         self.temperature, self.top_p, self.top_k = temperature, top_p, top_k
         self.T, self.tp, self.tk = _switch_args(temperature, top_p, top_k)
         self.max_new = int(max_new)
@@ -66,9 +86,15 @@ class SpecEngine:
         dev = torch.device(device)
         self.device = dev
         cap = capacity or (int(prompt_len) + 2 * self.max_new + self.k + 2)
+        self.capacity = int(cap)
         self.tcache = target.new_cache(self.B, cap, seed=seed)
         self.dcache = draft.new_cache(self.B, cap, seed=seed + 1)
         B, k, V = self.B, self.k, self.V
+        # error words: the round commit's, then the two caches' (their kernels write
+        # through these views), read back with `done` in one copy per round
+        self.err = torch.zeros(3, dtype=torch.int32, device=device)
+        self.tcache.error = self.err[1:2]
+        self.dcache.error = self.err[2:3]
         eos = [int(e) for e in eos_ids]
         self.eos = torch.tensor(eos or [-1], dtype=torch.int64, device=dev)
         self.n_eos = len(eos)
@@ -78,7 +104,7 @@ class SpecEngine:
         self.out = torch.zeros((B, self.max_new), dtype=torch.int64, device=dev)
         self.out_len = torch.zeros(B, dtype=torch.int64, device=dev)
         self.xs = torch.zeros((B, k), dtype=torch.int64, device=dev)
-        self.dlog = torch.zeros((B, k, V), dtype=torch.bfloat16, device=dev)
+        self.dlog = torch.zeros((B, k, V), dtype=self.dtype, device=dev)
         self.vin = torch.zeros((B, k + 1), dtype=torch.int64, device=dev)
         self.u_draft = torch.zeros((k, B), dtype=torch.float32, device=dev)
         self.u_acc = torch.zeros((B, k), dtype=torch.float32, device=dev)
@@ -94,28 +120,58 @@ class SpecEngine:
         self.last_target_logits = None
         self.last_k = 0
         L = _lib.lib()
-        self.draft_ws = _lib.workspace(L.sdx_draft_step_workspace(B, V, _lib.BF16), dev)
+        dcode = _lib.dtype_code(self.dlog)
+        self.draft_ws = _lib.workspace(L.sdx_draft_step_workspace(B, V, dcode), dev)
         self._verifiers = {}
         self._graphs = {}
         self.controller = controller
         self.rounds = 0
+        # observed cost ratio for the controller (0: keep c), from event timings
+        self.c_obs = torch.zeros(1, dtype=torch.float32, device=dev)
+        self.observe_cost = bool(observe_cost) and controller is not None
+        self._timing = None
+        self._t_draft = self._t_target = 0.0
+        self._n_draft = self._n_target = 0
 
     def _verifier(self, k):
         v = self._verifiers.get(k)
         if v is None:
-            v = Verifier(self.B, k, self.V, torch.bfloat16, temperature=self.temperature,
+            v = Verifier(self.B, k, self.V, self.dtype, temperature=self.temperature,
                          top_p=self.top_p, top_k=self.top_k, device=self.device)
             self._verifiers[k] = v
         return v
 
     # ---- start: prefill and the first token (`engine.py:212-226`)
-    def start(self, prompt, u_first=None):
-        """prompt [B, P] int64 on the device. The first token comes from the
-        target alone (greedy: its argmax; else a draw on u_first [B])."""
-        tlog = self.target.prefill(prompt, self.tcache)
-        self.draft.prefill(prompt, self.dcache)
+    def start(self, prompt, plen=None, u_first=None):
+        """prompt [B, P] int64 on the device, right-padded; plen [B] the real prompt
+        lengths (None: all P). The first token comes from the target alone at each
+        row's last real position (greedy: its argmax; else a draw on u_first [B])."""
+        B, P = prompt.shape
+        if B != self.B:
+            raise ValueError(f"prompt has {B} rows, the engine {self.B}")
+        need = P + self.max_new + self.k + 1
+        if need > self.capacity:
+            raise ValueError(f"prompt length {P} + max_new {self.max_new} + k {self.k} + 1 "
+                             f"exceeds the cache capacity {self.capacity}: pass capacity or "
+                             "prompt_len to SpecEngine")
+        if plen is None:
+            plen = torch.full((B,), P, dtype=torch.int64)
+        plen = torch.as_tensor(plen, dtype=torch.int64)
+        if plen.numel() != B or int(plen.min()) < 1 or int(plen.max()) > P:
+            raise ValueError("plen must hold B lengths in [1, P]")
+        self.err.zero_()
+        for c in (self.tcache, self.dcache):                    # a fresh sequence per row
+            if hasattr(c, "set_lengths"):
+                c.set_lengths(torch.zeros(B, dtype=torch.int64))
+            else:
+                c.lengths.zero_()
+        tlog = self.target.prefill(prompt, self.tcache, plen)
+        self.draft.prefill(prompt, self.dcache, plen)
         x, _, _ = draft_step(tlog.contiguous(), u_first, self.T, self.tp, self.tk,
                              out=self.step_out[self.k], workspace=self.draft_ws)
+        # a first token that could not be drawn (nonfinite prefill logits) raises
+        # the round-commit error word, read at the next sync
+        self.err[0:1].bitwise_or_((x < 0).any().view(1).to(torch.int32) * 2)
         self.pending.copy_(x)
         self.out.zero_()
         self.out[:, 0].copy_(x)
@@ -136,10 +192,15 @@ class SpecEngine:
         if not 1 <= kr <= self.k:
             raise ValueError(f"round k {kr} outside [1, {self.k}]")
         early = self.tau is not None
-        if early and torch.cuda.is_current_stream_capturing():
+        capturing = torch.cuda.is_current_stream_capturing()
+        if early and capturing:
             raise RuntimeError("the confidence early exit reads the device: not capturable")
         if early:
             self.conf.fill_(1.0)
+        timing = None
+        if self.observe_cost and not capturing:
+            timing = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+            timing[0].record()
         feed = self.pending.view(B, 1)
         k_eff = kr
         for i in range(kr):                                     # engine.py:246-258
@@ -162,7 +223,13 @@ class SpecEngine:
         self.vin[:, 0].copy_(self.pending)                      # engine.py:266-270
         self.vin[:, 1:k_eff + 1].copy_(self.xs[:, :k_eff])
         vin = self.vin if k_eff == self.k else self.vin[:, :k_eff + 1].contiguous()
+        if timing is not None:
+            timing[1].record()
+            timing[2].record()
         tlog = self.target.forward(vin, self.tcache)
+        if timing is not None:
+            timing[3].record()
+            self._timing = (timing, k_eff + 1)
         self.tcache.commit(k_eff + 1)
         self.last_target_logits = tlog
         if k_eff == self.k:
@@ -172,17 +239,23 @@ class SpecEngine:
             dlog = self.dlog[:, :k_eff].contiguous()
             ua = self.u_acc[:, :k_eff].contiguous()
         torch.sub(1, self.done, out=self.active)                # alive = ~done
-        n_acc, y, _ = self._verifier(k_eff)(tlog.contiguous(), dlog, xs, ua, self.u_fin,
-                                            self.active)        # engine.py:281-303
+        n_acc, y, flags = self._verifier(k_eff)(tlog.contiguous(), dlog, xs, ua, self.u_fin,
+                                                self.active)    # engine.py:281-303
         rc = _lib.lib().sdx_round_commit(                       # engine.py:305-340
             B, k_eff, None, _lib.ptr(n_acc), _lib.ptr(y), _lib.ptr(xs), _lib.ptr(self.done),
             _lib.ptr(self.out), _lib.ptr(self.out_len), self.max_new, _lib.ptr(self.eos),
             self.n_eos, _lib.ptr(self.tcache.lengths), _lib.ptr(self.dcache.lengths),
-            _lib.ptr(self.pending), _lib.stream_of(self.pending))
+            _lib.ptr(self.pending), _lib.ptr(flags), _lib.ptr(self.err),
+            _lib.stream_of(self.pending))
         _lib.check(rc, "SpecEngine.round")
+        for c in (self.tcache, self.dcache):                    # lengths moved on the device
+            moved = getattr(c, "device_rolled_back", None)
+            if moved is not None:
+                moved()
         if self.controller is not None:                         # controller.py:143-154
             self.k_used.fill_(k_eff)
-            self.controller.update(n_acc, self.k_used)
+            self.controller.update(n_acc, self.k_used,
+                                   c_obs=self.c_obs if self.observe_cost else None)
         self.n_acc, self.y, self.last_k = n_acc, y, k_eff
         self.rounds += 1
         return n_acc, y
@@ -212,8 +285,9 @@ class SpecEngine:
         return n_acc, y
 
     # ---- the generation loop (`engine.py:197-342`)
-    def generate(self, prompt, seed=0, graphs=False, max_rounds=None, on_round=None):
-        """Decode prompt [B, P] to the end (every row at EOS or max_new tokens).
+    def generate(self, prompt, plen=None, seed=0, graphs=False, max_rounds=None, on_round=None):
+        """Decode right-padded prompt [B, P] with real lengths plen [B] (None: all
+        P) to the end (every row at EOS or max_new tokens).
         Uniforms come from one device generator seeded with `seed`, drawn in a
         fixed order per round (u_draft, u_acc, u_fin) at the full k. With
         graphs=True every k is run eagerly once, then captured and replayed.
@@ -221,7 +295,7 @@ class SpecEngine:
         emitted tokens of every row."""
         g = torch.Generator(device=self.device).manual_seed(int(seed))
         u_first = torch.rand(self.B, generator=g, device=self.device)
-        self.start(prompt, u_first)
+        self.start(prompt, plen, u_first)
         n = 0
         while not self.all_done():
             if max_rounds is not None and n >= max_rounds:
@@ -244,8 +318,48 @@ class SpecEngine:
         return self.outputs()
 
     # ---- host reads
+    def sync(self):
+        """The round's one host read: whether every row is done, the error words,
+        and the host lengths of caches that keep them. Raises RuntimeError when a
+        round commit or cache kernel set its error word."""
+        mirrors = [c for c in (self.tcache, self.dcache) if hasattr(c, "set_host_lengths")]
+        parts = [self.done.all().view(1).to(torch.int64), self.err.to(torch.int64)]
+        parts += [c.lengths.view(-1) for c in mirrors]
+        v = torch.cat(parts).cpu()
+        off = 4
+        for c in mirrors:
+            c.set_host_lengths(v[off:off + self.B])
+            off += self.B
+        if self._timing is not None:
+            (ev, nt), self._timing = self._timing, None
+            self._t_draft += ev[0].elapsed_time(ev[1])
+            self._n_draft += nt                                 # k_eff + 1 draft forwards
+            self._t_target += ev[2].elapsed_time(ev[3])
+            self._n_target += 1
+            if self._t_target > 0.0:
+                ratio = (self._t_draft / self._n_draft) / (self._t_target / self._n_target)
+                self.c_obs.fill_(float(ratio))
+        e0, e1, e2 = (int(x) for x in v[1:4])
+        if e0 or e1 or e2:
+            if e0 & 1:  # a WORKSPACE flag marks the verifier's workspace: prepare it again
+                for ver in self._verifiers.values():
+                    if not ver.greedy:
+                        ver.reset_workspace()
+            what = []
+            if e0 & 1:
+                what.append("a live row was flagged NONFINITE, UNSUPPORTED, BAD_ROW or WORKSPACE")
+            if e0 & 2:
+                what.append("a live row got no token (y < 0)")
+            if e1:
+                what.append("the target cache overflowed or rolled back below zero")
+            if e2:
+                what.append("the draft cache overflowed or rolled back below zero")
+            self.err.zero_()
+            raise RuntimeError("SpecEngine: " + "; ".join(what))
+        return bool(v[0])
+
     def all_done(self):
-        return bool(self.done.all())
+        return self.sync()
 
     def outputs(self):
         """The emitted tokens of every row (one device read)."""
@@ -253,13 +367,16 @@ class SpecEngine:
         return [out[b, :min(int(n[b]), self.max_new)].tolist() for b in range(self.B)]
 
 
-def autoregressive(model, prompt, max_new, eos_ids=(), capacity=None, seed=0):
+def autoregressive(model, prompt, max_new, eos_ids=(), capacity=None, seed=0, plen=None):
     """Greedy decoding with the target alone through the same cache, attention and
     argmax kernels (`engine.py:347-381`, generate_autoregressive): the G2
-    baseline. Returns the emitted tokens of every row."""
+    baseline. prompt [B, P] right-padded, plen [B] its real lengths (None: P).
+    Returns the emitted tokens of every row."""
     B, P = prompt.shape
+    if plen is None:
+        plen = torch.full((B,), P, dtype=torch.int64)
     cache = model.new_cache(B, capacity or (P + max_new + 2), seed=seed)
-    logits = model.prefill(prompt, cache)
+    logits = model.prefill(prompt, cache, torch.as_tensor(plen, dtype=torch.int64))
     eos = set(int(e) for e in eos_ids)
     out = [[] for _ in range(B)]
     done = [False] * B

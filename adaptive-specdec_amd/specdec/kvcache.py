@@ -179,9 +179,27 @@ class RaggedCache(_HFCache):
         self._lengths_cpu += int(q)
         self._push()
 
+    def commit(self, q):
+        """`advance(q)` under the name the engine and `PagedKVCache` use."""
+        self.advance(q)
+
     def set_lengths(self, lengths):
         self._lengths_cpu.copy_(torch.as_tensor(lengths, dtype=torch.long).cpu())
         self._push()
+
+    def device_rolled_back(self):
+        """A kernel (the engine's round commit) moved the device lengths: the host
+        mirror is stale until `set_host_lengths` or `sync_lengths`, as after
+        `rollback_device`."""
+        self._dirty = True
+        self._uniform = False
+
+    def set_host_lengths(self, lengths_cpu):
+        """Take the device lengths the caller already read back (no sync here)."""
+        self._lengths_cpu.copy_(torch.as_tensor(lengths_cpu, dtype=torch.long))
+        self._dirty = False
+        self.max_len = int(self._lengths_cpu.max()) if self.batch_size else 0
+        self._uniform = bool(int(self._lengths_cpu.min()) == self.max_len) if self.batch_size else True
 
     def rollback(self, n):
         """Drop the last n[b] tokens of row b; raises below zero like the reference."""

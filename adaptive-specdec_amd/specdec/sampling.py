@@ -14,8 +14,10 @@ rule where it is not:
   probabilities with the first token always kept, renormalise;
 * ties inside the top-p boundary group keep the lowest token ids (the
   reference's CPU sort is unstable, so it leaves this unspecified);
-* the softmax numerator is exp evaluated in float64 and rounded once to fp32,
-  the normaliser and all masses are exact fixed-point sums, so decisions do
+* the softmax numerator is exp_det(s - m) with s = fl32(l / T): a float64
+  Cody-Waite reduction, then the degree-9 Taylor polynomial of exp in fp32
+  Horner form (plain multiply then add), scaled by a power of two; the
+  normaliser and all masses are exact 2^-62 fixed-point sums, so decisions do
   not depend on summation order;
 * sampling is an inverse-CDF draw on a uniform instead of torch.multinomial's
   exponential race: the same distribution, reproducible ids.
@@ -32,7 +34,7 @@ FLAG_ACCEPT_NEAR_TIE = 1   # an evaluated accept test had |u - min(p/q, 1)| < 1e
 FLAG_NONFINITE = 2         # a logit row held +inf or NaN
 FLAG_UNSUPPORTED = 4       # a row's mass spans more distinct values than the kernels represent
 FLAG_BAD_ROW = 8           # per-row k: inconsistent offsets
-FLAG_WORKSPACE = 16        # the workspace was not prepared by sdx_workspace_init
+FLAG_WORKSPACE = 16        # workspace not prepared, or a draw's bounded wait gave up
 FLAG_TIE_ORDER = 32        # a test or the draw touched a partially kept top-p tie group
 
 
@@ -327,6 +329,12 @@ class Verifier:
                                    _lib.ptr(self.ws), self.ws.numel(), st)
         _lib.check(rc, "Verifier")
         return self.n_acc, self.y, self.flags
+
+    def reset_workspace(self):
+        """Prepare the workspace again: after rows came back FLAG_WORKSPACE (a
+        draw's bounded wait gave up and marked the workspace header), every later
+        call flags its rows until this runs."""
+        _lib.prepare(self.ws)
 
     def stats(self, target, draft, draft_ids=None):
         """Phase 1 only (fused to_probs statistics of all rows), for timing.

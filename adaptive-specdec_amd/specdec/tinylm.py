@@ -32,6 +32,7 @@ class TinyLM:
         base's plus noise * N(0, 1/fan_in): a draft that agrees with its target
         on most tokens. `scale` multiplies the logits."""
         self.V, self.hq, self.hkv, self.max_pos = int(vocab), int(hq), int(hkv), int(max_pos)
+        self.dtype = torch.bfloat16  # of the logits
         self.D = self.hq * HEAD
         self.device = torch.device(device)
         g = torch.Generator(device="cpu").manual_seed(int(seed))
@@ -93,13 +94,23 @@ class TinyLM:
             logits.append(torch.mm(hj.contiguous(), p["wlm"]))
         return torch.stack(logits, 1)                                              # [B, q, V]
 
-    def prefill(self, prompt, cache, chunk=16):
-        """prompt [B, P] -> logits at the last position [B, V]; the cache holds the
-        prompt (lengths = P)."""
+    def prefill(self, prompt, cache, plen=None, chunk=16):
+        """Right-padded prompt [B, P] with real lengths plen [B] (None: all P) ->
+        logits at each row's last real position [B, V] (`engine.py:189-195`); the
+        cache then holds each row's own prompt (lengths = plen). Attention is
+        causal, so a real position never sees the pad after it, and the pad's K/V
+        lie past the row's length, where the next forward overwrites them."""
         B, P = prompt.shape
-        out = None
+        last = (torch.full((B,), P, dtype=torch.int64) if plen is None
+                else torch.as_tensor(plen, dtype=torch.int64)).to(self.device) - 1
+        out = torch.empty((B, self.V), dtype=self.dtype, device=self.device)
         for s in range(0, P, chunk):
             t = prompt[:, s:s + chunk].contiguous()
-            out = self.forward(t, cache)
+            logits = self.forward(t, cache)
             cache.commit(t.shape[1])
-        return out[:, -1]
+            here = (last >= s) & (last < s + t.shape[1])
+            off = (last - s).clamp(0, t.shape[1] - 1)
+            pick = logits[torch.arange(B, device=self.device), off]
+            out = torch.where(here.view(B, 1), pick, out)
+        cache.lengths.copy_(last + 1)
+        return out

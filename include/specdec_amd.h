@@ -14,10 +14,13 @@
  *
  * Numerics. Every discrete decision (nucleus membership, top-k threshold,
  * accept/reject, sampled id) is computed with a fixed deterministic rule:
- * softmax numerator exp evaluated in float64 and rounded once to fp32,
- * normaliser and every mass/CDF accumulated exactly in 2^-62 fixed point,
- * stable (lowest id first) tie order, inverse-CDF sampling on caller
- * uniforms. Identical inputs give identical ids on every run and launch
+ * s = fl32(x / T), m = max s, softmax numerator e = exp_det(s - m) where exp_det
+ * is a Cody-Waite reduction in float64 (k = floor(d / ln 2), r = fl32(d - k ln 2)
+ * clamped to [0, ln 2]) followed by the degree-9 Taylor polynomial of exp at r in
+ * fp32 Horner form (plain multiply then add, coefficients fl32(1/n!), clamped at
+ * 2) scaled by 2^k; the normaliser and every mass/CDF accumulated exactly in 2^-62
+ * fixed point; stable (lowest id first) tie order; inverse-CDF sampling on
+ * caller uniforms. Identical inputs give identical ids on every run and launch
  * configuration.
  */
 #ifndef SPECDEC_AMD_H
@@ -53,7 +56,13 @@ enum sdx_flag {
   SDX_FLAG_BAD_ROW = 8,         /* per-row k: the row offsets (cu_k) were inconsistent with
                                    k_max or the row counts; n_acc 0, y unspecified */
   SDX_FLAG_WORKSPACE = 16,      /* the verify workspace was not prepared by
-                                   sdx_workspace_init: results of the row unspecified */
+                                   sdx_workspace_init, or a draw of the fused bf16
+                                   verify gave up its bounded wait (20 ms) for the row
+                                   statistics: y -1, n_acc unspecified. After a give-up
+                                   the workspace header is marked and every later call
+                                   flags its rows until sdx_workspace_init runs again
+                                   (sdx_verify_noalloc prepares its scratch again by
+                                   itself at its next call) */
   SDX_FLAG_TIE_ORDER = 32       /* an evaluated accept test's drafted token, or the final
                                    draw, is a member of a partially kept top-p boundary tie
                                    group (tokens of equal probability of which the nucleus
@@ -166,6 +175,18 @@ int sdx_verify_ragged(const void* target_logits, const void* draft_logits, int d
                       float top_p, int32_t top_k, int64_t* n_acc, int64_t* y, uint8_t* flags,
                       void* workspace, size_t workspace_bytes, sdx_stream_t stream);
 
+/* Where the verify kernels keep their cross-workgroup counters (split-row arrivals,
+ * the fused kernel's per-batch-row row arrivals and draw counters) in a workspace of
+ * this shape (target_rows 0: one k for all rows; else per-row k with target_rows
+ * target rows) on a device of `cus` compute units: ranges[2i], ranges[2i+1] are the
+ * byte offsets [begin, end) of range i, from the same helpers the launches use;
+ * the last range is the header itself. Returns the number of ranges (4), or a
+ * negative status. Pure host arithmetic, for checking that every counter a kernel
+ * is handed lies in the fixed header, which every call leaves at zero. No reference
+ * counterpart. */
+int sdx_verify_counter_layout(int64_t batch, int64_t target_rows, int32_t k, int64_t vocab,
+                              int dtype, int32_t cus, int64_t* ranges, int32_t max_ranges);
+
 /* Phase 1 of sdx_verify alone: the fused to_probs statistics of every target and draft
  * row (normaliser, top-k/top-p boundary, drafted-token probabilities) into the workspace,
  * without the accept test or the final draw. Lets a caller time or overlap the
@@ -210,12 +231,19 @@ int sdx_draft_step(const void* logits, int dtype, int64_t batch, int64_t vocab, 
  * Unless done[b], the accepted drafts and then y[b] are appended to
  * out_tokens[b, out_len[b]..] (capacity max_new per row); a token in eos_ids
  * [n_eos], or the row reaching max_new tokens, sets done[b] and ends the row's
- * emission. pending[b] (nullable) = y[b], the next round's first input. */
+ * emission. pending[b] (nullable) = y[b], the next round's first input.
+ * flags (nullable) are the verify's per-row flags: a row that is not done and is
+ * flagged NONFINITE, UNSUPPORTED, BAD_ROW or WORKSPACE, or whose y is negative,
+ * emits nothing, is set done, gets pending 0 and ORs into *error (nullable, device
+ * int32) 1 (a flag) or 2 (y < 0): the caller reads it where it syncs anyway (the
+ * reference fails loudly there: torch.multinomial raises on NaN probabilities).
+ * draft_ids may be NULL only when no row drafted (k == 0 and no cu_k). */
 int sdx_round_commit(int64_t batch, int32_t k, const int64_t* cu_k, const int64_t* n_acc,
                      const int64_t* y, const int64_t* draft_ids, uint8_t* done,
                      int64_t* out_tokens, int64_t* out_len, int64_t max_new,
                      const int64_t* eos_ids, int32_t n_eos, int64_t* lengths0, int64_t* lengths1,
-                     int64_t* pending, sdx_stream_t stream);
+                     int64_t* pending, const uint8_t* flags, int32_t* error,
+                     sdx_stream_t stream);
 
 /* EWMAAnalytic (controller.py:121-154) on the device. One state per batch
  * (nstate 1: accepted = sum n_acc, reached = sum min(n_acc + 1, k_used[0]), as

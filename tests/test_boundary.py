@@ -123,3 +123,47 @@ def test_c_abi_argument_errors():
                                       fake, 64, fake, ctypes.c_float(0.125), 0, fake, 1 << 30,
                                       fake, None, None)
     assert rc == EUNSUP and b"head_dim" in L.sdx_last_error()
+    # round commit: drafted ids are required whenever a row may have drafted
+    i64 = ctypes.c_void_p(8192)
+
+    def commit(kk, cu, ids):
+        return L.sdx_round_commit(4, kk, cu, i64, i64, ids, fake, i64, i64, 8, None, 0, None,
+                                  None, None, None, None, None)
+
+    assert commit(2, None, None) == EINVAL
+    assert commit(0, i64, None) == EINVAL       # per-row k: any row may draft
+
+
+def test_verify_counters_lie_in_the_header():
+    """Every cross-workgroup counter the verify launches are handed (split-row
+    arrivals, the fused kernel's row arrivals and draw counters) lies inside the
+    fixed 16 KB header, after the magic word, and the ranges do not overlap, for
+    every shape the entry points accept (one k and per-row k, bf16 / fp16 / fp32,
+    devices of 1 to 304 compute units). A counter carved anywhere else would be
+    found stale by a later call of another shape."""
+    from specdec import _lib
+    L = _lib.lib()
+    HDR = 16384
+    r = (ctypes.c_int64 * 8)()
+    shapes = [(1, 1), (4, 4), (64, 4), (256, 8), (1024, 4), (300, 31), (1000, 2), (2048, 4),
+              (64, 40)]
+    n_checked = 0
+    for dt in (0, 1, 2):
+        for V in (16, 1000, 32000, 151936, 262136):
+            for B, k in shapes:
+                for ragged in (False, True):
+                    for cus in (1, 8, 80, 256, 304):
+                        tr = B * (k + 1) - (B // 3 if ragged else 0) if ragged else 0
+                        n = L.sdx_verify_counter_layout(B, tr, k, V, dt, cus, r, 4)
+                        assert n == 4, (dt, V, B, k, cus)
+                        rng = [(r[2 * i], r[2 * i + 1]) for i in range(n)]
+                        h0, h1 = rng[-1]
+                        assert (h0, h1) == (0, HDR)
+                        used = [(b, e) for b, e in rng[:-1] if e > b]
+                        for b, e in used:
+                            assert 4 <= b <= e <= HDR, (dt, V, B, k, cus, b, e)
+                        used.sort()
+                        for (b0, e0), (b1, _) in zip(used, used[1:]):
+                            assert e0 <= b1, (dt, V, B, k, cus, used)
+                        n_checked += 1
+    assert n_checked > 1000

@@ -136,7 +136,7 @@ def test_round_commit_matches_oracle(B, ragged):
     rc = _lib.lib().sdx_round_commit(
         B, k, _lib.ptr(cu), _lib.ptr(d["n_acc"]), _lib.ptr(d["y"]), _lib.ptr(d["ids"]),
         _lib.ptr(done), _lib.ptr(d["out"]), _lib.ptr(d["out_len"]), c["max_new"], _lib.ptr(eos),
-        len(c["eos"]), _lib.ptr(d["len0"]), _lib.ptr(d["len1"]), _lib.ptr(pending),
+        len(c["eos"]), _lib.ptr(d["len0"]), _lib.ptr(d["len1"]), _lib.ptr(pending), None, None,
         _lib.stream_of(pending))
     _lib.check(rc, "sdx_round_commit")
     outs = [list(c["out"][b, :c["out_len"][b]]) for b in range(B)]
@@ -157,6 +157,33 @@ def test_round_commit_matches_oracle(B, ragged):
     assert np.array_equal(d["len0"].cpu().numpy(), c["len0"] - drop)
     assert np.array_equal(d["len1"].cpu().numpy(), c["len1"] - drop)
     assert np.array_equal(pending.cpu().numpy(), c["y"])
+
+
+def test_round_commit_flags_raise_error_word():
+    """A live row flagged NONFINITE / UNSUPPORTED / BAD_ROW / WORKSPACE, or with
+    y < 0, emits nothing and is set done with pending 0, and the error word gets
+    1 (flag) or 2 (y < 0); informational flags (near tie, tie order) and finished
+    rows change nothing."""
+    B, k, max_new = 8, 2, 10
+    n_acc = torch.tensor([1, 1, 1, 1, 1, 1, 1, 1], dtype=torch.int64, device=DEV)
+    y = torch.tensor([5, 6, 7, -1, 9, 10, 11, -1], dtype=torch.int64, device=DEV)
+    ids = torch.arange(100, 100 + B * k, dtype=torch.int64, device=DEV)
+    flags = torch.tensor([0, 2, 1 | 32, 0, 16, 8, 4, 2], dtype=torch.uint8, device=DEV)
+    done = torch.tensor([0, 0, 0, 0, 0, 0, 0, 1], dtype=torch.uint8, device=DEV)
+    out = torch.zeros((B, max_new), dtype=torch.int64, device=DEV)
+    out_len = torch.ones(B, dtype=torch.int64, device=DEV)
+    pending = torch.full((B,), -5, dtype=torch.int64, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    rc = _lib.lib().sdx_round_commit(
+        B, k, None, _lib.ptr(n_acc), _lib.ptr(y), _lib.ptr(ids), _lib.ptr(done), _lib.ptr(out),
+        _lib.ptr(out_len), max_new, None, 0, None, None, _lib.ptr(pending), _lib.ptr(flags),
+        _lib.ptr(err), _lib.stream_of(pending))
+    _lib.check(rc, "sdx_round_commit")
+    assert int(err.item()) == 3
+    assert out_len.cpu().tolist() == [3, 1, 3, 1, 1, 1, 1, 1]
+    assert done.cpu().tolist() == [0, 1, 0, 1, 1, 1, 1, 1]
+    assert pending.cpu().tolist() == [5, 0, 7, 0, 0, 0, 0, -1]
+    assert out[0, 1:3].cpu().tolist() == [100, 5] and out[2, 1:3].cpu().tolist() == [104, 7]
 
 
 # ------------------------------------------------------------------ controller
@@ -385,7 +412,7 @@ def test_engine_device_controller(models, graphs):
     ctl = DeviceController(B, "batch", k_max=kmax, beta=0.98, k_init=3, warmup=2, device=DEV)
     oc = OC.EWMAState(k_max=kmax, beta=0.98, k_init=3, warmup=2)
     eng = SpecEngine(tgt, drf, B, kmax, temperature=0.0, max_new=max_new, prompt_len=P,
-                     device=DEV, controller=ctl)
+                     device=DEV, controller=ctl, observe_cost=False)
     ks = []
 
     def check(e):
@@ -398,3 +425,49 @@ def test_engine_device_controller(models, graphs):
     assert out == autoregressive(tgt, prompt, max_new)
     assert oc.propose_k() == int(ctl.k[0])
     assert len(ks) > 3
+
+
+@pytest.mark.parametrize("graphs", [False, True])
+def test_engine_ragged_prompts_greedy(models, graphs):
+    """Right-padded prompts with per-row lengths (`engine.py:189-226`): each row
+    decodes as it would alone from its unpadded prompt, and greedy speculative
+    decoding still equals target-only decoding from the same padded batch."""
+    tgt, drf = models
+    B, P, max_new = 4, 12, 30
+    prompt = _prompt(B, P, 23)
+    plen = torch.tensor([12, 7, 9, 1])
+    ref = autoregressive(tgt, prompt, max_new, plen=plen)
+    for b in range(B):   # a row alone, unpadded, gives the same tokens
+        alone = autoregressive(tgt, prompt[b:b + 1, :int(plen[b])].contiguous(), max_new)
+        assert alone[0] == ref[b], b
+    eng = SpecEngine(tgt, drf, B, 3, temperature=0.0, max_new=max_new, prompt_len=P, device=DEV)
+    assert eng.generate(prompt, plen, graphs=graphs) == ref
+    assert eng.tcache.lengths.tolist() == eng.dcache.lengths.tolist()
+
+
+def test_engine_rejects_prompt_past_capacity(models):
+    tgt, drf = models
+    eng = SpecEngine(tgt, drf, 2, 4, temperature=0.0, max_new=8, capacity=20, device=DEV)
+    with pytest.raises(ValueError, match="capacity"):
+        eng.start(_prompt(2, 9, 1))
+    eng.start(_prompt(2, 7, 1))        # 7 + 8 + 4 + 1 = 20 fits
+
+
+def test_engine_raises_on_flagged_rows(models):
+    """A target whose logits hold +inf: the verify flags the rows NONFINITE, the
+    round commit emits nothing for them and raises its error word, and the
+    engine's next read raises instead of emitting tokens."""
+    tgt, drf = models
+
+    class InfLM(TinyLM):
+        def forward(self, tokens, cache):
+            out = super().forward(tokens, cache)
+            out[..., 7] = float("inf")
+            return out
+
+    bad = InfLM(V_LM, hq=2, hkv=1, seed=1, device=DEV, scale=4.0)
+    eng = SpecEngine(bad, drf, 3, 2, temperature=0.8, top_p=0.9, max_new=10, prompt_len=6,
+                     device=DEV)
+    with pytest.raises(RuntimeError, match="NONFINITE|no token"):
+        eng.generate(_prompt(3, 6, 2), seed=1)
+    assert eng.out_len.cpu().tolist() == [1, 1, 1]   # only the first token went out
