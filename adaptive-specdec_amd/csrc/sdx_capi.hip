@@ -321,6 +321,38 @@ int scratch_for_current_device(hipStream_t s, void** out) {
 }  // namespace
 
 // ------------------------------------------------------------------ verify
+static size_t verify_split_bytes(int dtype, int64_t rows, int64_t ntgt, int64_t vocab) {
+  if (dtype != SDX_BF16) return 0;
+  const size_t a = sdx::rowstream_split_bytes(rows, vocab), b = sdx::rowstream_split_bytes(ntgt, vocab);
+  return a > b ? a : b;
+}
+
+// Byte offsets of the row statistics and tables in a draft-step workspace (the
+// carve of sdx_draft_step: header, then RowStat[batch], then tables).
+static void draft_ws_offsets(int64_t batch, size_t* st_off, size_t* tb_off) {
+  Carve c{nullptr};
+  c.take<uint8_t>(sdx::kWsHeaderBytes);
+  *st_off = c.used;
+  c.take<sdx::RowStat>(batch);
+  *tb_off = c.used;
+}
+
+static size_t draft_ws_x_offset(int64_t batch, int64_t vocab, int dtype);
+
+// The signature a bf16 draft step leaves in its workspace header (the words its
+// epilogue writes): the verify that takes its statistics over compares it.
+static void draft_sig(int64_t batch, int64_t vocab, float T, float top_p, int32_t top_k,
+                      uint32_t* sig) {
+  const Switches sw = switches(T, top_p, top_k, vocab);
+  const float tp = sw.use_p ? top_p : 1.0f;
+  const int32_t tk = sw.use_k ? top_k : 0;
+  uint32_t tb, pb;
+  memcpy(&tb, &T, 4);
+  memcpy(&pb, &tp, 4);
+  sig[0] = sdx::kDraftSig; sig[1] = (uint32_t)batch; sig[2] = (uint32_t)vocab;
+  sig[3] = tb; sig[4] = pb; sig[5] = (uint32_t)tk;
+}
+
 // verify workspace for ntgt target and ndrf draft rows (per-row k adds the
 // target row map and the bad-row bytes)
 static size_t verify_ws_bytes(int64_t batch, int64_t ntgt, int64_t ndrf, int64_t vocab, int dtype,
@@ -332,8 +364,9 @@ static size_t verify_ws_bytes(int64_t batch, int64_t ntgt, int64_t ndrf, int64_t
   c.take<uint8_t>(sdx::kWsHeaderBytes);  // magic word + split-row counters, fixed offsets
   transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jb, &rc, &ct, &ra);
   c.take<int64_t>(ntgt);  // greedy argmax
-  // part histograms of rows split over blocks
-  c.take<uint8_t>(dtype == SDX_BF16 ? sdx::rowstream_split_bytes(rows, vocab) : 0);
+  // part histograms of rows split over blocks (all rows, or the target rows alone
+  // when the draft rows' statistics come from the draft steps)
+  c.take<uint8_t>(verify_split_bytes(dtype, rows, ntgt, vocab));
   if (ragged) {
     c.take<int64_t>(ntgt);
     c.take<uint8_t>(batch);
@@ -370,7 +403,7 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
                        float temperature, float top_p, int32_t top_k, int64_t* n_acc, int64_t* y,
                        uint8_t* flags, void* workspace, size_t workspace_bytes,
                        sdx_stream_t stream, bool stats_only, const int64_t* cu_k = nullptr,
-                       int64_t target_rows = 0);
+                       int64_t target_rows = 0, const void* const* draft_ws = nullptr);
 
 int sdx_verify(const void* target_logits, const void* draft_logits, int dtype, int64_t batch,
                int32_t k, int64_t vocab, const int64_t* draft_ids, const float* u_accept,
@@ -381,6 +414,25 @@ int sdx_verify(const void* target_logits, const void* draft_logits, int dtype, i
   return verify_impl(target_logits, draft_logits, dtype, batch, k, vocab, draft_ids, u_accept,
                      u_final, active, temperature, top_p, top_k, n_acc, y, flags, workspace,
                      workspace_bytes, stream, false);
+}
+
+int sdx_verify_drafted(const void* target_logits, const void* draft_logits, int dtype,
+                       int64_t batch, int32_t k, int64_t vocab, const int64_t* draft_ids,
+                       const float* u_accept, const float* u_final, const uint8_t* active,
+                       float temperature, float top_p, int32_t top_k,
+                       const void* const* draft_workspaces, int64_t* n_acc, int64_t* y,
+                       uint8_t* flags, void* workspace, size_t workspace_bytes,
+                       sdx_stream_t stream) {
+  if (!n_acc || !y || !flags || !draft_workspaces || k < 1)
+    return fail(SDX_EINVAL, "sdx_verify_drafted: bad arguments");
+  const bool takes_stats = dtype == SDX_BF16 && temperature > 0.0f && k <= sdx::kMaxDraftK;
+  if (takes_stats)
+    for (int i = 0; i < k; ++i)
+      if (!draft_workspaces[i]) return fail(SDX_EINVAL, "sdx_verify_drafted: null draft workspace");
+  return verify_impl(target_logits, draft_logits, dtype, batch, k, vocab, draft_ids, u_accept,
+                     u_final, active, temperature, top_p, top_k, n_acc, y, flags, workspace,
+                     workspace_bytes, stream, false, nullptr, 0,
+                     takes_stats ? draft_workspaces : nullptr);
 }
 
 int sdx_verify_ragged(const void* target_logits, const void* draft_logits, int dtype,
@@ -417,7 +469,7 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
                        float temperature, float top_p, int32_t top_k, int64_t* n_acc, int64_t* y,
                        uint8_t* flags, void* workspace, size_t workspace_bytes,
                        sdx_stream_t stream, bool stats_only, const int64_t* cu_k,
-                       int64_t target_rows) {
+                       int64_t target_rows, const void* const* draft_ws) {
   if (!target_logits || (!draft_ids && !stats_only) || !u_accept || !u_final || batch < 0 ||
       k < 1 || !dtype_ok(dtype))
     return fail(SDX_EINVAL, "sdx_verify: bad arguments");
@@ -439,7 +491,7 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
   uint32_t* header = c.take<uint32_t>(sdx::kWsHeaderBytes / 4);
   transform_ws(c, rows, vocab, dtype, batch, &st, &tb, &dn, &jobs, &recs, &counters, &rank_acc);
   int64_t* am = c.take<int64_t>(ntgt);
-  const size_t split_bytes = dtype == SDX_BF16 ? sdx::rowstream_split_bytes(rows, vocab) : 0;
+  const size_t split_bytes = verify_split_bytes(dtype, rows, ntgt, vocab);
   uint8_t* split_ws = c.take<uint8_t>(split_bytes);
   int64_t* tgt_idx = nullptr;
   uint8_t* bad = nullptr;
@@ -496,8 +548,25 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
     a.split_ws = split_ws;
     a.split_bytes = split_bytes;
     a.ws_header = header;
-    if (dtype == SDX_BF16 && !stats_only && 2 * (int64_t)k + 1 <= 64 &&
-        batch <= sdx::kWsFusedMaxJobs && fused_enabled()) {
+    int64_t stream_rows = rows;
+    if (draft_ws) {
+      // the draft rows' statistics from the draft steps' workspaces: only the
+      // target rows stream, then the draw of the two-launch form. (The fused
+      // kernel with target rows alone was measured slower: at 320 rows its row
+      // workgroups stream one whole row each at the per-workgroup rate.)
+      sdx::DraftGatherArgs g = {};
+      for (int i = 0; i < k; ++i) g.ws[i] = (const uint8_t*)draft_ws[i];
+      g.k = k; g.B = batch; g.V = vocab;
+      draft_ws_offsets(batch, &g.st_off, &g.tb_off);
+      g.x_off = draft_ws_x_offset(batch, vocab, SDX_BF16);
+      g.stats = st; g.tables = tb; g.ntgt = ntgt;
+      g.dlog = (const uint16_t*)draft_logits; g.ld = vocab; g.ids = draft_ids;
+      draft_sig(batch, vocab, temperature, top_p, top_k, g.sig);
+      g.T = temperature;
+      if (int e = hip_status(sdx::launch_draft_gather(g, s), "draft_gather")) return e;
+      stream_rows = ntgt;
+    } else if (dtype == SDX_BF16 && !stats_only && 2 * (int64_t)k + 1 <= 64 &&
+               batch <= sdx::kWsFusedMaxJobs && fused_enabled()) {
       // one launch: the draw of each batch row starts as soon as its rows are in.
       // Its counters sit at fixed header offsets (every call leaves them at zero),
       // so a workspace reused across shapes never hands it stale counts. Per-row
@@ -513,7 +582,7 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
                                         sdx::fused_job_words(header), y, s, rowjob),
           "verify_fused_bf16");
     }
-    if (int e = row_stats16(dtype, a, rows, s)) return e;
+    if (int e = row_stats16(dtype, a, stream_rows, s)) return e;
     // bf16: drafted tokens the row kernel could not rank (a tie group of several
     // values) are ranked by the draw's accept chain; the statistics-only call
     // (and drafts too long for the one-wave chain) complete them with the rank kernel
@@ -555,7 +624,11 @@ int sdx_verify_counter_layout(int64_t batch, int64_t target_rows, int32_t k, int
     return (int64_t)header_at + (int64_t)((const uint8_t*)p - (const uint8_t*)h);
   };
   int n = 0;
-  const int64_t nsplit = dtype == SDX_BF16 ? sdx::rowstream_split_rows(rows, vocab, cus) : 0;
+  int64_t nsplit = dtype == SDX_BF16 ? sdx::rowstream_split_rows(rows, vocab, cus) : 0;
+  if (dtype == SDX_BF16 && !ragged) {  // sdx_verify_drafted streams the target rows alone
+    const int64_t n2 = sdx::rowstream_split_rows(ntgt, vocab, cus);
+    nsplit = n2 > nsplit ? n2 : nsplit;
+  }
   ranges[2 * n] = off(sdx::split_counter_words(h));
   ranges[2 * n + 1] = off(sdx::split_counter_words(h) + nsplit);
   ++n;
@@ -633,7 +706,13 @@ static size_t draft_ws_bytes(int64_t batch, int64_t vocab, int dtype) {
   c.take<uint8_t>(sdx::kWsHeaderBytes);
   transform_ws(c, batch, vocab, dtype, batch, &st, &tb, &dn, &jb, &rc, &ct);
   c.take<uint8_t>(dtype == SDX_BF16 ? sdx::rowstream_split_bytes(batch, vocab) : 0);
+  c.take<int64_t>(batch);  // the drawn ids, kept for sdx_verify_drafted
   return c.used;
+}
+
+// Byte offset of the drawn ids in a draft-step workspace (its last piece).
+static size_t draft_ws_x_offset(int64_t batch, int64_t vocab, int dtype) {
+  return draft_ws_bytes(batch, vocab, dtype) - align256((size_t)batch * sizeof(int64_t));
 }
 
 size_t sdx_draft_step_workspace(int64_t batch, int64_t vocab, int dtype) {
@@ -674,10 +753,10 @@ int sdx_draft_step(const void* logits, int dtype, int64_t batch, int64_t vocab, 
     e.greedy = true;
     return hip_status(sdx::launch_draft_epilogue(e, s), "draft_epilogue");
   }
-  hipLaunchKernelGGL(sdx_jobs_from_u, dim3((unsigned)((batch + 255) / 256)), dim3(256), 0, s, jobs,
-                     u, batch, (int64_t)-1, counters);
-  if (int r = hip_status(hipGetLastError(), "jobs")) return r;
   if (dtype == SDX_F32) {
+    hipLaunchKernelGGL(sdx_jobs_from_u, dim3((unsigned)((batch + 255) / 256)), dim3(256), 0, s,
+                       jobs, u, batch, (int64_t)-1, counters);
+    if (int r = hip_status(hipGetLastError(), "jobs")) return r;
     sdx::F32Args a = {};
     a.base[0] = (const float*)logits; a.nrows[0] = batch; a.ld[0] = ld;
     a.base[1] = a.base[0]; a.nrows[1] = 0; a.ld[1] = ld;
@@ -706,17 +785,45 @@ int sdx_draft_step(const void* logits, int dtype, int64_t batch, int64_t vocab, 
   a.use_p = sw.use_p; a.use_k = sw.use_k; a.greedy = 0;
   a.stats = st; a.tables = tb;
   a.split_ws = split_ws; a.split_bytes = split_bytes; a.ws_header = header;
-  if (int r = row_stats16(dtype, a, batch, s)) return r;
   sdx::RowSource16 src{(const uint16_t*)logits, ld, (const uint16_t*)logits, ld, batch, true};
-  if (int r = hip_status(sdx::launch_draw_rows16(dtype, src, st, tb, temperature, jobs, batch,
-                                                 vocab, recs, counters, x, s),
-                         "draw_rows16"))
-    return r;
+  if (dtype == SDX_BF16 && batch <= sdx::kWsFusedMaxJobs && fused_enabled()) {
+    // one launch: the fused verify at k = 0 (one row per batch row, no accept
+    // test: its bonus draw from the row is the draft's draw on u), whose row
+    // counters sit in the workspace header like the verify's
+    sdx::AcceptArgs aa{st,      batch,   0,       u,       u,       nullptr, jobs,
+                       nullptr, nullptr, nullptr, nullptr, nullptr, batch};
+    if (int r = hip_status(sdx::launch_verify_fused_bf16(a, batch, src, aa, batch, vocab,
+                                                         temperature, recs,
+                                                         sdx::fused_draw_words(header),
+                                                         sdx::fused_job_words(header), x, s,
+                                                         nullptr),
+                           "draft_fused_bf16"))
+      return r;
+  } else {
+    if (int r = row_stats16(dtype, a, batch, s)) return r;
+    hipLaunchKernelGGL(sdx_jobs_from_u, dim3((unsigned)((batch + 255) / 256)), dim3(256), 0, s,
+                       jobs, u, batch, (int64_t)-1, counters);
+    if (int r = hip_status(hipGetLastError(), "jobs")) return r;
+    if (int r = hip_status(sdx::launch_draw_rows16(dtype, src, st, tb, temperature, jobs, batch,
+                                                   vocab, recs, counters, x, s),
+                           "draw_rows16"))
+      return r;
+  }
   e.fmt = dtype;
   e.codes = (const uint16_t*)logits;
   e.ld = ld;
   e.stats = st;
   e.tables = tb;
+  if (dtype == SDX_BF16) {  // what sdx_verify_drafted checks before it takes these statistics
+    e.xcopy = (int64_t*)((uint8_t*)workspace + draft_ws_x_offset(batch, vocab, dtype));
+    uint32_t sig[sdx::kDraftSigWords];
+    draft_sig(batch, vocab, temperature, top_p, top_k, sig);
+    float tp;
+    memcpy(&tp, &sig[4], 4);
+    e.sig = header + sdx::kWsDraftSigWord;
+    e.top_p = tp;
+    e.top_k = (int32_t)sig[5];
+  }
   return hip_status(sdx::launch_draft_epilogue(e, s), "draft_epilogue");
 }
 

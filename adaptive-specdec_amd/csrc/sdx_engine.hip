@@ -46,6 +46,13 @@ __global__ void __launch_bounds__(256) draft_epilogue_kernel(DraftEpiArgs a) {
     }
     if (a.qx) a.qx[b] = p;
     if (a.conf) a.conf[b] = a.conf[b] * p;
+    if (a.xcopy) a.xcopy[b] = x;
+  }
+  if (a.sig && threadIdx.x == 0) {
+    const uint32_t w[kDraftSigWords] = {kDraftSig, (uint32_t)a.B, (uint32_t)a.V,
+                                        __float_as_uint(a.T), __float_as_uint(a.top_p),
+                                        (uint32_t)a.top_k};
+    for (int i = 0; i < kDraftSigWords; ++i) a.sig[i] = w[i];
   }
   if (!a.stop) return;
   __threadfence_block();
@@ -63,6 +70,68 @@ __global__ void __launch_bounds__(256) draft_epilogue_kernel(DraftEpiArgs a) {
 
 hipError_t launch_draft_epilogue(const DraftEpiArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(draft_epilogue_kernel, dim3(1), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- draft statistics gather
+// Block (b, i): row b of draft step i. Its RowStat and table move to draft row
+// ntgt + b k + i of the verify workspace; pgather and the tie flags are those the
+// row kernel gives a drafted token x = ids[b k + i]: 0 below the cut; a member of
+// a partially kept boundary group carries the group value when x is the id the
+// draft step drew (a drawn id is kept), else it is ranked by the verify's accept
+// chain (kRowRank); any other kept token gets its table (or exp) value.
+__global__ void __launch_bounds__(256) draft_gather_kernel(DraftGatherArgs a) {
+  const int64_t b = blockIdx.x;
+  const int i = (int)blockIdx.y;
+  const uint8_t* ws = a.ws[i];
+  const uint32_t* sig = reinterpret_cast<const uint32_t*>(ws) + kWsDraftSigWord;
+  bool ok = true;
+  for (int w = 0; w < kDraftSigWords; ++w) ok = ok && sig[w] == a.sig[w];
+  const int64_t row = a.ntgt + b * a.k + i;
+  RowStat* dst = a.stats + row;
+  float* dtb = a.tables + row * kTbl;
+  if (!ok) {
+    if (threadIdx.x == 0) {
+      RowStat st = {};
+      st.flags = kRowBadWs | kRowUnsupported;
+      st.zf = 1.0f; st.totf = 1.0f; st.klo = 0x7FFFFFFF; st.glo = 1; st.ghi = 0; st.argmax = -1;
+      *dst = st;
+    }
+    return;
+  }
+  const RowStat* sst = reinterpret_cast<const RowStat*>(ws + a.st_off) + b;
+  const float* stb = reinterpret_cast<const float*>(ws + a.tb_off) + b * kTbl;
+  RowStat st = *sst;
+  for (int t = threadIdx.x; t < st.ntbl; t += blockDim.x) dtb[t] = stb[t];
+  if (threadIdx.x != 0) return;
+  const int64_t x = a.ids[b * a.k + i];
+  float pg = 0.0f;
+  st.flags &= ~(kRowRank | kRowGatherTie);
+  if (x >= 0 && x < a.V) {
+    const uint32_t code = a.dlog[(b * a.k + i) * a.ld + x];
+    const int32_t key = (int32_t)key_of_code16(code);
+    if (key >= st.klo) {
+      if (key >= st.glo && key <= st.ghi) {
+        const int64_t drawn = *(reinterpret_cast<const int64_t*>(ws + a.x_off) + b);
+        if (st.rstar >= st.gcount) {
+          pg = val16<SDX_BF16>(st, stb, code, a.T);
+        } else if (st.rstar > 0) {  // partial group: kept if drawn, else ranked by the chain
+          st.flags |= kRowGatherTie;
+          if (x == drawn) pg = val16<SDX_BF16>(st, stb, code, a.T);
+          else st.flags |= kRowRank;
+        }
+      } else {
+        pg = val16<SDX_BF16>(st, stb, code, a.T);
+      }
+    }
+  }
+  st.pgather = pg;
+  *dst = st;
+}
+
+hipError_t launch_draft_gather(const DraftGatherArgs& a, hipStream_t s) {
+  if (a.k < 1 || a.k > kMaxDraftK || a.B < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(draft_gather_kernel, dim3((unsigned)a.B, (unsigned)a.k), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

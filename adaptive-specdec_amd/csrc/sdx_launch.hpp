@@ -169,6 +169,8 @@ struct RowSource16;
 struct ChunkRec;
 // per-row k (acc.cu_k): `rowjob` gives each row its batch row (-1: none) and
 // rs.jm_order the rows' batch-row order, both from launch_ragged_rows
+// k = 0 (no draft rows): each batch row's one row gets the bonus draw, the draft
+// step's draw.
 hipError_t launch_verify_fused_bf16(const RowStatArgs& rs, int64_t rows, const RowSource16& src,
                                     const AcceptArgs& acc, int64_t njobs, int64_t V, float T,
                                     ChunkRec* recs, uint32_t* counters, uint32_t* job_cnt,
@@ -270,6 +272,13 @@ hipError_t launch_draw_rows16(int fmt, const RowSource16& src, const RowStat* st
                               int64_t V, ChunkRec* recs, uint32_t* counters, int64_t* y,
                               hipStream_t s);
 // sdx_engine.hip: the device-side bookkeeping of a speculative round
+// A draft step leaves in its workspace header, at word kWsDraftSigWord, what its
+// statistics were computed with: kDraftSig, batch, vocab, temperature, top_p and
+// top_k (as 32-bit patterns). The verify that takes them over checks it.
+constexpr int kWsDraftSigWord = 3072;
+constexpr uint32_t kDraftSig = 0x44524654u;
+constexpr int kDraftSigWords = 6;
+constexpr int kMaxDraftK = 31;  // the fused verify's 2k + 1 <= 64
 struct DraftEpiArgs {
   int fmt;                 // SDX_BF16 / SDX_F16 (16-bit rows)
   bool greedy;             // temperature <= 0: the drafted token has probability 1
@@ -287,8 +296,32 @@ struct DraftEpiArgs {
   float tau;
   int32_t step, min_k;
   int32_t* stop;           // [1] or null
+  uint32_t* sig;           // the workspace's signature words (kWsDraftSigWord), or null
+  float top_p;
+  int32_t top_k;
+  int64_t* xcopy;          // [B] the drawn ids kept in the workspace, or null
 };
 hipError_t launch_draft_epilogue(const DraftEpiArgs& a, hipStream_t s);
+// The statistics of k draft steps (their workspaces ws[i]: RowStat[B] at st_off,
+// tables [B][kTbl] at tb_off) copied to the verify workspace's draft rows
+// (row ntgt + b k + i), with the drafted token's probability and tie flags set as
+// the row kernel sets them. A workspace whose signature does not match flags its
+// rows kRowBadWs (the verify then reports SDX_FLAG_WORKSPACE).
+struct DraftGatherArgs {
+  const uint8_t* ws[kMaxDraftK];
+  int32_t k;
+  int64_t B, V;
+  size_t st_off, tb_off, x_off;  // RowStat[B], tables [B][kTbl], the drawn ids [B]
+  RowStat* stats;
+  float* tables;
+  int64_t ntgt;
+  const uint16_t* dlog;    // draft logits, row b k + i at dlog + (b k + i) ld
+  int64_t ld;
+  const int64_t* ids;      // draft ids [B, k]
+  uint32_t sig[kDraftSigWords];
+  float T;
+};
+hipError_t launch_draft_gather(const DraftGatherArgs& a, hipStream_t s);
 struct RoundCommitArgs {
   int64_t B;
   int32_t k;               // drafts per row (uniform), or with cu_k the rows' own

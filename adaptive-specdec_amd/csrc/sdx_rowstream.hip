@@ -1322,10 +1322,10 @@ hipError_t launch_verify_fused_bf16(const RowStatArgs& rs, int64_t rows, const R
                                     ChunkRec* recs, uint32_t* counters, uint32_t* job_cnt,
                                     int64_t* y, hipStream_t s, const int32_t* rowjob) {
   const bool ragged = acc.cu_k != nullptr;
-  if (!src.vec || !y || !job_cnt || !rs.ws_header || V % 8 != 0 || rs.k < 1 ||
-      2 * rs.k + 1 > kWave ||
-      (ragged ? (!rowjob || !rs.jm_order || !acc.bad)
-              : rows != njobs * (2 * (int64_t)rs.k + 1)))
+  const int64_t per_job = 2 * (int64_t)rs.k + 1;
+  if (!src.vec || !y || !job_cnt || !rs.ws_header || V % 8 != 0 || rs.k < 0 ||
+      2 * rs.k + 1 > kWave || (rs.k == 0 && (ragged || rs.nrows[1] != 0)) ||
+      (ragged ? (!rowjob || !rs.jm_order || !acc.bad) : rows != njobs * per_job))
     return hipErrorInvalidValue;
   FusedArgs a = {};
   a.rs = rs;
@@ -1348,7 +1348,7 @@ hipError_t launch_verify_fused_bf16(const RowStatArgs& rs, int64_t rows, const R
   d.counters = counters;
   d.job_cnt = job_cnt;
   d.y = y;
-  a.need = (uint32_t)(2 * rs.k + 1);
+  a.need = (uint32_t)per_job;
   a.wait_ticks = fused_wait_ticks();
   const int64_t grid = a.nrow_pad + njobs * d.nblk;
   hipLaunchKernelGGL(verify_fused_bf16_kernel, dim3((unsigned)grid), dim3(SK_NT), 0, s, a);

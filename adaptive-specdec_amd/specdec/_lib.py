@@ -41,6 +41,8 @@ _SIGS = {
     "sdx_verify_ragged_workspace": (SZ, [I64, I64, I64, INT]),
     "sdx_verify_ragged": (INT, [P, P, INT, I64, I32, I64, I64, P, P, P, P, P, F, F, I32, P, P, P, P,
                                 SZ, P]),
+    "sdx_verify_drafted": (INT, [P, P, INT, I64, I32, I64, P, P, P, P, F, F, I32, P, P, P, P, P,
+                                 SZ, P]),
     "sdx_verify_counter_layout": (INT, [I64, I64, I32, I64, INT, I32, P, I32]),
     "sdx_verify_stats": (INT, [P, P, INT, I64, I32, I64, P, F, F, I32, P, SZ, P]),
     "sdx_verify_greedy_workspace": (SZ, [I64, I32]),

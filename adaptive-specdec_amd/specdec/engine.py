@@ -121,11 +121,15 @@ class SpecEngine:
         self.last_k = 0
         L = _lib.lib()
         dcode = _lib.dtype_code(self.dlog)
-        self.draft_ws = _lib.workspace(L.sdx_draft_step_workspace(B, V, dcode), dev)
+        # one workspace per draft position: each keeps its rows' statistics for the
+        # verify (`Verifier.drafted`), which then streams the target rows alone
+        self.draft_ws = [_lib.workspace(L.sdx_draft_step_workspace(B, V, dcode), dev)
+                         for _ in range(k)]
         self._verifiers = {}
         self._graphs = {}
         self.controller = controller
         self.rounds = 0
+        self._out_ok = bool(getattr(draft, "writes_out", False))
         # observed cost ratio for the controller (0: keep c), from event timings
         self.c_obs = torch.zeros(1, dtype=torch.float32, device=dev)
         self.observe_cost = bool(observe_cost) and controller is not None
@@ -168,7 +172,7 @@ class SpecEngine:
         tlog = self.target.prefill(prompt, self.tcache, plen)
         self.draft.prefill(prompt, self.dcache, plen)
         x, _, _ = draft_step(tlog.contiguous(), u_first, self.T, self.tp, self.tk,
-                             out=self.step_out[self.k], workspace=self.draft_ws)
+                             out=self.step_out[self.k], workspace=self.draft_ws[0])
         # a first token that could not be drawn (nonfinite prefill logits) raises
         # the round-commit error word, read at the next sync
         self.err[0:1].bitwise_or_((x < 0).any().view(1).to(torch.int32) * 2)
@@ -204,15 +208,16 @@ class SpecEngine:
         feed = self.pending.view(B, 1)
         k_eff = kr
         for i in range(kr):                                     # engine.py:246-258
-            logits = self.draft.forward(feed, self.dcache)
+            if self._out_ok:   # the draft writes its logits into dlog[:, i] itself
+                self.draft.forward(feed, self.dcache, out=self.dlog[:, i:i + 1])
+            else:
+                self.dlog[:, i].copy_(self.draft.forward(feed, self.dcache)[:, -1])
             self.dcache.commit(1)
-            last = logits[:, -1]
-            self.dlog[:, i].copy_(last)
-            x, _, stop = draft_step(last.contiguous(), self.u_draft[i], self.T, self.tp, self.tk,
+            x, _, stop = draft_step(self.dlog[:, i], self.u_draft[i], self.T, self.tp, self.tk,
                                     conf=self.conf if early else None,
                                     tau=self.tau if early else None, step=i + 1,
                                     min_k=self.min_k, out=self.step_out[i],
-                                    workspace=self.draft_ws)
+                                    workspace=self.draft_ws[i])
             self.xs[:, i].copy_(x)
             feed = x.view(B, 1)
             if early and i + 1 < kr and bool(stop.item()):     # controller.py:184-187
@@ -239,8 +244,10 @@ class SpecEngine:
             dlog = self.dlog[:, :k_eff].contiguous()
             ua = self.u_acc[:, :k_eff].contiguous()
         torch.sub(1, self.done, out=self.active)                # alive = ~done
-        n_acc, y, flags = self._verifier(k_eff)(tlog.contiguous(), dlog, xs, ua, self.u_fin,
-                                                self.active)    # engine.py:281-303
+        # engine.py:281-303, with q's statistics from this round's draft steps
+        n_acc, y, flags = self._verifier(k_eff).drafted(tlog.contiguous(), dlog, xs, ua,
+                                                        self.u_fin, self.draft_ws[:k_eff],
+                                                        self.active)
         rc = _lib.lib().sdx_round_commit(                       # engine.py:305-340
             B, k_eff, None, _lib.ptr(n_acc), _lib.ptr(y), _lib.ptr(xs), _lib.ptr(self.done),
             _lib.ptr(self.out), _lib.ptr(self.out_len), self.max_new, _lib.ptr(self.eos),

@@ -55,6 +55,9 @@ def _kernel_rows(x):
     mult = 4 if x.dtype == torch.float32 else 8
     if x.is_contiguous() and V % mult == 0 and x.data_ptr() % 16 == 0:
         return x, V
+    if (x.dim() == 2 and x.stride(1) == 1 and x.stride(0) >= V and x.stride(0) % mult == 0
+            and V % mult == 0 and x.data_ptr() % 16 == 0):
+        return x, x.stride(0)              # rows of a wider buffer, read in place
     ld = (V + mult - 1) // mult * mult
     buf = torch.empty((x.shape[0], ld), dtype=x.dtype, device=x.device)
     buf[:, :V].copy_(x)
@@ -328,6 +331,30 @@ class Verifier:
                                    _lib.ptr(self.n_acc), _lib.ptr(self.y), _lib.ptr(self.flags),
                                    _lib.ptr(self.ws), self.ws.numel(), st)
         _lib.check(rc, "Verifier")
+        return self.n_acc, self.y, self.flags
+
+    def drafted(self, target, draft, draft_ids, u_accept, u_final, draft_workspaces,
+                active=None):
+        """The same call as `__call__` for a round whose k draft rows went through
+        `draft_step`: draft_workspaces[i] is the workspace of the draft step that
+        drew draft_ids[:, i] from draft[:, i]. The draft rows' statistics are taken
+        from there instead of streaming draft again (bf16 at T > 0; other cases
+        verify as `__call__`). Same results as `__call__`."""
+        import ctypes
+        self._check(target, draft, draft_ids, u_accept, u_final)
+        if len(draft_workspaces) != self.k:
+            raise ValueError(f"need {self.k} draft workspaces, got {len(draft_workspaces)}")
+        if self.greedy:
+            return self(target, draft, draft_ids, u_accept, u_final, active)
+        act = None if active is None else active.to(torch.uint8)
+        arr = (ctypes.c_void_p * self.k)(*[w.data_ptr() for w in draft_workspaces])
+        rc = self.L.sdx_verify_drafted(_lib.ptr(target), _lib.ptr(draft), self.dt, self.B, self.k,
+                                       self.V, _lib.ptr(draft_ids), _lib.ptr(u_accept),
+                                       _lib.ptr(u_final), _lib.ptr(act), self.T, self.tp, self.tk,
+                                       ctypes.cast(arr, ctypes.c_void_p), _lib.ptr(self.n_acc),
+                                       _lib.ptr(self.y), _lib.ptr(self.flags), _lib.ptr(self.ws),
+                                       self.ws.numel(), _lib.stream_of(target))
+        _lib.check(rc, "Verifier.drafted")
         return self.n_acc, self.y, self.flags
 
     def reset_workspace(self):

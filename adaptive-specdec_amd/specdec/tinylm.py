@@ -33,6 +33,7 @@ class TinyLM:
         on most tokens. `scale` multiplies the logits."""
         self.V, self.hq, self.hkv, self.max_pos = int(vocab), int(hq), int(hkv), int(max_pos)
         self.dtype = torch.bfloat16  # of the logits
+        self.writes_out = True       # forward(..., out=) writes logits into a caller view
         self.D = self.hq * HEAD
         self.device = torch.device(device)
         g = torch.Generator(device="cpu").manual_seed(int(seed))
@@ -64,8 +65,9 @@ class TinyLM:
         c.block_table.copy_(torch.randperm(batch * mb, generator=g).to(torch.int32).view(batch, mb))
         return c
 
-    def forward(self, tokens, cache):
-        """tokens [B, q] int64 (q <= 64 // (hq / hkv)) -> logits [B, q, V] bf16."""
+    def forward(self, tokens, cache, out=None):
+        """tokens [B, q] int64 (q <= 64 // (hq / hkv)) -> logits [B, q, V] bf16,
+        written into `out` ([B, q, V], rows of unit stride) when given."""
         B, q = tokens.shape
         p = self.p
         pos = (cache.lengths.view(B, 1) + torch.arange(q, device=self.device).view(1, q))
@@ -91,8 +93,11 @@ class TinyLM:
         logits = []
         for j in range(q):
             hj = h[:, j] + torch.mm(att[:, j].contiguous(), p["wo"])
-            logits.append(torch.mm(hj.contiguous(), p["wlm"]))
-        return torch.stack(logits, 1)                                              # [B, q, V]
+            if out is not None:
+                torch.mm(hj.contiguous(), p["wlm"], out=out[:, j])
+            else:
+                logits.append(torch.mm(hj.contiguous(), p["wlm"]))
+        return out if out is not None else torch.stack(logits, 1)                  # [B, q, V]
 
     def prefill(self, prompt, cache, plen=None, chunk=16):
         """Right-padded prompt [B, P] with real lengths plen [B] (None: all P) ->

@@ -9,7 +9,8 @@ logits with a Zipf head, draft = target + N(0,1), draft ids drawn from q) are
 resident in HBM; three input sets (525 MB, more than the 256 MB MALL) rotate so
 no step reads another step's bytes from cache.
 
-    python bench.py [--steps K] [--warmup W] [--workload verify|greedy|kv|attn|ragged|probs]
+    python bench.py [--steps K] [--warmup W]
+                    [--workload verify|greedy|kv|attn|ragged|probs|draft|round]
 
 Prints one JSON line: verified tokens/s (sum over rows of n_acc + 1 per
 step), the roofline of the fused verify step (algorithmic bytes = every logit
@@ -516,13 +517,140 @@ def bench_attn(args, torch):
             "cpu_baseline": None}
 
 
+def bench_draft(args, torch):
+    """One draft step of the device round (engine.py:246-258 with the early exit of
+    controller.py:184-187): B=64 rows of V=151936 bf16 draft logits, T=0.8, top-p
+    0.95; to_probs statistics, the inverse-CDF draw, q(x), conf *= q(x) and the
+    early-exit flag, all on the device. HBM roofline: every logit read once."""
+    from specdec import _lib
+    from specdec.sampling import draft_step
+    from specdec.workloads import uniforms, zipf_logits
+    B, V, T, tp = 64, args.vocab, 0.8, 0.95
+    dev = "cuda:0"
+    g = torch.Generator(device=dev).manual_seed(3000)
+    xs = [zipf_logits(B, V, g, dev) for _ in range(args.sets)]
+    us = [uniforms((B,), g, dev) for _ in range(args.sets)]
+    confs = [torch.ones(B, dtype=torch.float32, device=dev) for _ in range(args.sets)]
+    outs = [(torch.empty(B, dtype=torch.int64, device=dev),
+             torch.empty(B, dtype=torch.float32, device=dev),
+             torch.zeros(1, dtype=torch.int32, device=dev)) for _ in range(args.sets)]
+    L = _lib.lib()
+    wss = [_lib.workspace(L.sdx_draft_step_workspace(B, V, _lib.BF16), dev)
+           for _ in range(args.sets)]
+
+    def call(i):
+        return draft_step(xs[i], us[i], T, tp, 0, conf=confs[i], tau=0.3, step=2, min_k=1,
+                          out=outs[i], workspace=wss[i])
+    for i in range(args.warmup):
+        call(i % args.sets)
+    torch.cuda.synchronize()
+    graphs = [capture(lambda i=i: call(i), torch) for i in range(args.sets)]
+    ms = timed_graphs(graphs, args.steps, torch)
+    alg = B * V * 2
+    ach = alg / (ms / 1e3) / 1e9
+    return {"metric": "draft steps/sec, B=64 V=151936 bf16 (to_probs + draw + q(x) + early exit)",
+            "value": round(1e3 / ms, 1), "unit": "draft steps/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic",
+            "config": {"workload": f"draft step B={B} V={V} bf16 T=0.8 top-p 0.95, conf + tau",
+                       "batch": B, "input_sets": args.sets, "hip_graph": True},
+            "roofline": {"bound": "hbm", "kernel": "whole draft step (all launches)",
+                         "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                         "algorithmic_bytes": int(alg), "avg_launch_us": round(ms * 1e3, 2)},
+            "cpu_baseline": None}
+
+
+def bench_round(args, torch):
+    """One speculative round of `SpecEngine` (engine.py:228-342) replayed from a HIP
+    graph: k=4 draft forwards of the stand-in TinyLM draft, each followed by the
+    fused draft step, the commit-only draft forward, one target forward over the
+    5 positions, the fused verify and the round commit. B=64, V=151936 bf16 logits,
+    T=0.8, top-p 0.95 (no checkpoints: seeded one-layer models whose lm_head dominates
+    the model time). The round's verify takes the draft rows' statistics from its
+    draft steps (`Verifier.drafted`). Reported beside the round: the sampling path
+    alone, the k draft steps, the verify as the round runs it and the verify that
+    streams the draft rows too, on the round's own logits, each replayed from its
+    own graph."""
+    from specdec.engine import SpecEngine
+    from specdec.tinylm import TinyLM
+    B, k, V, T, tp = 64, 4, args.vocab, 0.8, 0.95
+    dev = "cuda:0"
+    tgt = TinyLM(V, hq=2, hkv=1, seed=1, device=dev, scale=4.0)
+    drf = TinyLM(V, hq=2, hkv=1, seed=2, device=dev, base=tgt, noise=0.6)
+    P = 16
+    rounds_max = args.steps + args.warmup + 8
+    max_new = rounds_max * (k + 1) + 2
+    eng = SpecEngine(tgt, drf, B, k, temperature=T, top_p=tp, max_new=max_new, prompt_len=P,
+                     device=dev, observe_cost=False)
+    gen = torch.Generator(device="cpu").manual_seed(7)
+    prompt = torch.randint(0, V, (B, P), generator=gen).to(dev)
+    g = torch.Generator(device=dev).manual_seed(11)
+    eng.start(prompt, u_first=torch.rand(B, generator=g, device=dev))
+    torch.rand(eng.u_draft.shape, generator=g, device=dev, out=eng.u_draft)
+    torch.rand(eng.u_acc.shape, generator=g, device=dev, out=eng.u_acc)
+    torch.rand(eng.u_fin.shape, generator=g, device=dev, out=eng.u_fin)
+    tokens = []
+    for _ in range(max(args.warmup, 2)):           # eager rounds (the capture needs one)
+        n_acc, _ = eng.round(k)
+        tokens.append(int((n_acc + 1).sum().item()))
+    graph = eng.capture(k)
+    torch.cuda.synchronize()
+    ms = timed_graphs([graph], args.steps, torch)
+    torch.cuda.synchronize()
+    # the sampling path alone on the last round's logits: k draft steps, then the verify
+    from specdec.sampling import draft_step
+    dlog = eng.dlog.clone()
+    tlog = eng.last_target_logits.contiguous().clone()
+    xs, ua, uf = eng.xs.clone(), eng.u_acc.clone(), eng.u_fin.clone()
+    ud = eng.u_draft.clone()
+    conf = torch.ones(B, dtype=torch.float32, device=dev)
+    douts = [eng.step_out[i] for i in range(k)]
+    dws = eng.draft_ws
+
+    def steps():
+        for i in range(k):
+            draft_step(dlog[:, i], ud[i], T, tp, 0, out=douts[i], workspace=dws[i])
+    ver = eng._verifier(k)
+
+    def verify():
+        ver(tlog, dlog, xs, ua, uf)
+
+    def verify_drafted():
+        ver.drafted(tlog, dlog, xs, ua, uf, dws)
+    for _ in range(3):
+        steps()
+        verify()
+        verify_drafted()
+    gs, gv, gd = capture(steps, torch), capture(verify, torch), capture(verify_drafted, torch)
+    ms_steps = timed_graphs([gs], args.steps, torch)
+    ms_verify = timed_graphs([gv], args.steps, torch)
+    ms_drafted = timed_graphs([gd], args.steps, torch)
+    tok = sum(tokens) / len(tokens)
+    return {"metric": "speculative rounds/sec, TinyLM pair B=64 k=4 V=151936 (graph replay)",
+            "value": round(1e3 / ms, 2), "unit": "rounds/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded one-layer models, no checkpoint)",
+            "config": {"workload": f"SpecEngine round B={B} k={k} V={V} bf16 T=0.8 top-p 0.95",
+                       "batch": B, "k": k, "prompt_len": P, "hip_graph": True},
+            "tokens_per_round": round(tok, 2),
+            "tokens_per_s": round(tok / (ms / 1e3), 1),
+            "draft_steps_ms": round(ms_steps, 5), "verify_ms": round(ms_verify, 5),
+            "verify_drafted_ms": round(ms_drafted, 5),
+            "sampling_share": round((ms_steps + ms_drafted) / ms, 4),
+            "roofline": None, "cpu_baseline": None}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="verify",
-                    choices=["verify", "greedy", "kv", "attn", "ragged", "probs"])
+                    choices=["verify", "greedy", "kv", "attn", "ragged", "probs", "draft",
+                             "round"])
     ap.add_argument("--sets", type=int, default=3)
     ap.add_argument("--vocab", type=int, default=151936,
                     help="verify workload: vocabulary of the bf16 rows (151936: the headline)")
@@ -544,7 +672,8 @@ def main():
         print("bench.py: no ROCm device visible", file=sys.stderr)
         sys.exit(1)
     fn = {"verify": bench_verify, "greedy": bench_greedy, "kv": bench_kv,
-          "attn": bench_attn, "ragged": bench_ragged, "probs": bench_probs}[args.workload]
+          "attn": bench_attn, "ragged": bench_ragged, "probs": bench_probs,
+          "draft": bench_draft, "round": bench_round}[args.workload]
     result = fn(args, torch)
     if args.calibrate_copy:
         # a device-to-device copy of known size: its FETCH_SIZE / WRITE_SIZE per

@@ -155,6 +155,27 @@ int sdx_verify_noalloc(const void* target_logits, const void* draft_logits, int 
                        const uint8_t* active, float temperature, float top_p, int32_t top_k,
                        int64_t* n_acc, int64_t* y, uint8_t* flags, sdx_stream_t stream);
 
+/* sdx_verify for a round whose draft rows already went through sdx_draft_step:
+ * draft_workspaces (a host array of k device pointers) holds, for each draft
+ * position i, the workspace of the sdx_draft_step call that sampled draft_ids[:, i]
+ * from draft_logits[:, i] (batch rows, same vocab, temperature, top_p and top_k).
+ * The draft rows' to_probs statistics are taken from those workspaces instead of
+ * streaming draft_logits again: only the k + 1 target rows per batch row are read
+ * in full, plus the draft rows of the final residual draws (the row statistics
+ * then the draw, two launches). Outputs, rules and workspace as sdx_verify, and
+ * the same results as sdx_verify on the same inputs. A draft workspace whose
+ * statistics were made for another shape or sampling configuration flags its
+ * rows SDX_FLAG_WORKSPACE. Other dtypes, temperature <= 0 and k > 31 run
+ * sdx_verify and ignore the draft workspaces. No reference counterpart: the
+ * reference's verify recomputes q from the draft logits (engine.py:250,288). */
+int sdx_verify_drafted(const void* target_logits, const void* draft_logits, int dtype,
+                       int64_t batch, int32_t k, int64_t vocab, const int64_t* draft_ids,
+                       const float* u_accept, const float* u_final, const uint8_t* active,
+                       float temperature, float top_p, int32_t top_k,
+                       const void* const* draft_workspaces, int64_t* n_acc, int64_t* y,
+                       uint8_t* flags, void* workspace, size_t workspace_bytes,
+                       sdx_stream_t stream);
+
 /* Verify with a different k per batch row (config 5's adaptive k): row b drafts
  * k_b = cu_k[b+1] - cu_k[b] tokens, 0 <= k_b <= k_max (cu_k int64 [batch+1] on the
  * device, cu_k[0] = 0). Rows are packed: target_logits [target_rows, vocab] with
@@ -209,7 +230,9 @@ int sdx_verify_greedy(const void* target_logits, int dtype, int64_t batch, int32
 
 /* ---- one speculative round on the device: specdec/engine.py:228-342 ------- */
 
-/* One draft step (engine.py:246-258 with the early exit of controller.py:184-187):
+/* One draft step (engine.py:246-258 with the early exit of controller.py:184-187).
+ * Its workspace keeps the rows' statistics until the next call on it, for
+ * sdx_verify_drafted:
  * q = to_probs(logits[b]) (sampling.py:34-67); x[b] = the inverse-CDF draw from q on
  * u[b] (the rule of sdx_sample_probs; temperature <= 0: the first argmax, u unused);
  * qx[b] = q(x[b]) (nullable); conf[b] *= qx[b] (nullable, the running product of
