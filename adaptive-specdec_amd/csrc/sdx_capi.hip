@@ -373,7 +373,7 @@ static size_t verify_ws_bytes(int64_t batch, int64_t ntgt, int64_t ndrf, int64_t
     c.take<int32_t>(rows);  // the rows in batch-row order (fused kernel)
     c.take<int32_t>(rows);  // each row's batch row
   }
-  if (dtype == SDX_F32) c.take<uint32_t>((size_t)rows * sdx::kF32TieWords);  // tie-group bits
+  if (dtype == SDX_F32) c.take<uint32_t>((size_t)rows * sdx::f32_tie_words(vocab));  // tie bits
   return c.used;
 }
 
@@ -508,7 +508,7 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
       return e;
   }
   uint32_t* tie_bits =
-      dtype == SDX_F32 ? c.take<uint32_t>((size_t)rows * sdx::kF32TieWords) : nullptr;
+      dtype == SDX_F32 ? c.take<uint32_t>((size_t)rows * sdx::f32_tie_words(vocab)) : nullptr;
 
   if (sw.greedy) {
     // one-hot p: only the target argmax matters (see sdx_verify_greedy)
@@ -531,6 +531,7 @@ static int verify_impl(const void* target_logits, const void* draft_logits, int 
     a.out = dn; a.ld_out = vocab; a.stats = st;
     a.zero = counters; a.nzero = batch;
     a.tie_bits = tie_bits;
+    a.tie_ld = sdx::f32_tie_words(vocab);
     if (int e = hip_status(sdx::launch_to_probs_f32(a, rows, s), "to_probs_f32")) return e;
   } else {
     if (!aligned16(target_logits) || !aligned16(draft_logits) || (vocab % 8) != 0)

@@ -1,5 +1,6 @@
-// to_probs for fp32 logits (specdec/sampling.py:34-67), vocabularies up to
-// 8192: the literal algorithm on one 1024-thread workgroup per row.
+// to_probs for fp32 logits (specdec/sampling.py:34-67): vocabularies up to 8192
+// with the literal algorithm on one 1024-thread workgroup per row; larger ones
+// with the multi-pass kernel below, which sorts only the nucleus boundary region.
 //
 // fp32 logits are not limited to 65,536 distinct values, so the histogram
 // of the 16-bit path does not apply. The row is small enough to sort in LDS:
@@ -77,7 +78,7 @@ __global__ void __launch_bounds__(F32_NT) to_probs_f32_kernel(F32Args a) {
     const int64_t am = (int64_t)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFu));
     for (int i = tid; i < V; i += F32_NT) o[i] = i == am ? 1.0f : 0.0f;
     if (a.tie_bits)  // no tie groups in a one-hot row
-      for (int i = tid; i < (int)kF32TieWords; i += F32_NT) a.tie_bits[row * kF32TieWords + i] = 0u;
+      for (int i = tid; i < (int)a.tie_ld; i += F32_NT) a.tie_bits[row * a.tie_ld + i] = 0u;
     if (tid == 0 && a.stats) {
       RowStat st = {};
       st.flags = kRowGreedy | kRowProbs;
@@ -233,7 +234,7 @@ __global__ void __launch_bounds__(F32_NT) to_probs_f32_kernel(F32Args a) {
       if (mem && i == gid) gtie = true;
       const uint64_t bm = __ballot(mem);
       if (a.tie_bits && lane == 0) {  // ids t*F32_NT + 64*wv + [0, 64): two words
-        uint32_t* dst = a.tie_bits + row * kF32TieWords + ((t * F32_NT + wv * kWave) >> 5);
+        uint32_t* dst = a.tie_bits + row * a.tie_ld + ((t * F32_NT + wv * kWave) >> 5);
         dst[0] = (uint32_t)bm;
         dst[1] = (uint32_t)(bm >> 32);
       }
@@ -269,8 +270,540 @@ __global__ void __launch_bounds__(F32_NT) to_probs_f32_kernel(F32Args a) {
   }
 }
 
+// ---------------------------------------------------------------- large vocabularies
+// The same rule for rows longer than the LDS sort holds, in passes over the row
+// by one 1024-thread workgroup. p is non-decreasing in s, so the reference's
+// order (p descending, id ascending) visits the values of s in descending key
+// order, ids ascending within each tie group of equal p:
+//  1. m = max s (s = fl32(x / T)) and, per bucket of the top 12 bits of key(s),
+//     the element count and the smallest and largest key present;
+//  2. the exact normaliser Z (128-bit fixed point); with top-k, the k-th largest
+//     key from the bucket counts and the distinct keys of its bucket;
+//  3. per bucket the fixed-point mass of the top-k-zeroed p. The keep test
+//     `cum - p < top_p` fails first inside the first bucket whose last element
+//     fails it (cum: the buckets above plus its own mass; p: that of its smallest
+//     key). That bucket, widened while a neighbouring bucket holds the same p at
+//     the shared edge (so no tie group straddles the region's edge), is the
+//     region;
+//  4. the region's distinct probabilities with their counts (an LDS hash table:
+//     one entry per tie group), sorted descending and walked with the exact
+//     prefix of the buckets above: the first group whose last element fails is
+//     the boundary group, and a 64-way search gives its members kept, lowest ids
+//     first;
+//  5. the output (p / totf where kept, 0 elsewhere; group members ranked by id
+//     with one block scan per 1024 ids), the tie-group bits and the statistics.
+// A region with more than FB_KEYS distinct probabilities marks the row
+// unsupported and writes NaN probabilities. (The top-k bucket is read the same
+// way: the k-th largest p is the group where the bucket's counts reach k.)
+constexpr int FB_NT = 1024;
+constexpr int FB_NB = 4096;
+constexpr int FB_SHIFT = 20;  // bucket = key >> 20
+constexpr int FB_TAB = 8192;  // hash slots for distinct keys
+constexpr int FB_KEYS = 7168; // distinct probabilities a region may hold (87.5% of the slots)
+constexpr int FB_NW = FB_NT / kWave;
+constexpr int FB_PER = FB_TAB / FB_NT;  // sorted entries per thread
+
+struct FbLds {
+  uint32_t cnt[FB_NB];
+  uint32_t kmin[FB_NB];
+  uint32_t kmax[FB_NB];
+  uint64_t mass[FB_NB];
+  uint64_t ent[FB_TAB];  // hash table (key word, count word), then sorted (~key << 32 | count)
+  uint64_t red[2 * FB_NW];
+  uint32_t ndist;
+  int32_t i32[8];
+  float f32[8];
+  uint64_t u64[4];
+};
+
+__device__ __forceinline__ float fb_of_key(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+__device__ __forceinline__ float fb_pmask(float p, bool use_k, float kth) {
+  return (use_k && p < kth) ? 0.0f : p;
+}
+__device__ uint64_t fb_sum_u64(uint64_t v, FbLds& L) {
+  v = wave_sum_u64(v);
+  __syncthreads();
+  if ((threadIdx.x & (kWave - 1)) == 0) L.red[threadIdx.x / kWave] = v;
+  __syncthreads();
+  uint64_t t = 0;
+  for (int i = 0; i < FB_NW; ++i) t += L.red[i];
+  return t;
+}
+__device__ uint32_t blk_min_u32_fb(int v, FbLds& L) {
+  uint32_t x = (uint32_t)v;
+  x = ~wave_max_u32(~x);
+  __syncthreads();
+  if ((threadIdx.x & (kWave - 1)) == 0) L.red[threadIdx.x / kWave] = x;
+  __syncthreads();
+  uint32_t t = 0xFFFFFFFFu;
+  for (int i = 0; i < FB_NW; ++i) t = min(t, (uint32_t)L.red[i]);
+  return t;
+}
+// Inclusive block scan (u64), one value per thread.
+__device__ uint64_t fb_scan_u64(uint64_t v, FbLds& L, uint64_t* total) {
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  const uint64_t incl = wave_incl_scan_u64(v, lane);
+  __syncthreads();
+  if (lane == kWave - 1) L.red[w] = incl;
+  __syncthreads();
+  uint64_t off = 0, tot = 0;
+  for (int i = 0; i < FB_NW; ++i) {
+    off += i < w ? L.red[i] : 0ull;
+    tot += L.red[i];
+  }
+  *total = tot;
+  return off + incl;
+}
+// The distinct probabilities of the row's elements in buckets [bd, bu] (with
+// top-k zeroing when mask_k) and their counts, sorted descending as
+// ent[i] = (~bits(p) << 32) | count (empty slots, ~0, last): each entry is one
+// tie group of the reference's order. Returns their number, or -1 when more than
+// FB_KEYS.
+__device__ int fb_distinct_p(FbLds& L, const float* __restrict__ x, int64_t V, float T, int bd,
+                             int bu, float m, float zf, bool mask_k, float kth) {
+  uint32_t* const hk = reinterpret_cast<uint32_t*>(L.ent);
+  uint32_t* const hc = hk + FB_TAB;
+  for (int i = threadIdx.x; i < FB_TAB; i += FB_NT) { hk[i] = 0u; hc[i] = 0u; }  // 0: empty
+  if (threadIdx.x == 0) L.ndist = 0u;
+  __syncthreads();
+  for (int64_t i = threadIdx.x; i < V; i += FB_NT) {
+    const float sv = x[i] / T;
+    const int b = (int)(key_of_f32(sv) >> FB_SHIFT);
+    if (b < bd || b > bu) continue;
+    const uint32_t k = __float_as_uint(fb_pmask(exp_det(sv - m) / zf, mask_k, kth)) + 1u;
+    uint32_t h = (k * 0x9E3779B1u) >> 19;  // 13 bits
+    for (int probe = 0; probe < FB_TAB; ++probe) {
+      const uint32_t old = atomicCAS(&hk[h], 0u, k);
+      if (old == 0u || old == k) {
+        if (old == 0u) atomicAdd(&L.ndist, 1u);
+        atomicAdd(&hc[h], 1u);
+        break;
+      }
+      h = (h + 1) & (FB_TAB - 1);
+    }
+  }
+  __syncthreads();
+  const int nd = (int)L.ndist;
+  uint64_t e[FB_PER];
+#pragma unroll
+  for (int t = 0; t < FB_PER; ++t) {
+    const int i = threadIdx.x + t * FB_NT;
+    e[t] = hk[i] ? (((uint64_t)(~(hk[i] - 1u)) << 32) | hc[i]) : ~0ull;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < FB_PER; ++t) L.ent[threadIdx.x + t * FB_NT] = e[t];
+  __syncthreads();
+  if (nd > FB_KEYS) return -1;
+  for (int size = 2; size <= FB_TAB; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < FB_TAB; i += FB_NT) {
+        const int jx = i ^ stride;
+        if (jx > i) {
+          const bool up = (i & size) == 0;
+          const uint64_t ai = L.ent[i], aj = L.ent[jx];
+          if ((ai > aj) == up) { L.ent[i] = aj; L.ent[jx] = ai; }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  return nd;
+}
+__device__ __forceinline__ float fb_ent_p(uint64_t e) { return __uint_as_float(~(uint32_t)(e >> 32)); }
+
+__global__ void __launch_bounds__(FB_NT) to_probs_f32_big_kernel(F32Args a) {
+  __shared__ FbLds L;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
+  const int64_t row = blockIdx.x;
+  if (tid == 0 && row < a.nzero) a.zero[row] = 0u;
+  const int g = row < a.nrows[0] ? 0 : 1;
+  const int64_t r = g ? row - a.nrows[0] : row;
+  const float* __restrict__ x = a.base[g] + r * a.ld[g];
+  const int64_t V = a.V;
+  const int64_t gid = draft_id_of_row(a.ids, a.tgt_idx, a.k, a.nrows[1], g, r);
+  float* o = a.out + row * a.ld_out;
+  uint32_t* bits = a.tie_bits ? a.tie_bits + row * a.tie_ld : nullptr;
+
+  // ---- greedy: one-hot at the first maximum (-0 == +0)
+  if (a.greedy) {
+    uint64_t best = 0;
+    for (int64_t i = tid; i < V; i += FB_NT) {
+      uint32_t k = key_of_f32(x[i]);
+      if (k == 0x7FFFFFFFu) k = 0x80000000u;
+      const uint64_t c = ((uint64_t)k << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i);
+      best = c > best ? c : best;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const uint64_t w = (uint64_t)__shfl_xor((long long)best, off, kWave);
+      best = w > best ? w : best;
+    }
+    if (lane == 0) L.red[wv] = best;
+    __syncthreads();
+    uint64_t b = 0;
+    for (int w = 0; w < FB_NW; ++w) b = L.red[w] > b ? L.red[w] : b;
+    const int64_t am = (int64_t)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFu));
+    for (int64_t i = tid; i < V; i += FB_NT) o[i] = i == am ? 1.0f : 0.0f;
+    if (bits)
+      for (int64_t i = tid; i < a.tie_ld; i += FB_NT) bits[i] = 0u;
+    if (tid == 0 && a.stats) {
+      RowStat st = {};
+      st.flags = kRowGreedy | kRowProbs;
+      st.argmax = am;
+      st.zf = 1.0f; st.totf = 1.0f; st.glo = 1; st.ghi = 0;
+      st.pgather = gid >= 0 ? (gid == am ? 1.0f : 0.0f) : 0.0f;
+      a.stats[row] = st;
+    }
+    return;
+  }
+  const float T = a.T;
+  const bool use_k = a.use_k, use_p = a.use_p;
+
+  // ---- 1. m, bucket counts and key extremes
+  for (int b = tid; b < FB_NB; b += FB_NT) {
+    L.cnt[b] = 0u; L.kmin[b] = 0xFFFFFFFFu; L.kmax[b] = 0u; L.mass[b] = 0ull;
+  }
+  if (tid == 0) { L.i32[0] = 0; L.f32[2] = 0.0f; }
+  __syncthreads();
+  float mx = -INFINITY;
+  for (int64_t i = tid; i < V; i += FB_NT) {
+    const float sv = x[i] / T;
+    mx = fmaxf(mx, sv);
+    const uint32_t k = key_of_f32(sv);
+    const int b = (int)(k >> FB_SHIFT);
+    atomicAdd(&L.cnt[b], 1u);
+    atomicMin(&L.kmin[b], k);
+    atomicMax(&L.kmax[b], k);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+  if (lane == 0) L.red[wv] = __float_as_uint(mx);
+  __syncthreads();
+  if (tid == 0) {
+    float m2 = -INFINITY;
+    for (int w = 0; w < FB_NW; ++w) m2 = fmaxf(m2, __uint_as_float((uint32_t)L.red[w]));
+    L.f32[0] = m2;
+  }
+  __syncthreads();
+  const float m = L.f32[0];
+
+  // ---- 2. exact normaliser
+  U128 acc = {0, 0};
+  for (int64_t i = tid; i < V; i += FB_NT) acc = u128_add(acc, U128{fixed62(exp_det(x[i] / T - m)), 0});
+  acc = wave_sum_u128(acc);
+  __syncthreads();
+  if (lane == 0) { L.red[2 * wv] = acc.lo; L.red[2 * wv + 1] = acc.hi; }
+  __syncthreads();
+  if (tid == 0) {
+    U128 z = {0, 0};
+    for (int w = 0; w < FB_NW; ++w) z = u128_add(z, U128{L.red[2 * w], L.red[2 * w + 1]});
+    L.f32[1] = rn32_u128(z);
+  }
+  __syncthreads();
+  const float zf = L.f32[1];
+  auto pfun = [&](uint32_t key) -> float { return exp_det(fb_of_key(key) - m) / zf; };
+
+  // top-k: the k-th largest key. Wave 0 finds its bucket (lane l holds buckets
+  // FB_NB - 1 - 64 l - j, j = 0..63, descending), then the bucket's distinct keys
+  // give the key itself.
+  float kth = 0.0f;
+  if (use_k) {
+    if (wv == 0) {
+      uint32_t c = 0;
+      for (int j = 0; j < 64; ++j) c += L.cnt[FB_NB - 1 - 64 * lane - j];
+      const uint32_t incl = wave_incl_scan_u32(c, lane);
+      const uint64_t hit = __ballot(incl >= (uint32_t)a.top_k);
+      const int hl = __ffsll((unsigned long long)hit) - 1;  // top_k < V: some lane hits
+      if (lane == hl) {
+        uint32_t run = incl - c;
+        for (int j = 0; j < 64; ++j) {
+          const int b = FB_NB - 1 - 64 * lane - j;
+          if (run + L.cnt[b] >= (uint32_t)a.top_k) {
+            L.i32[1] = b;
+            L.i32[2] = (int32_t)run;  // elements above the bucket
+            break;
+          }
+          run += L.cnt[b];
+        }
+      }
+    }
+    __syncthreads();
+    const int bk = L.i32[1];
+    const uint32_t need = (uint32_t)a.top_k - (uint32_t)L.i32[2];
+    const int nd = fb_distinct_p(L, x, V, T, bk, bk, m, zf, false, 0.0f);
+    if (nd < 0) {
+      if (tid == 0) L.i32[0] = 1;
+    } else {
+      uint64_t c = 0;
+#pragma unroll
+      for (int t = 0; t < FB_PER; ++t) {
+        const uint64_t e = L.ent[tid * FB_PER + t];
+        c += e == ~0ull ? 0u : (uint32_t)e;
+      }
+      uint64_t tot;
+      const uint64_t incl = fb_scan_u64(c, L, &tot);
+      uint64_t run = incl - c;
+      for (int t = 0; t < FB_PER; ++t) {
+        const uint64_t e = L.ent[tid * FB_PER + t];
+        if (e == ~0ull) break;
+        const uint64_t before = run;
+        run += (uint32_t)e;
+        if (before < need && run >= need) L.f32[2] = fb_ent_p(e);
+      }
+    }
+    __syncthreads();
+    kth = L.f32[2];
+  }
+
+  // ---- 3. per-bucket masses of the top-k-zeroed p, then the region
+  for (int64_t i = tid; i < V; i += FB_NT) {
+    const float sv = x[i] / T;
+    const float pv = fb_pmask(exp_det(sv - m) / zf, use_k, kth);
+    if (pv > 0.0f) atomicAdd((unsigned long long*)&L.mass[key_of_f32(sv) >> FB_SHIFT],
+                             (unsigned long long)fixed62(pv));
+  }
+  __syncthreads();
+  bool cut = false;
+  int bd = 0, bu = -1;
+  if (use_p) {
+    if (wv == 0) {
+      const float tp = a.top_p;
+      uint64_t ms = 0;
+      for (int j = 0; j < 64; ++j) ms += L.mass[FB_NB - 1 - 64 * lane - j];
+      const uint64_t incl = wave_incl_scan_u64(ms, lane);
+      uint64_t run = incl - ms;
+      int fb = -1;
+      for (int j = 0; j < 64; ++j) {
+        const int b = FB_NB - 1 - 64 * lane - j;
+        if (L.cnt[b] == 0) continue;
+        run += L.mass[b];
+        const float pmin = fb_pmask(pfun(L.kmin[b]), use_k, kth);
+        if (!((rn32_u64(run) - pmin) < tp)) { fb = b; break; }
+      }
+      const uint64_t hit = __ballot(fb >= 0);
+      if (hit) {
+        if (lane == __ffsll((unsigned long long)hit) - 1) L.i32[3] = fb;
+      } else if (lane == 0) {
+        L.i32[3] = -1;
+      }
+    }
+    __syncthreads();
+    const int bs = L.i32[3];
+    if (bs >= 0) {
+      if (tid == 0) {  // widen while a neighbour holds the same (nonzero) p at the shared edge
+        int lo = bs, hi = bs;
+        for (;;) {
+          int nx = hi + 1;
+          while (nx < FB_NB && L.cnt[nx] == 0) ++nx;
+          if (nx >= FB_NB) break;
+          const float e = fb_pmask(pfun(L.kmax[hi]), use_k, kth);
+          if (e > 0.0f && fb_pmask(pfun(L.kmin[nx]), use_k, kth) == e) hi = nx; else break;
+        }
+        for (;;) {
+          int nx = lo - 1;
+          while (nx >= 0 && L.cnt[nx] == 0) --nx;
+          if (nx < 0) break;
+          const float e = fb_pmask(pfun(L.kmin[lo]), use_k, kth);
+          if (e > 0.0f && fb_pmask(pfun(L.kmax[nx]), use_k, kth) == e) lo = nx; else break;
+        }
+        L.i32[4] = lo;
+        L.i32[5] = hi;
+      }
+      __syncthreads();
+      cut = true;
+      bd = L.i32[4];
+      bu = L.i32[5];
+    }
+  }
+  uint64_t nabove = 0, sabove = 0;
+  if (cut) {
+    for (int b = tid; b < FB_NB; b += FB_NT)
+      if (b > bu) { nabove += L.cnt[b]; sabove += L.mass[b]; }
+    nabove = fb_sum_u64(nabove, L);
+    sabove = fb_sum_u64(sabove, L);
+  }
+
+  // ---- 4. the boundary tie group from the region's distinct keys
+  // vb: the value of the last kept element; partial: its group keeps only its
+  // rstar lowest ids; vb = +inf when no element of the region is kept
+  float vb = 0.0f;
+  bool partial = false;
+  int64_t rstar = 0;
+  uint64_t tot = 0;
+  if (cut) {
+    const int nd = fb_distinct_p(L, x, V, T, bd, bu, m, zf, use_k, kth);
+    if (nd < 0) {
+      if (tid == 0) L.i32[0] = 1;
+    } else {
+      const float tp = a.top_p;
+      // masses and counts of the sorted distinct keys: thread t holds entries
+      // FB_PER t .. FB_PER t + FB_PER - 1
+      uint64_t mk = 0, ck = 0;
+#pragma unroll
+      for (int t = 0; t < FB_PER; ++t) {
+        const uint64_t e = L.ent[tid * FB_PER + t];
+        if (e != ~0ull) {
+          const uint32_t c = (uint32_t)e;
+          mk += (uint64_t)c * fixed62(fb_ent_p(e));
+          ck += c;
+        }
+      }
+      uint64_t mtot, ctot;
+      const uint64_t mincl = fb_scan_u64(mk, L, &mtot);
+      const uint64_t cincl = fb_scan_u64(ck, L, &ctot);
+      // the first key whose last element fails (or is dropped by top-k)
+      uint64_t mrun = sabove + mincl - mk;
+      int first = 0x7FFFFFFF;
+      for (int t = 0; t < FB_PER; ++t) {
+        const int i = tid * FB_PER + t;
+        const uint64_t e = L.ent[i];
+        if (e == ~0ull) break;
+        const float pv = fb_ent_p(e);
+        mrun += (uint64_t)(uint32_t)e * fixed62(pv);
+        const bool dropped = use_k && pv < kth;
+        if (dropped || !((rn32_u64(mrun) - pv) < tp)) { first = i; break; }
+      }
+      const uint32_t f = blk_min_u32_fb(first, L);
+      // entry f is the boundary tie group (one entry per distinct p)
+      const int g0 = f == 0x7FFFFFFFu ? -1 : (int)f, g1 = g0;
+      if (tid == 0 && g0 >= 0) L.f32[4] = fb_ent_p(L.ent[g0]);
+      __syncthreads();
+      // the mass and count before the group, and the group's count
+      uint64_t sb = 0, nb = 0, gc = 0;
+      if (g0 >= 0) {
+#pragma unroll
+        for (int t = 0; t < FB_PER; ++t) {
+          const int i = tid * FB_PER + t;
+          const uint64_t e = L.ent[i];
+          if (e == ~0ull) continue;
+          const uint32_t c = (uint32_t)e;
+          if (i < g0) {
+            sb += (uint64_t)c * fixed62(fb_ent_p(e));
+            nb += c;
+          } else if (i <= g1) {
+            gc += c;
+          }
+        }
+        sb = sabove + fb_sum_u64(sb, L);
+        nb = nabove + fb_sum_u64(nb, L);
+        gc = fb_sum_u64(gc, L);
+      }
+      if (g0 < 0) {
+        vb = 0.0f;
+        tot = sabove + mtot;
+        cut = false;  // every region element is kept as the elements above it
+      } else {
+        const float vf = L.f32[4];
+        // members kept: keep_j = rn32(sb + (j+1) f(vf)) - vf < tp holds for a prefix
+        // of j (the position-0 rule keeps j = 0 when nothing precedes); top-k-dropped
+        // members keep none
+        uint64_t r0 = 0;
+        if (!(use_k && vf < kth)) {
+          const uint64_t P = fixed62(vf);
+          if (wv == 0) {
+            uint64_t lo = 0, hi = gc;  // answer in [lo, hi]
+            while (lo < hi) {
+              const uint64_t step = (hi - lo + kWave - 1) / kWave;
+              const uint64_t cand = lo + (uint64_t)lane * step;
+              const bool keep = cand < hi &&
+                                (((rn32_u64(sb + (cand + 1) * P) - vf) < tp) || (nb + cand == 0));
+              const int nk = __popcll(__ballot(keep));
+              if (nk == 0) break;
+              const uint64_t last = lo + (uint64_t)(nk - 1) * step;
+              lo = last + 1;
+              hi = min(hi, last + step);
+            }
+            if (lane == 0) L.u64[3] = lo;
+          }
+          __syncthreads();
+          r0 = L.u64[3];
+        }
+        if (r0 > 0) {
+          vb = vf;
+          rstar = (int64_t)r0;
+          partial = r0 < gc && vf > 0.0f;
+          tot = sb + r0 * fixed62(vf);
+        } else if (g0 > 0) {  // the last kept element is of the entry before the group
+          vb = fb_ent_p(L.ent[g0 - 1]);
+          tot = sb;
+        } else {              // ... or above the region
+          vb = INFINITY;
+          tot = sb;
+        }
+      }
+    }
+    __syncthreads();
+  } else {  // no top-p cut: every element top-k keeps
+    uint64_t t0 = 0;
+    for (int64_t i = tid; i < V; i += FB_NT)
+      t0 += fixed62(fb_pmask(exp_det(x[i] / T - m) / zf, use_k, kth));
+    tot = fb_sum_u64(t0, L);
+  }
+  const bool unsupported = L.i32[0] != 0;
+  const float totf = fmaxf(rn32_u64(tot), 1e-12f);
+
+  // ---- 5. output, tie-group bits, statistics (members ranked by id, one block
+  // scan per 1024 ids, only for a partially kept group)
+  if (tid == 0) { L.f32[3] = 0.0f; L.i32[7] = 0; }
+  __syncthreads();
+  uint64_t mbase = 0;
+  for (int64_t base = 0; base < V; base += FB_NT) {  // uniform loop
+    const int64_t i = base + tid;
+    float p = 0.0f, pv = 0.0f;
+    int b = -1;
+    if (i < V) {
+      const float sv = x[i] / T;
+      p = exp_det(sv - m) / zf;
+      pv = fb_pmask(p, use_k, kth);
+      b = (int)(key_of_f32(sv) >> FB_SHIFT);
+    }
+    const bool mem = partial && i < V && pv == vb;
+    uint64_t rank = 0;
+    if (partial) {
+      uint64_t tot_m;
+      const uint64_t incl = fb_scan_u64(mem ? 1u : 0u, L, &tot_m);
+      rank = mbase + incl - (mem ? 1u : 0u);
+      mbase += tot_m;
+    }
+    if (i < V) {
+      bool kept = !(use_k && p < kth);
+      if (cut) {
+        if (b < bd) kept = false;
+        else if (b <= bu) kept = kept && (pv > vb || (pv == vb && (!partial || rank < (uint64_t)rstar)));
+      }
+      const float pf = unsupported ? __builtin_nanf("") : (kept ? p / totf : 0.0f);
+      o[i] = pf;
+      if (i == gid) {
+        L.f32[3] = pf;
+        if (mem) L.i32[7] = 1;
+      }
+    }
+    const uint64_t bm = __ballot(mem);
+    const int64_t w0 = (base + wv * kWave) >> 5;  // the wave's 64 ids: two words
+    if (bits && lane == 0 && w0 < a.tie_ld) {
+      bits[w0] = (uint32_t)bm;
+      if (w0 + 1 < a.tie_ld) bits[w0 + 1] = (uint32_t)(bm >> 32);
+    }
+  }
+  __syncthreads();
+  if (tid == 0 && a.stats) {
+    RowStat st = {};
+    st.flags = kRowProbs | (L.i32[7] ? kRowGatherTie : 0u) | (unsupported ? kRowUnsupported : 0u);
+    st.m = m; st.zf = zf; st.totf = totf; st.mass = tot;
+    st.glo = 1; st.ghi = 0; st.argmax = -1;
+    st.pgather = (gid >= 0 && gid < V) ? L.f32[3] : 0.0f;
+    a.stats[row] = st;
+  }
+}
+
 hipError_t launch_to_probs_f32(const F32Args& a, int64_t rows, hipStream_t s) {
-  hipLaunchKernelGGL(to_probs_f32_kernel, dim3((unsigned)rows), dim3(F32_NT), 0, s, a);
+  if (a.V <= F32_MAXV)
+    hipLaunchKernelGGL(to_probs_f32_kernel, dim3((unsigned)rows), dim3(F32_NT), 0, s, a);
+  else
+    hipLaunchKernelGGL(to_probs_f32_big_kernel, dim3((unsigned)rows), dim3(FB_NT), 0, s, a);
   return hipGetLastError();
 }
 

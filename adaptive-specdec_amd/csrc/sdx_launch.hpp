@@ -72,7 +72,8 @@ struct F32Args {
   RowStat* stats;  // may be null
   uint32_t* zero;  // words [0, nzero) cleared (block `row` clears word `row`), or null
   int64_t nzero;
-  uint32_t* tie_bits;  // [rows, kF32TieWords]: members of the row's partially kept
+  int64_t tie_ld;      // words per row of tie_bits (f32_tie_words(V))
+  uint32_t* tie_bits;  // [rows, tie_ld]: members of the row's partially kept
                        // boundary tie group, one bit per id (null: not written)
 };
 
@@ -204,8 +205,9 @@ hipError_t launch_rank_bf16(const RowStatArgs& a, int64_t rows, hipStream_t s);
 // workgroup: 16 x 20 x 512 values.
 constexpr int64_t kMaxVocabBf16 = (1 << 18) - 8;
 constexpr int64_t kMaxVocabF16 = 16 * 20 * 512;
-constexpr int64_t kF32MaxVocab = 8192;
-constexpr int64_t kF32TieWords = kF32MaxVocab / 32;  // tie-group bit words per fp32 row
+constexpr int64_t kF32MaxVocab = 262144;
+// tie-group bit words per fp32 row: one bit per id, whole 64-id wave rounds
+inline int64_t f32_tie_words(int64_t V) { return (V + 63) / 64 * 2; }
 hipError_t launch_to_probs_f32(const F32Args& a, int64_t rows, hipStream_t s);
 // sdx_sample.hip
 // Draw: chunk records and the per-job select in one launch (with the accept

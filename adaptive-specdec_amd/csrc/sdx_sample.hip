@@ -41,8 +41,9 @@ struct EvalProb {
   int64_t ld2;
   int64_t split;
   bool vec;
-  const uint32_t* tie_bits;  // per row kF32TieWords words: members of a partial
+  const uint32_t* tie_bits;  // per row bits_ld words: members of a partial
                              // boundary tie group (null: no membership known)
+  int64_t bits_ld;
   struct Row {
     const float* ptr;
     float vg;
@@ -52,7 +53,7 @@ struct EvalProb {
   __device__ void bind(Row& r, int64_t row, const float*) const {
     r.ptr = row < split ? base + row * ld : base2 + (row - split) * ld2;
     r.vg = 0.0f;
-    r.bits = tie_bits ? tie_bits + row * kF32TieWords : nullptr;
+    r.bits = tie_bits ? tie_bits + row * bits_ld : nullptr;
   }
   __device__ static int32_t rstar(const Row&) { return 0; }
   __device__ static bool in_tie_group(const Row& r, int64_t id) {
@@ -977,13 +978,13 @@ hipError_t launch_draw_rows16(int fmt, const RowSource16& src, const RowStat* st
 hipError_t launch_draw_probs(const RowSourceF32& src, const AcceptArgs* acc, SampleJob* jobs,
                              int64_t njobs, int64_t V, ChunkRec* recs, uint32_t* counters,
                              int64_t* y, hipStream_t s, const uint32_t* tie_bits) {
-  EvalProb ev{src.base, src.ld, src.base2, src.ld2, src.split, src.vec, tie_bits};
+  EvalProb ev{src.base, src.ld, src.base2, src.ld2, src.split, src.vec, tie_bits, f32_tie_words(V)};
   return launch_draw(ev, acc, jobs, njobs, V, recs, counters, y, s);
 }
 
 hipError_t launch_chunk_mass_probs(const RowSourceF32& src, SampleJob* jobs, int64_t njobs,
                                    int64_t V, ChunkRec* recs, hipStream_t s) {
-  EvalProb ev{src.base, src.ld, src.base2, src.ld2, src.split, src.vec, nullptr};
+  EvalProb ev{src.base, src.ld, src.base2, src.ld2, src.split, src.vec, nullptr, 0};
   return launch_draw(ev, nullptr, jobs, njobs, V, recs, nullptr, nullptr, s);
 }
 

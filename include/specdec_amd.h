@@ -90,8 +90,11 @@ int sdx_workspace_init(void* workspace, size_t bytes, sdx_stream_t stream);
  * (first index among maxima); top_p outside (0, 1) -> no nucleus; top_k <= 0
  * or >= vocab -> no top-k.
  * Vocabularies: bf16 rows up to 262,136 (2^18 - 8), fp16 up to 163,840, fp32 up
- * to 8,192; larger ones return SDX_EUNSUPPORTED (here and in the verify entry
- * points) before anything is launched. */
+ * to 262,144 (above 8,192 the fp32 rows take a multi-pass kernel that sorts only
+ * the nucleus boundary region, at most 7,168 distinct probabilities: a row whose region is
+ * larger is flagged SDX_FLAG_UNSUPPORTED with NaN probabilities); larger ones
+ * return SDX_EUNSUPPORTED (here and in the verify entry points) before anything
+ * is launched. */
 
 /* to_probs (sampling.py:34-67): logits [rows, vocab] (dtype) -> probs [rows, vocab] fp32. */
 size_t sdx_to_probs_workspace(int64_t rows, int64_t vocab, int dtype);
