@@ -19,11 +19,12 @@
 // its keys then stream through LDS
 // in tiles of 32 tokens (each token's head slice is 256 contiguous bytes of
 // its page), two tiles in flight in registers while one is used:
-//   S = Q K^T       16 x 32 per wave: 2 x 8 v_mfma_f32_16x16x16_bf16
+//   S = Q K^T       16 x 32 per wave: 2 x 4 v_mfma_f32_16x16x32_bf16 (gfx950)
 //   online softmax  per row in fp32 (max and sum across the 16-lane rows)
-//   O += P V        16 x 128 per wave: 8 x 2 MFMAs, P rounded to bf16
+//   O += P V        16 x 128 per wave: 8 MFMAs (K = the tile's 32 tokens), P
+//                   rounded to bf16
 // Q operands stay in registers; V is stored transposed in LDS so both MFMA
-// operands of P V are 8-byte reads. A row that fits one chunk writes its
+// operands of P V are pairs of 8-byte reads. A row that fits one chunk writes its
 // output directly; otherwise each chunk writes (O unnormalised, max, sum) in
 // fp32 and a second kernel merges the chunks of the row.
 // The kernels are bound by the KV bytes streamed (about 22 flop per byte),
@@ -45,7 +46,23 @@ constexpr int VA_PS = VA_TOK + 4;
 constexpr int VA_CHMAX = 1024;  // most tokens per chunk (multiple of 2 tiles)
 
 typedef short va_s4 __attribute__((ext_vector_type(4)));
+typedef short va_s8 __attribute__((ext_vector_type(8)));
+typedef __bf16 va_bf8 __attribute__((ext_vector_type(8)));
 typedef float va_f4 __attribute__((ext_vector_type(4)));
+
+// gfx950's v_mfma_f32_16x16x32_bf16: lane l holds A[l % 16][8 (l / 16) .. + 7] and
+// B[8 (l / 16) .. + 7][l % 16] (eight bf16 each); D[4 (l / 16) + r][l % 16] in
+// element r, as in the 16x16x16 form.
+__device__ __forceinline__ va_f4 va_mfma32(va_s8 a, va_s8 b, va_f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(va_bf8, a),
+                                                 __builtin_bit_cast(va_bf8, b), c, 0, 0, 0);
+}
+// Eight bf16 from two 8-byte LDS reads (the operand rows are 8-byte aligned).
+__device__ __forceinline__ va_s8 va_ld8(const uint16_t* p) {
+  const va_s4 lo = *reinterpret_cast<const va_s4*>(p);
+  const va_s4 hi = *reinterpret_cast<const va_s4*>(p + 4);
+  return (va_s8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
 
 
 __device__ __forceinline__ uint16_t va_bf16(float x) {  // round to nearest even
@@ -282,15 +299,17 @@ verify_attn_kernel(AttnArgs a) {
   }
 
   // the wave's query operands, in registers: lane holds row r0 + lc, dims
-  // 16 kc + lr .. + 3
-  va_s4 qa[VA_D / 16];
+  // 32 kc + lk .. + 7 (lk = 8 (lane / 16), the operand layout of the 16x16x32 form)
+  const int lk = 8 * (lane / 16);
+  va_s8 qa[VA_D / 32];
   {
     const int i = r0 + lc;
     const bool has = active && i < M;
     const uint16_t* src = a.q + (has ? sRow[i] : 0);
 #pragma unroll
-    for (int kc = 0; kc < VA_D / 16; ++kc)
-      qa[kc] = has ? *reinterpret_cast<const va_s4*>(src + kc * 16 + lr) : (va_s4){0, 0, 0, 0};
+    for (int kc = 0; kc < VA_D / 32; ++kc)
+      qa[kc] = has ? *reinterpret_cast<const va_s8*>(src + kc * 32 + lk)
+                   : (va_s8){0, 0, 0, 0, 0, 0, 0, 0};
   }
 
   // one tile: the wave's rows against the 32 keys from chunk token t0 in LDS
@@ -300,12 +319,9 @@ verify_attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) s[j] = (va_f4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int kc = 0; kc < VA_D / 16; ++kc) {
+    for (int kc = 0; kc < VA_D / 32; ++kc) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const va_s4 kb = *reinterpret_cast<const va_s4*>(&sK[j * 16 + lc][kc * 16 + lr]);
-        s[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(qa[kc], kb, s[j], 0, 0, 0);
-      }
+      for (int j = 0; j < 2; ++j) s[j] = va_mfma32(qa[kc], va_ld8(&sK[j * 16 + lc][kc * 32 + lk]), s[j]);
     }
     // online softmax in base 2; s[j][r] is row lr + r, token t0 + 16 j + lc
 #pragma unroll
@@ -332,16 +348,11 @@ verify_attn_kernel(AttnArgs a) {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_wave_barrier();  // P written by the whole wave before it is read
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    // O += P V: K = the tile's 32 tokens
+    // O += P V: K = the tile's 32 tokens, one 16x16x32 product per 16 output dims
+    static_assert(VA_TOK == 32, "one K step of the 16x16x32 form per tile");
+    const va_s8 pa = va_ld8(&sP[w][lc][lk]);
 #pragma unroll
-    for (int kc = 0; kc < VA_TOK / 16; ++kc) {
-      const va_s4 pa = *reinterpret_cast<const va_s4*>(&sP[w][lc][kc * 16 + lr]);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const va_s4 vb = *reinterpret_cast<const va_s4*>(&sVt[j * 16 + lc][kc * 16 + lr]);
-        o[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[j], 0, 0, 0);
-      }
-    }
+    for (int j = 0; j < 8; ++j) o[j] = va_mfma32(pa, va_ld8(&sVt[j * 16 + lc][lk]), o[j]);
   };
 
   __syncthreads();  // the slot map is complete
