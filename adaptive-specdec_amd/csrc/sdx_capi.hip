@@ -143,6 +143,12 @@ int sdx_to_probs(const void* logits, int dtype, int64_t rows, int64_t vocab, int
   const Switches sw = switches(temperature, top_p, top_k, vocab);
   Carve c{(uint8_t*)workspace};
   if (dtype == SDX_F32) {
+    // the large-vocabulary kernel keeps per-element intermediates in the output
+    // rows between its passes, so the output may not overlap the logits
+    const uintptr_t l0 = (uintptr_t)logits, l1 = l0 + (uintptr_t)(((rows - 1) * ld + vocab) * 4);
+    const uintptr_t p0 = (uintptr_t)probs, p1 = p0 + (uintptr_t)(((rows - 1) * ld_out + vocab) * 4);
+    if (l0 < p1 && p0 < l1)
+      return fail(SDX_EINVAL, "sdx_to_probs: probs overlap the fp32 logits");
     sdx::F32Args a = {};
     a.base[0] = (const float*)logits; a.nrows[0] = rows; a.ld[0] = ld;
     a.base[1] = a.base[0]; a.nrows[1] = 0; a.ld[1] = ld;

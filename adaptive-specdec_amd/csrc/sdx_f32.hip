@@ -290,8 +290,14 @@ __global__ void __launch_bounds__(F32_NT) to_probs_f32_kernel(F32Args a) {
 //     prefix of the buckets above: the first group whose last element fails is
 //     the boundary group, and a 64-way search gives its members kept, lowest ids
 //     first;
-//  5. the output (p / totf where kept, 0 elsewhere; group members ranked by id
+//  5. the output (p / totf where kept, 0 elsewhere; group members ranked by id,
+//     from wave ballots per 4,096 ids when the rows are 16-byte aligned, else
 //     with one block scan per 1024 ids), the tie-group bits and the statistics.
+// Every element's exp is evaluated once: pass 2 leaves it in the output row,
+// pass 3 replaces it by p = exp / Z, which passes 4 and 5 read back. The
+// passes stream with 16-byte loads, several in flight per thread; the kernel
+// is bound by VALU issue (about 220 instructions per element over the passes,
+// 59% of one CU's issue rate with one row per CU).
 // A region with more than FB_KEYS distinct probabilities marks the row
 // unsupported and writes NaN probabilities. (The top-k bucket is read the same
 // way: the k-th largest p is the group where the bucket's counts reach k.)
@@ -310,7 +316,8 @@ struct FbLds {
   uint64_t mass[FB_NB];
   uint64_t ent[FB_TAB];  // hash table (key word, count word), then sorted (~key << 32 | count)
   uint64_t red[2 * FB_NW];
-  uint32_t ndist;
+  uint32_t wt[2][FB_NW];  // output pass: members per wave, double-buffered by step
+  uint32_t ndist, nfill;
   int32_t i32[8];
   float f32[8];
   uint64_t u64[4];
@@ -356,25 +363,121 @@ __device__ uint64_t fb_scan_u64(uint64_t v, FbLds& L, uint64_t* total) {
   *total = tot;
   return off + incl;
 }
+// Streams the row x[0, V) through f(i, x[i]), every element exactly once, in no
+// particular order: 16-byte loads, FB_UN of them per thread issued before any is
+// used (one scalar load per thread and pass left the passes waiting on memory),
+// and the elements before the first 16-byte boundary and after the last whole
+// vector one per thread.
+constexpr int FB_UN = 4;
+template <class F>
+__device__ __forceinline__ void fb_stream(const float* __restrict__ x, int64_t V, F&& f) {
+  const int tid = threadIdx.x;
+  int64_t head = (int64_t)(((16u - ((uint32_t)(uintptr_t)x & 15u)) & 15u) >> 2);
+  if (head > V) head = V;
+  if (tid < head) f((int64_t)tid, x[tid]);
+  const float4* __restrict__ x4 = reinterpret_cast<const float4*>(x + head);
+  const int64_t n4 = (V - head) >> 2;
+  int64_t j = tid;
+  for (; j + (int64_t)(FB_UN - 1) * FB_NT < n4; j += (int64_t)FB_UN * FB_NT) {
+    float4 v[FB_UN];
+#pragma unroll
+    for (int u = 0; u < FB_UN; ++u) v[u] = x4[j + (int64_t)u * FB_NT];
+#pragma unroll
+    for (int u = 0; u < FB_UN; ++u) {
+      const int64_t i = head + 4 * (j + (int64_t)u * FB_NT);
+      f(i, v[u].x);
+      f(i + 1, v[u].y);
+      f(i + 2, v[u].z);
+      f(i + 3, v[u].w);
+    }
+  }
+  for (; j < n4; j += FB_NT) {
+    const float4 v = x4[j];
+    const int64_t i = head + 4 * j;
+    f(i, v.x);
+    f(i + 1, v.y);
+    f(i + 2, v.z);
+    f(i + 3, v.w);
+  }
+  const int64_t t0 = head + 4 * n4;  // fewer than 4 elements left
+  if (t0 + tid < V) f(t0 + tid, x[t0 + tid]);
+}
+// The same over the logits x and the output row o together: r = f(i, x[i], o[i])
+// (o[i] is not read, 0 is passed, when READ_O is false), stored to o[i] when
+// WRITE_O. The output row holds each element's exp, then its probability,
+// between the passes, so the exp is evaluated once per element; it is read
+// with the logits, 16 bytes at a time, rather than element by element (a load
+// inside the element's work would wait for every load in flight). Rows whose x
+// and o differ in 16-byte phase take one element per thread.
+template <bool READ_O, bool WRITE_O, class F>
+__device__ __forceinline__ void fb_stream_io(const float* __restrict__ x, float* __restrict__ o,
+                                             int64_t V, F&& f) {
+  const int tid = threadIdx.x;
+  auto put = [&](int64_t i, float r) {
+    if (WRITE_O) o[i] = r;
+  };
+  if ((((uint32_t)(uintptr_t)x ^ (uint32_t)(uintptr_t)o) & 15u) != 0) {  // uniform
+    for (int64_t i = tid; i < V; i += FB_NT) put(i, f(i, x[i], READ_O ? o[i] : 0.0f));
+    return;
+  }
+  int64_t head = (int64_t)(((16u - ((uint32_t)(uintptr_t)x & 15u)) & 15u) >> 2);
+  if (head > V) head = V;
+  if (tid < head) put((int64_t)tid, f((int64_t)tid, x[tid], READ_O ? o[tid] : 0.0f));
+  const float4* __restrict__ x4 = reinterpret_cast<const float4*>(x + head);
+  float4* __restrict__ o4 = reinterpret_cast<float4*>(o + head);
+  const int64_t n4 = (V - head) >> 2;
+  constexpr int UN = READ_O ? 2 : FB_UN;
+  auto one = [&](int64_t j, const float4& v, const float4& w) {
+    const int64_t i = head + 4 * j;
+    float4 r;
+    r.x = f(i, v.x, w.x);
+    r.y = f(i + 1, v.y, w.y);
+    r.z = f(i + 2, v.z, w.z);
+    r.w = f(i + 3, v.w, w.w);
+    if (WRITE_O) o4[j] = r;
+  };
+  int64_t j = tid;
+  for (; j + (int64_t)(UN - 1) * FB_NT < n4; j += (int64_t)UN * FB_NT) {
+    float4 v[UN], w[UN];
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      v[u] = x4[j + (int64_t)u * FB_NT];
+      w[u] = READ_O ? o4[j + (int64_t)u * FB_NT] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int u = 0; u < UN; ++u) one(j + (int64_t)u * FB_NT, v[u], w[u]);
+  }
+  for (; j < n4; j += FB_NT)
+    one(j, x4[j], READ_O ? o4[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f));
+  const int64_t t0 = head + 4 * n4;  // fewer than 4 elements left
+  if (t0 + tid < V) put(t0 + tid, f(t0 + tid, x[t0 + tid], READ_O ? o[t0 + tid] : 0.0f));
+}
+
 // The distinct probabilities of the row's elements in buckets [bd, bu] (with
 // top-k zeroing when mask_k) and their counts, sorted descending as
 // ent[i] = (~bits(p) << 32) | count (empty slots, ~0, last): each entry is one
 // tie group of the reference's order. Returns their number, or -1 when more than
-// FB_KEYS.
-__device__ int fb_distinct_p(FbLds& L, const float* __restrict__ x, int64_t V, float T, int bd,
-                             int bu, float m, float zf, bool mask_k, float kth) {
+// FB_KEYS. The occupied hash slots are packed to the front first, so the sort
+// covers the next power of two above their number, not the whole table.
+// The output row o holds each element's exp (o_is_e) or its probability.
+__device__ __forceinline__ int fb_distinct_p(FbLds& L, const float* __restrict__ x,
+                                             const float* __restrict__ o, bool o_is_e, int64_t V,
+                                             float T, int bd, int bu, float zf, bool mask_k,
+                                             float kth) {
   uint32_t* const hk = reinterpret_cast<uint32_t*>(L.ent);
   uint32_t* const hc = hk + FB_TAB;
   for (int i = threadIdx.x; i < FB_TAB; i += FB_NT) { hk[i] = 0u; hc[i] = 0u; }  // 0: empty
-  if (threadIdx.x == 0) L.ndist = 0u;
+  if (threadIdx.x == 0) { L.ndist = 0u; L.nfill = 0u; }
   __syncthreads();
-  for (int64_t i = threadIdx.x; i < V; i += FB_NT) {
-    const float sv = x[i] / T;
+  // (o is only read here: the cast serves the shared streaming helper)
+  fb_stream_io<true, false>(x, const_cast<float*>(o), V, [&](int64_t, float xv, float ov) -> float {
+    const float sv = xv / T;
     const int b = (int)(key_of_f32(sv) >> FB_SHIFT);
-    if (b < bd || b > bu) continue;
-    const uint32_t k = __float_as_uint(fb_pmask(exp_det(sv - m) / zf, mask_k, kth)) + 1u;
+    if (b < bd || b > bu) return 0.0f;
+    const uint32_t k = __float_as_uint(fb_pmask(o_is_e ? ov / zf : ov, mask_k, kth)) + 1u;
     uint32_t h = (k * 0x9E3779B1u) >> 19;  // 13 bits
-    for (int probe = 0; probe < FB_TAB; ++probe) {
+#pragma nounroll
+    for (int probe = 0; probe < FB_TAB; ++probe) {  // kept rolled: 16 copies sit in the stream
       const uint32_t old = atomicCAS(&hk[h], 0u, k);
       if (old == 0u || old == k) {
         if (old == 0u) atomicAdd(&L.ndist, 1u);
@@ -383,7 +486,8 @@ __device__ int fb_distinct_p(FbLds& L, const float* __restrict__ x, int64_t V, f
       }
       h = (h + 1) & (FB_TAB - 1);
     }
-  }
+    return 0.0f;
+  });
   __syncthreads();
   const int nd = (int)L.ndist;
   uint64_t e[FB_PER];
@@ -392,14 +496,18 @@ __device__ int fb_distinct_p(FbLds& L, const float* __restrict__ x, int64_t V, f
     const int i = threadIdx.x + t * FB_NT;
     e[t] = hk[i] ? (((uint64_t)(~(hk[i] - 1u)) << 32) | hc[i]) : ~0ull;
   }
-  __syncthreads();
-#pragma unroll
-  for (int t = 0; t < FB_PER; ++t) L.ent[threadIdx.x + t * FB_NT] = e[t];
-  __syncthreads();
+  __syncthreads();  // the table is read: its words become the packed entries
   if (nd > FB_KEYS) return -1;
-  for (int size = 2; size <= FB_TAB; size <<= 1) {
+#pragma unroll
+  for (int t = 0; t < FB_PER; ++t)
+    if (e[t] != ~0ull) L.ent[atomicAdd(&L.nfill, 1u)] = e[t];  // slots [0, nd), any order
+  for (int i = nd + threadIdx.x; i < FB_TAB; i += FB_NT) L.ent[i] = ~0ull;
+  __syncthreads();
+  int S = 2;
+  while (S < nd) S <<= 1;
+  for (int size = 2; size <= S; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = threadIdx.x; i < FB_TAB; i += FB_NT) {
+      for (int i = threadIdx.x; i < S; i += FB_NT) {
         const int jx = i ^ stride;
         if (jx > i) {
           const bool up = (i & size) == 0;
@@ -430,12 +538,12 @@ __global__ void __launch_bounds__(FB_NT) to_probs_f32_big_kernel(F32Args a) {
   // ---- greedy: one-hot at the first maximum (-0 == +0)
   if (a.greedy) {
     uint64_t best = 0;
-    for (int64_t i = tid; i < V; i += FB_NT) {
-      uint32_t k = key_of_f32(x[i]);
+    fb_stream(x, V, [&](int64_t i, float xv) {
+      uint32_t k = key_of_f32(xv);
       if (k == 0x7FFFFFFFu) k = 0x80000000u;
       const uint64_t c = ((uint64_t)k << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i);
       best = c > best ? c : best;
-    }
+    });
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
       const uint64_t w = (uint64_t)__shfl_xor((long long)best, off, kWave);
@@ -469,15 +577,15 @@ __global__ void __launch_bounds__(FB_NT) to_probs_f32_big_kernel(F32Args a) {
   if (tid == 0) { L.i32[0] = 0; L.f32[2] = 0.0f; }
   __syncthreads();
   float mx = -INFINITY;
-  for (int64_t i = tid; i < V; i += FB_NT) {
-    const float sv = x[i] / T;
+  fb_stream(x, V, [&](int64_t, float xv) {
+    const float sv = xv / T;
     mx = fmaxf(mx, sv);
     const uint32_t k = key_of_f32(sv);
     const int b = (int)(k >> FB_SHIFT);
     atomicAdd(&L.cnt[b], 1u);
     atomicMin(&L.kmin[b], k);
     atomicMax(&L.kmax[b], k);
-  }
+  });
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
   if (lane == 0) L.red[wv] = __float_as_uint(mx);
@@ -492,7 +600,11 @@ __global__ void __launch_bounds__(FB_NT) to_probs_f32_big_kernel(F32Args a) {
 
   // ---- 2. exact normaliser
   U128 acc = {0, 0};
-  for (int64_t i = tid; i < V; i += FB_NT) acc = u128_add(acc, U128{fixed62(exp_det(x[i] / T - m)), 0});
+  fb_stream_io<false, true>(x, o, V, [&](int64_t, float xv, float) -> float {
+    const float e = exp_det(xv / T - m);
+    acc = u128_add(acc, U128{fixed62(e), 0});
+    return e;  // the output row holds the exp until the masses pass
+  });
   acc = wave_sum_u128(acc);
   __syncthreads();
   if (lane == 0) { L.red[2 * wv] = acc.lo; L.red[2 * wv + 1] = acc.hi; }
@@ -533,7 +645,7 @@ __global__ void __launch_bounds__(FB_NT) to_probs_f32_big_kernel(F32Args a) {
     __syncthreads();
     const int bk = L.i32[1];
     const uint32_t need = (uint32_t)a.top_k - (uint32_t)L.i32[2];
-    const int nd = fb_distinct_p(L, x, V, T, bk, bk, m, zf, false, 0.0f);
+    const int nd = fb_distinct_p(L, x, o, true, V, T, bk, bk, zf, false, 0.0f);
     if (nd < 0) {
       if (tid == 0) L.i32[0] = 1;
     } else {
@@ -559,16 +671,24 @@ __global__ void __launch_bounds__(FB_NT) to_probs_f32_big_kernel(F32Args a) {
   }
 
   // ---- 3. per-bucket masses of the top-k-zeroed p, then the region
-  for (int64_t i = tid; i < V; i += FB_NT) {
-    const float sv = x[i] / T;
-    const float pv = fb_pmask(exp_det(sv - m) / zf, use_k, kth);
+  fb_stream_io<true, true>(x, o, V, [&](int64_t, float xv, float e) -> float {
+    const float sv = xv / T;
+    const float p = e / zf;
+    const float pv = fb_pmask(p, use_k, kth);
     if (pv > 0.0f) atomicAdd((unsigned long long*)&L.mass[key_of_f32(sv) >> FB_SHIFT],
                              (unsigned long long)fixed62(pv));
-  }
+    return p;  // from here on the output row holds the probability
+  });
   __syncthreads();
   bool cut = false;
   int bd = 0, bu = -1;
   if (use_p) {
+    // every occupied bucket's smallest p, by the whole block (the walk below
+    // would otherwise evaluate them one after another on each lane)
+    float* const pmin_b = reinterpret_cast<float*>(L.ent);  // free until the region's keys
+    for (int b = tid; b < FB_NB; b += FB_NT)
+      pmin_b[b] = L.cnt[b] ? fb_pmask(pfun(L.kmin[b]), use_k, kth) : 0.0f;
+    __syncthreads();
     if (wv == 0) {
       const float tp = a.top_p;
       uint64_t ms = 0;
@@ -580,8 +700,7 @@ __global__ void __launch_bounds__(FB_NT) to_probs_f32_big_kernel(F32Args a) {
         const int b = FB_NB - 1 - 64 * lane - j;
         if (L.cnt[b] == 0) continue;
         run += L.mass[b];
-        const float pmin = fb_pmask(pfun(L.kmin[b]), use_k, kth);
-        if (!((rn32_u64(run) - pmin) < tp)) { fb = b; break; }
+        if (!((rn32_u64(run) - pmin_b[b]) < tp)) { fb = b; break; }
       }
       const uint64_t hit = __ballot(fb >= 0);
       if (hit) {
@@ -634,7 +753,7 @@ __global__ void __launch_bounds__(FB_NT) to_probs_f32_big_kernel(F32Args a) {
   int64_t rstar = 0;
   uint64_t tot = 0;
   if (cut) {
-    const int nd = fb_distinct_p(L, x, V, T, bd, bu, m, zf, use_k, kth);
+    const int nd = fb_distinct_p(L, x, o, false, V, T, bd, bu, zf, use_k, kth);
     if (nd < 0) {
       if (tid == 0) L.i32[0] = 1;
     } else {
@@ -738,8 +857,7 @@ __global__ void __launch_bounds__(FB_NT) to_probs_f32_big_kernel(F32Args a) {
     __syncthreads();
   } else {  // no top-p cut: every element top-k keeps
     uint64_t t0 = 0;
-    for (int64_t i = tid; i < V; i += FB_NT)
-      t0 += fixed62(fb_pmask(exp_det(x[i] / T - m) / zf, use_k, kth));
+    fb_stream(o, V, [&](int64_t, float p) { t0 += fixed62(fb_pmask(p, use_k, kth)); });
     tot = fb_sum_u64(t0, L);
   }
   const bool unsupported = L.i32[0] != 0;
@@ -750,13 +868,102 @@ __global__ void __launch_bounds__(FB_NT) to_probs_f32_big_kernel(F32Args a) {
   if (tid == 0) { L.f32[3] = 0.0f; L.i32[7] = 0; }
   __syncthreads();
   uint64_t mbase = 0;
-  for (int64_t base = 0; base < V; base += FB_NT) {  // uniform loop
+  // Rows whose logits and probabilities both start 16-byte aligned: four
+  // consecutive ids per thread, 4,096 per block step, 16-byte loads and stores;
+  // member ranks from three ballots per wave (a thread holds at most 4 members)
+  // and one barrier per step. Other rows: one id per thread and a block scan
+  // per 1,024 ids.
+  const bool vec = (((uintptr_t)x | (uintptr_t)o) & 15u) == 0;  // uniform
+  const uint64_t lt_mask = (1ull << lane) - 1ull;
+  for (int64_t base = 0, step = 0; vec && base < V; base += 4 * FB_NT, ++step) {  // uniform loop
+    const int64_t i0 = base + 4 * tid;
+    const bool whole = i0 + 3 < V;
+    float xv[4], p[4];
+    if (whole) {
+      const float4 v = *reinterpret_cast<const float4*>(x + i0);
+      const float4 w = *reinterpret_cast<const float4*>(o + i0);
+      xv[0] = v.x; xv[1] = v.y; xv[2] = v.z; xv[3] = v.w;
+      p[0] = w.x; p[1] = w.y; p[2] = w.z; p[3] = w.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xv[j] = i0 + j < V ? x[i0 + j] : 0.0f;
+        p[j] = i0 + j < V ? o[i0 + j] : 0.0f;
+      }
+    }
+    float pv[4];
+    int b[4];
+    uint32_t nib = 0;  // bit j: id i0 + j is a member of the partially kept group
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float sv = xv[j] / T;
+      pv[j] = fb_pmask(p[j], use_k, kth);
+      b[j] = (int)(key_of_f32(sv) >> FB_SHIFT);
+      if (partial && i0 + j < V && pv[j] == vb) nib |= 1u << j;
+    }
+    uint64_t rank = 0;  // members before id i0
+    if (partial) {      // uniform
+      const uint32_t c = (uint32_t)__popc(nib);
+      uint32_t ex = 0, wt = 0;
+#pragma unroll
+      for (int bit = 0; bit < 3; ++bit) {
+        const uint64_t bb = __ballot((c >> bit) & 1u);
+        ex += (uint32_t)__popcll(bb & lt_mask) << bit;
+        wt += (uint32_t)__popcll(bb) << bit;
+      }
+      // slot parity alternates, so a wave a step ahead never overwrites a total
+      // still being read: the step between them has its own barrier
+      if (lane == 0) L.wt[step & 1][wv] = wt;
+      __syncthreads();
+      uint32_t off = 0, tot_m = 0;
+#pragma unroll
+      for (int w = 0; w < FB_NW; ++w) {
+        const uint32_t t = L.wt[step & 1][w];
+        off += w < wv ? t : 0u;
+        tot_m += t;
+      }
+      rank = mbase + off + ex;
+      mbase += tot_m;
+    }
+    float pf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool mem = (nib >> j) & 1u;
+      bool kept = !(use_k && p[j] < kth);
+      if (cut) {
+        if (b[j] < bd) kept = false;
+        else if (b[j] <= bu)
+          kept = kept && (pv[j] > vb || (pv[j] == vb && (!partial || rank < (uint64_t)rstar)));
+      }
+      if (mem) ++rank;
+      pf[j] = unsupported ? __builtin_nanf("") : (kept ? p[j] / totf : 0.0f);
+      if (i0 + j == gid) {
+        L.f32[3] = pf[j];
+        if (mem) L.i32[7] = 1;
+      }
+    }
+    if (whole) {
+      *reinterpret_cast<float4*>(o + i0) = make_float4(pf[0], pf[1], pf[2], pf[3]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (i0 + j < V) o[i0 + j] = pf[j];
+    }
+    if (bits) {  // uniform: word q of the row holds ids 32q .. 32q + 31, from 8 lanes
+      uint32_t wd = nib;
+#pragma unroll
+      for (int q = 1; q < 8; ++q) wd |= (uint32_t)__shfl(nib, lane + q, kWave) << (4 * q);
+      const int64_t w0 = i0 >> 5;
+      if ((lane & 7) == 0 && w0 < a.tie_ld) bits[w0] = wd;
+    }
+  }
+  for (int64_t base = 0; !vec && base < V; base += FB_NT) {  // uniform loop
     const int64_t i = base + tid;
     float p = 0.0f, pv = 0.0f;
     int b = -1;
     if (i < V) {
       const float sv = x[i] / T;
-      p = exp_det(sv - m) / zf;
+      p = o[i];  // the probability, left by the masses pass
       pv = fb_pmask(p, use_k, kth);
       b = (int)(key_of_f32(sv) >> FB_SHIFT);
     }

@@ -342,15 +342,20 @@ def bench_probs(args, torch):
     `to_probs`, `engine.py:301-302` `sample_from_probs`): 256 rows of V=151936
     bf16 logits (B=64 x k=4 draft positions), T=0.8, top-p 0.95 -> fp32
     probabilities, then one inverse-CDF draw per row from them. Each call is
-    timed on its own, replayed from graphs over three rotating input sets."""
+    timed on its own, replayed from graphs over three rotating input sets.
+    `--logits f32` feeds fp32 logits instead (the fp32 row kernel: each row
+    read once, its probabilities written once)."""
     from specdec.sampling import sample_from_probs, to_probs
     from specdec.workloads import uniforms, zipf_logits
     rows, V, T, tp = 256, 151936, 0.8, 0.95
+    f32 = args.logits == "f32"
+    ldt = torch.float32 if f32 else torch.bfloat16
+    isz = 4 if f32 else 2
     dev = "cuda:0"
     sets = []
     for i in range(3):
         g = torch.Generator(device=dev).manual_seed(2000 + i)
-        sets.append((zipf_logits(rows, V, g, dev), uniforms((rows,), g, dev)))
+        sets.append((zipf_logits(rows, V, g, dev, dtype=ldt), uniforms((rows,), g, dev)))
     probs = [None] * 3
 
     def tp_step(i):  # captured: probs[i] is the graph's static output
@@ -371,22 +376,24 @@ def bench_probs(args, torch):
     fills = [torch.empty(rows, V, dtype=torch.float32, device=dev) for _ in range(3)]
     gf = [capture(lambda f=f: f.fill_(0.5), torch) for f in fills]
     ms_fill = timed_graphs(gf, args.steps, torch)
-    alg_tp = rows * V * (2 + 4)                     # bf16 logits in, fp32 probs out
+    alg_tp = rows * V * (isz + 4)                   # logits in, fp32 probs out
     alg_sp = rows * V * 4                           # fp32 probs in
     ach_tp = alg_tp / (ms_tp_call / 1e3) / 1e9
     ach_sp = alg_sp / (ms_sp / 1e3) / 1e9
-    return {"metric": "to_probs + sample_from_probs, 256 x 151936 bf16 logits, GB/s",
+    lname = "f32" if f32 else "bf16"
+    kname = "to_probs_f32_big_kernel" if f32 else "rowstream + member_count + materialize16"
+    return {"metric": f"to_probs + sample_from_probs, 256 x 151936 {lname} logits, GB/s",
             "value": round((alg_tp + alg_sp) / ((ms_tp_call + ms_sp) / 1e3) / 1e9, 1),
             "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(ms_tp_call + ms_sp, 5), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-            "config": {"workload": "to_probs 256 x 151936 bf16 (T=0.8, top-p 0.95) -> fp32, "
+            "config": {"workload": f"to_probs 256 x 151936 {lname} (T=0.8, top-p 0.95) -> fp32, "
                                    "then sample_from_probs on it", "rows": rows, "vocab": V},
             "to_probs_us": round(ms_tp_call * 1e3, 2),
             "sample_from_probs_us": round(ms_sp * 1e3, 2),
             "fill_output_us": round(ms_fill * 1e3, 2),
             "roofline": {"bound": "hbm",
-                         "kernel": "to_probs (rowstream + member_count + materialize16)",
+                         "kernel": f"to_probs ({kname})",
                          "achieved": round(ach_tp, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(ach_tp / HBM_PEAK_GBS, 4), "traffic": None,
                          "algorithmic_bytes": alg_tp, "avg_launch_us": round(ms_tp_call * 1e3, 2)},
@@ -656,6 +663,8 @@ def main():
                     help="verify workload: vocabulary of the bf16 rows (151936: the headline)")
     ap.add_argument("--attn-chunk", type=int, default=0,
                     help="attn workload: keys per chunk (0: the library default)")
+    ap.add_argument("--logits", default="bf16", choices=["bf16", "f32"],
+                    help="probs workload: dtype of the logits")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true")

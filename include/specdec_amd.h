@@ -96,7 +96,9 @@ int sdx_workspace_init(void* workspace, size_t bytes, sdx_stream_t stream);
  * return SDX_EUNSUPPORTED (here and in the verify entry points) before anything
  * is launched. */
 
-/* to_probs (sampling.py:34-67): logits [rows, vocab] (dtype) -> probs [rows, vocab] fp32. */
+/* to_probs (sampling.py:34-67): logits [rows, vocab] (dtype) -> probs [rows, vocab] fp32.
+ * probs may not overlap fp32 logits (SDX_EINVAL): above 8,192 tokens the fp32 kernel
+ * keeps each element's exp, then its probability, in the output row between passes. */
 size_t sdx_to_probs_workspace(int64_t rows, int64_t vocab, int dtype);
 int sdx_to_probs(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t ld,
                  float temperature, float top_p, int32_t top_k,

@@ -113,6 +113,12 @@ def test_c_abi_argument_errors():
     F16 = 2
     assert L.sdx_to_probs(fake, F16, 1, 163840 + 8, 163840 + 8, ctypes.c_float(0.8),
                           ctypes.c_float(0.95), 0, fake, 163840 + 8, fake, 1 << 40, None) == EUNSUP
+    # fp32 to_probs: the output rows may not overlap the logits (in place is refused)
+    F32 = 0
+    Vf = 151936
+    assert L.sdx_to_probs(fake, F32, 2, Vf, Vf, ctypes.c_float(0.8), ctypes.c_float(0.95), 0,
+                          ctypes.c_void_p(4096 + 4 * Vf), Vf, fake, 1 << 40, None) == EINVAL
+    assert b"overlap" in L.sdx_last_error()
     assert verify(B, 0, V, need) == EINVAL
     assert verify(B, k, V, need, draft_ids=None) == EINVAL
     assert verify(0, k, V, need) == OK  # an empty batch is a no-op
