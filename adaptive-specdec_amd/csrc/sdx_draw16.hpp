@@ -15,6 +15,7 @@ constexpr int SM_ROUND = SM_NT * 8;  // ids per block round, 8 per thread
 
 // ---------------------------------------------------------------- block scans
 // Exclusive scans over the SM_NT threads of a block; `s` holds SM_NW words.
+template <int NW = SM_NW>
 __device__ inline uint32_t block_excl_u32(uint32_t v, uint32_t* s, uint32_t* total) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const uint32_t incl = wave_incl_scan_u32(v, lane);
@@ -22,7 +23,7 @@ __device__ inline uint32_t block_excl_u32(uint32_t v, uint32_t* s, uint32_t* tot
   __syncthreads();
   uint32_t off = 0, tot = 0;
 #pragma unroll
-  for (int i = 0; i < SM_NW; ++i) {
+  for (int i = 0; i < NW; ++i) {
     const uint32_t x = s[i];
     off += i < w ? x : 0u;
     tot += x;
@@ -31,6 +32,7 @@ __device__ inline uint32_t block_excl_u32(uint32_t v, uint32_t* s, uint32_t* tot
   *total = tot;
   return off + incl - v;
 }
+template <int NW = SM_NW>
 __device__ inline uint64_t block_excl_u64(uint64_t v, uint64_t* s, uint64_t* total) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const uint64_t incl = wave_incl_scan_u64(v, lane);
@@ -38,7 +40,7 @@ __device__ inline uint64_t block_excl_u64(uint64_t v, uint64_t* s, uint64_t* tot
   __syncthreads();
   uint64_t off = 0, tot = 0;
 #pragma unroll
-  for (int i = 0; i < SM_NW; ++i) {
+  for (int i = 0; i < NW; ++i) {
     const uint64_t x = s[i];
     off += i < w ? x : 0ull;
     tot += x;
@@ -391,24 +393,40 @@ __device__ inline int64_t chain16_wave(const AcceptArgs& a, const Eval16<FMT>& e
   return n;
 }
 
-// A record's four rounds of 16-byte loads as named registers; pick() selects
-// one by value (an array indexed at run time would live in scratch).
-struct Quad4 {
-  uint4 a, b, c, d;
+// A record's R (4 or 5) rounds of 16-byte loads as named registers; pick()
+// selects one by value (an array indexed at run time would live in scratch).
+template <int R>
+struct QuadT {
+  static_assert(R == 4 || R == 5, "records of four or five rounds");
+  uint4 a, b, c, d, e;
 };
+using Quad4 = QuadT<4>;
 __device__ __forceinline__ uint32_t pick1(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3,
                                           int u) {
   return u == 0 ? x0 : (u == 1 ? x1 : (u == 2 ? x2 : x3));
 }
-__device__ __forceinline__ uint4 pick(const Quad4& q, int u) {
-  return make_uint4(pick1(q.a.x, q.b.x, q.c.x, q.d.x, u), pick1(q.a.y, q.b.y, q.c.y, q.d.y, u),
-                    pick1(q.a.z, q.b.z, q.c.z, q.d.z, u), pick1(q.a.w, q.b.w, q.c.w, q.d.w, u));
+__device__ __forceinline__ uint32_t pick1(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3,
+                                          uint32_t x4, int u) {
+  return u == 0 ? x0 : (u == 1 ? x1 : (u == 2 ? x2 : (u == 3 ? x3 : x4)));
 }
-__device__ __forceinline__ void put(Quad4& q, int u, const uint4& v) {
+template <int R>
+__device__ __forceinline__ uint4 pick(const QuadT<R>& q, int u) {
+  if constexpr (R == 4)
+    return make_uint4(pick1(q.a.x, q.b.x, q.c.x, q.d.x, u), pick1(q.a.y, q.b.y, q.c.y, q.d.y, u),
+                      pick1(q.a.z, q.b.z, q.c.z, q.d.z, u), pick1(q.a.w, q.b.w, q.c.w, q.d.w, u));
+  else
+    return make_uint4(pick1(q.a.x, q.b.x, q.c.x, q.d.x, q.e.x, u),
+                      pick1(q.a.y, q.b.y, q.c.y, q.d.y, q.e.y, u),
+                      pick1(q.a.z, q.b.z, q.c.z, q.d.z, q.e.z, u),
+                      pick1(q.a.w, q.b.w, q.c.w, q.d.w, q.e.w, u));
+}
+template <int R>
+__device__ __forceinline__ void put(QuadT<R>& q, int u, const uint4& v) {
   if (u == 0) q.a = v;
   else if (u == 1) q.b = v;
   else if (u == 2) q.c = v;
-  else q.d = v;
+  else if (R == 4 || u == 3) q.d = v;
+  else q.e = v;
 }
 __device__ __forceinline__ uint32_t sel_word(const uint4& v, int i) {
   return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
@@ -420,7 +438,7 @@ __device__ __forceinline__ uint32_t sel_word(const uint4& v, int i) {
 // (bp[i], bq[i]) at its start; returns its mass (residual when use_r, else p)
 // in m[i]. With `find` (NR == 1, base <= t): the id whose prefix mass, counted
 // from `base`, first exceeds t goes to *found. `s32` / `s64` hold SM_NW words.
-template <int FMT, int NR>
+template <int FMT, int NR, int NW = SM_NW>
 __device__ void block_walk16(const Eval16<FMT>& ev, const typename Eval16<FMT>::Row& rp,
                              const typename Eval16<FMT>::Row& rq, bool use_r,
                              const int64_t (&i0)[NR], const int64_t (&i1)[NR],
@@ -458,7 +476,7 @@ __device__ void block_walk16(const Eval16<FMT>& ev, const typename Eval16<FMT>::
     __syncthreads();
     uint32_t off = 0;
 #pragma unroll
-    for (int v = 0; v < SM_NW; ++v) off += v < w ? s32[v] : 0u;
+    for (int v = 0; v < NW; ++v) off += v < w ? s32[v] : 0u;
     uint32_t rk_p = bp[i] + ((off + incl - cnt) & 0xFFFFu);
     uint32_t rk_q = bq[i] + ((off + incl - cnt) >> 16);
     uint64_t wv[8], mine = 0;
@@ -480,7 +498,7 @@ __device__ void block_walk16(const Eval16<FMT>& ev, const typename Eval16<FMT>::
     __syncthreads();
     uint64_t before = 0, tot = 0;
 #pragma unroll
-    for (int v = 0; v < SM_NW; ++v) {
+    for (int v = 0; v < NW; ++v) {
       const uint64_t x = s64[v];
       before += v < w ? x : 0ull;
       tot += x;
@@ -561,8 +579,9 @@ __device__ __forceinline__ void rec16_entry(const Rec16Rows& R, Rec16Acc& A, uin
 // the packed codes into nq_l (in the last record, TAIL, by a wave vote per id
 // into nq_s); the p-live ids go through the wave's LDS list L, evaluated one per
 // lane once 64 have gathered. TAIL: the record runs past V (ids past V are skipped).
-template <int FMT, bool TAIL>
-__device__ __forceinline__ void rec16_fast(const Quad4& P, const Quad4& Q, int64_t x0, int64_t V,
+template <int FMT, bool TAIL, int RD = kRec16Rounds>
+__device__ __forceinline__ void rec16_fast(const QuadT<RD>& P, const QuadT<RD>& Q, int64_t x0,
+                                           int64_t V,
                                            int lane, int32_t thp, bool hasgq, uint32_t cqg,
                                            uint32_t* L, const Rec16Rows& R, Rec16Acc& A,
                                            uint32_t& nq_s, uint32_t& nq_l) {
@@ -570,7 +589,7 @@ __device__ __forceinline__ void rec16_fast(const Quad4& P, const Quad4& Q, int64
   const uint32_t cqg2 = cqg | (cqg << 16);
   uint32_t off = 0;  // uniform
 #pragma unroll
-  for (int u = 0; u < kRec16Rounds; ++u) {
+  for (int u = 0; u < RD; ++u) {
     const uint4 pu = pick(P, u), qu = pick(Q, u);
     const uint32_t pw[4] = {pu.x, pu.y, pu.z, pu.w};
     const uint32_t qw[4] = {qu.x, qu.y, qu.z, qu.w};
@@ -598,11 +617,11 @@ __device__ __forceinline__ void rec16_fast(const Quad4& P, const Quad4& Q, int64
         off += (uint32_t)__popcll(m);
       }
     }
-    if (off >= kWave || u == kRec16Rounds - 1) {  // evaluate whole lanes' worth
+    if (off >= kWave || u == RD - 1) {  // evaluate whole lanes' worth
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
       __builtin_amdgcn_wave_barrier();
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      const uint32_t full = u == kRec16Rounds - 1 ? off : (off & ~(uint32_t)(kWave - 1));
+      const uint32_t full = u == RD - 1 ? off : (off & ~(uint32_t)(kWave - 1));
       for (uint32_t i = lane; i < full; i += kWave) {
         const uint32_t e = L[i];
         rec16_entry<FMT>(R, A, e & 0xFFFFu, e >> 16);
@@ -622,12 +641,13 @@ __device__ __forceinline__ void rec16_fast(const Quad4& P, const Quad4& Q, int64
   }
 }
 // Any rows: every id evaluated in place (one loop body, words picked by selects).
-template <int FMT>
-__device__ __forceinline__ void rec16_general(const Quad4& P, const Quad4& Q, int64_t x0,
+template <int FMT, int RD = kRec16Rounds>
+__device__ __forceinline__ void rec16_general(const QuadT<RD>& P, const QuadT<RD>& Q, int64_t x0,
                                               int64_t V, int lane, int32_t klo_p,
                                               const Rec16Rows& R, Rec16Acc& A, uint32_t& nqv) {
+  static_assert(RD == 4, "the in-place path serves four-round records");
 #pragma unroll 1
-  for (int i = 0; i < kRec16Rounds * 8; ++i) {
+  for (int i = 0; i < RD * 8; ++i) {
     const int u = i >> 3, t = i & 7;
     const int64_t id = x0 + u * kDrawSub + (int64_t)lane * 8 + t;
     const uint32_t pw = sel_word(pick(P, u), t >> 1), qw = sel_word(pick(Q, u), t >> 1);
@@ -646,35 +666,41 @@ __device__ __forceinline__ void rec16_general(const Quad4& P, const Quad4& Q, in
 
 // The draw body's LDS (one object, so the fused kernel can overlay it on the
 // row blocks' histogram).
-struct Draw16Lds {
+template <int NW>
+struct Draw16LdsT {
   float tbl_p[kTbl];
   float tbl_q[kTbl];
   // per-wave list of p-live ids' (p code, q code); the completing block keeps the
   // job's records here afterwards
-  alignas(16) uint32_t lst[SM_NW][kLst16];
+  alignas(16) uint32_t lst[NW][kLst16];
   RowStat st[2];
   SampleJob job;
-  uint64_t s64[SM_NW];
-  uint64_t rm2[SM_NW];
+  uint64_t s64[NW];
+  uint64_t rm2[NW];
   int32_t last;
   int32_t part[2];    // records where p's / q's kept group members run out
   uint32_t pbase[4];  // their member ranks (bp, bq) at the record start
   int64_t pick[3];
   int64_t found;
-  uint32_t s32w[SM_NW];
-  uint64_t s64w[SM_NW];
+  uint32_t s32w[NW];
+  uint64_t s64w[NW];
   uint32_t fl;
 };
+using Draw16Lds = Draw16LdsT<SM_NW>;
 
 // One job's accept chain and draw, run by a block of SM_NT threads: block bi of
 // the job's blocks (wave w of it owns record bi * SM_NW + w); the block that
 // completes the job's records draws y.
-template <int FMT, bool COH>
-__device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a, Draw16Lds& S, int64_t j,
-                                            int bi) {
+template <int FMT, bool COH, int NT = SM_NT, int R = kRec16Rounds>
+__device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a,
+                                            Draw16LdsT<NT / kWave>& S, int64_t j, int bi) {
+  constexpr int NW = NT / kWave;
+  constexpr int REC = R * kDrawSub;  // ids per record
+  constexpr int MAXREC = (int)((kMaxVocabBf16 + REC - 1) / REC);
+  static_assert(R <= NW, "the walks give each round of a record to one wave");
   float* const tbl_p = S.tbl_p;
   float* const tbl_q = S.tbl_q;
-  uint32_t(&lst)[SM_NW][kLst16] = S.lst;
+  uint32_t(&lst)[NW][kLst16] = S.lst;
   RowStat* const s_st = S.st;
   SampleJob& s_job = S.job;
   uint64_t* const s64 = S.s64;
@@ -741,16 +767,16 @@ __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a, Draw16Lds&
   // each round is used as soon as it lands), then the tables go to LDS
   // (loads without branches, so the waits before use count them exactly;
   // addresses stay inside the rows / tables, unused values are replaced)
-  const int t0 = threadIdx.x;  // first SM_NT entries now, the rest (wide nuclei) after
+  const int t0 = threadIdx.x;  // first NT entries now, the rest (wide nuclei) after
   const float tp0 = ld_f32<COH>(ev.tables + job.prow * kTbl + t0);
   const float tq0 = ld_f32<COH>(ev.tables + (hasq ? job.qrow : job.prow) * kTbl + t0);
   __builtin_amdgcn_sched_barrier(0);  // keep the issue order: tables, then rows
-  const int rec = bi * SM_NW + w;
+  const int rec = bi * NW + w;
   const bool has_rec = rec < a.nrec;  // uniform per wave
-  const int64_t x0 = (int64_t)rec * kRec16;
-  Quad4 P, Q;
+  const int64_t x0 = (int64_t)rec * REC;
+  QuadT<R> P, Q;
 #pragma unroll
-  for (int u = 0; u < kRec16Rounds; ++u) {
+  for (int u = 0; u < R; ++u) {
     const int64_t idx = x0 + u * kDrawSub + (int64_t)lane * 8;
     // ids at or past V (the last record) are skipped when read, and q codes
     // are read only when the draw has a q row
@@ -761,10 +787,10 @@ __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a, Draw16Lds&
   __builtin_amdgcn_sched_barrier(0);
   if (t0 < rp.st.ntbl) tbl_p[t0] = tp0;
   if (hasq && t0 < rq.st.ntbl) tbl_q[t0] = tq0;
-  for (int t = t0 + SM_NT; t < rp.st.ntbl; t += SM_NT)
+  for (int t = t0 + NT; t < rp.st.ntbl; t += NT)
     tbl_p[t] = ld_f32<COH>(ev.tables + job.prow * kTbl + t);
   if (hasq)
-    for (int t = t0 + SM_NT; t < rq.st.ntbl; t += SM_NT)
+    for (int t = t0 + NT; t < rq.st.ntbl; t += NT)
       tbl_q[t] = ld_f32<COH>(ev.tables + job.qrow * kTbl + t);
   __syncthreads();
   rp.vg = rp.st.glo <= rp.st.ghi
@@ -774,27 +800,27 @@ __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a, Draw16Lds&
 
   // ---- 3. the record
   if (has_rec) {
-    Rec16Rows R;
-    R.tbl_p = tbl_p; R.tbl_q = tbl_q; R.hasq = hasq; R.T = ev.T;
-    R.kmax_p = rp.st.kmax; R.ntbl_p = rp.st.ntbl; R.glo_p = rp.st.glo; R.ghi_p = rp.st.ghi;
-    R.vg_p = rp.vg; R.m_p = rp.st.m; R.zf_p = rp.st.zf; R.totf_p = rp.st.totf;
-    R.kmax_q = rq.st.kmax; R.ntbl_q = rq.st.ntbl; R.klo_q = rq.st.klo; R.glo_q = rq.st.glo;
-    R.ghi_q = rq.st.ghi; R.vg_q = rq.vg; R.m_q = rq.st.m; R.zf_q = rq.st.zf;
-    R.totf_q = rq.st.totf;
+    Rec16Rows RR;
+    RR.tbl_p = tbl_p; RR.tbl_q = tbl_q; RR.hasq = hasq; RR.T = ev.T;
+    RR.kmax_p = rp.st.kmax; RR.ntbl_p = rp.st.ntbl; RR.glo_p = rp.st.glo; RR.ghi_p = rp.st.ghi;
+    RR.vg_p = rp.vg; RR.m_p = rp.st.m; RR.zf_p = rp.st.zf; RR.totf_p = rp.st.totf;
+    RR.kmax_q = rq.st.kmax; RR.ntbl_q = rq.st.ntbl; RR.klo_q = rq.st.klo; RR.glo_q = rq.st.glo;
+    RR.ghi_q = rq.st.ghi; RR.vg_q = rq.vg; RR.m_q = rq.st.m; RR.zf_q = rq.st.zf;
+    RR.totf_q = rq.st.totf;
     const int32_t klo_p = rp.st.klo;
     Rec16Acc A = {0, 0, 0, 0, 0, 0};
     uint32_t nqv = 0;   // per lane: q group members (in-place path, packed counts)
     uint32_t nq_s = 0;  // per wave: q group members (listed path)
-    if (klo_p >= 0x8000 && (!hasq || R.glo_q >= R.ghi_q)) {
+    if (klo_p >= 0x8000 && (!hasq || RR.glo_q >= RR.ghi_q)) {
       const int32_t thp = klo_p - 0x8000;  // p-live: positive code >= this
-      const bool hasgq = hasq && R.glo_q == R.ghi_q;
-      const uint32_t cqg = hasgq ? code_of_key16((uint32_t)R.glo_q) : 0u;
-      if (x0 + kRec16 <= V)
-        rec16_fast<FMT, false>(P, Q, x0, V, lane, thp, hasgq, cqg, lst[w], R, A, nq_s, nqv);
+      const bool hasgq = hasq && RR.glo_q == RR.ghi_q;
+      const uint32_t cqg = hasgq ? code_of_key16((uint32_t)RR.glo_q) : 0u;
+      if (x0 + REC <= V)
+        rec16_fast<FMT, false, R>(P, Q, x0, V, lane, thp, hasgq, cqg, lst[w], RR, A, nq_s, nqv);
       else
-        rec16_fast<FMT, true>(P, Q, x0, V, lane, thp, hasgq, cqg, lst[w], R, A, nq_s, nqv);
+        rec16_fast<FMT, true, R>(P, Q, x0, V, lane, thp, hasgq, cqg, lst[w], RR, A, nq_s, nqv);
     } else {
-      rec16_general<FMT>(P, Q, x0, V, lane, klo_p, R, A, nqv);
+      rec16_general<FMT, R>(P, Q, x0, V, lane, klo_p, RR, A, nqv);
     }
     const uint64_t p2 = A.p2, r0 = A.r0, ra = A.ra, rb = A.rb, rpm = A.rp;
     const uint32_t cnt = A.cnt;
@@ -836,10 +862,10 @@ __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a, Draw16Lds&
 
   const int32_t sp = rp.st.rstar, sq = hasq ? rq.st.rstar : 0;
   const float vp = rp.vg, vq = hasq ? rq.vg : 0.0f;
-  // the job's records (at most kMaxRec16 <= SM_NT) go to LDS, one per thread, in
+  // the job's records (at most MAXREC <= NT) go to LDS, one per thread, in
   // the list space the record pass no longer needs: held in registers across the
   // walks below they spilled to scratch, and scratch slows every wave's launch
-  static_assert(sizeof(lst) >= kMaxRec16 * sizeof(ChunkRec) && kMaxRec16 <= SM_NT,
+  static_assert(sizeof(lst) >= MAXREC * sizeof(ChunkRec) && MAXREC <= NT,
                 "a job's records fit in the list space, one per thread");
   ChunkRec* const lrec = reinterpret_cast<ChunkRec*>(&lst[0][0]);
   const ChunkRec* jrecs = a.recs + j * a.nrec;
@@ -853,7 +879,7 @@ __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a, Draw16Lds&
     cntn += (uint64_t)rec.np | ((uint64_t)rec.nq << 32);
   }
   uint64_t tot_n;
-  const uint64_t ex_n = block_excl_u64(cntn, s64, &tot_n);
+  const uint64_t ex_n = block_excl_u64<NW>(cntn, s64, &tot_n);
   uint64_t sum_r = 0, sum_p = 0;
   {
     uint32_t bp = (uint32_t)ex_n, bq = (uint32_t)(ex_n >> 32);
@@ -879,8 +905,8 @@ __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a, Draw16Lds&
   uint64_t rm_part[2] = {0, 0};
   if (pa >= 0 || pb >= 0) {  // uniform: the (at most two) records where kept members run out
     const int ra_ = pa >= 0 ? pa : pb, rb_ = (pa >= 0 && pb >= 0 && pb != pa) ? pb : -1;
-    const int64_t i0[2] = {(int64_t)ra_ * kRec16, rb_ >= 0 ? (int64_t)rb_ * kRec16 : 0};
-    const int64_t i1[2] = {min(V, i0[0] + kRec16), rb_ >= 0 ? min(V, i0[1] + kRec16) : 0};
+    const int64_t i0[2] = {(int64_t)ra_ * REC, rb_ >= 0 ? (int64_t)rb_ * REC : 0};
+    const int64_t i1[2] = {min(V, i0[0] + REC), rb_ >= 0 ? min(V, i0[1] + REC) : 0};
     const int sa = pa >= 0 ? 0 : 1;
     const uint32_t bp2[2] = {s_pbase[2 * sa], s_pbase[2]};
     const uint32_t bq2[2] = {s_pbase[2 * sa + 1], s_pbase[3]};
@@ -893,7 +919,7 @@ __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a, Draw16Lds&
         const int64_t a0[1] = {i0[i]}, a1[1] = {i1[i]};
         const uint32_t p1[1] = {bp2[i]}, q1[1] = {bq2[i]};
         uint64_t m1[1];
-        block_walk16<FMT, 1>(ev, rp, rq, true, a0, a1, p1, q1, m1, 0, false, 0, &s_found, s32w,
+        block_walk16<FMT, 1, NW>(ev, rp, rq, true, a0, a1, p1, q1, m1, 0, false, 0, &s_found, s32w,
                              s64w);
         mm[i] = m1[0];
       }
@@ -914,7 +940,7 @@ __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a, Draw16Lds&
     tot_r = 0;
     tot_p = 0;
 #pragma unroll
-    for (int i = 0; i < SM_NW; ++i) {
+    for (int i = 0; i < NW; ++i) {
       const uint64_t xr = s64[i], xp = s_rm2[i];
       orr += i < w ? xr : 0ull;
       opp += i < w ? xp : 0ull;
@@ -975,10 +1001,10 @@ __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a, Draw16Lds&
   }
   {
     const int64_t packed = s_pick[1];
-    const int64_t i0[1] = {rec_star * kRec16}, i1[1] = {min(V, rec_star * kRec16 + kRec16)};
+    const int64_t i0[1] = {rec_star * REC}, i1[1] = {min(V, rec_star * REC + REC)};
     const uint32_t bp1[1] = {(uint32_t)(packed & 0xFFFFFFFF)}, bq1[1] = {(uint32_t)(packed >> 32)};
     uint64_t mm[1];
-    block_walk16<FMT, 1>(ev, rp, rq, use_r, i0, i1, bp1, bq1, mm, (uint64_t)s_pick[2], true, t,
+    block_walk16<FMT, 1, NW>(ev, rp, rq, use_r, i0, i1, bp1, bq1, mm, (uint64_t)s_pick[2], true, t,
                          &s_found, s32w, s64w);
   }
   finish(s_found);

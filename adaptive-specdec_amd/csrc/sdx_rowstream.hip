@@ -148,9 +148,11 @@ __device__ __forceinline__ float sk_d(uint32_t key, double invT, float m) {
 // Partials go to LDS slot set `rs`, which then flips: a set is written again
 // only after the next helper's barrier, which every thread passes after
 // reading it, so each helper needs one barrier.
-struct SkRed {
-  uint64_t v[2][4][SK_NW];
+template <int NW>
+struct SkRedT {
+  uint64_t v[2][4][NW];
 };
+using SkRed = SkRedT<SK_NW>;
 enum : int { kOpNone = 0, kOpSum64 = 1, kOpMin32 = 2, kOpMax32 = 3, kOpSum32 = 4 };
 template <int O>
 __device__ __forceinline__ uint64_t sk_wave_op(uint64_t v) {
@@ -173,9 +175,9 @@ __device__ __forceinline__ uint64_t sk_ident() {
 struct Red4 {
   uint64_t v[4];
 };
-template <int O0, int O1 = kOpNone, int O2 = kOpNone, int O3 = kOpNone>
+template <int O0, int O1 = kOpNone, int O2 = kOpNone, int O3 = kOpNone, int NW>
 __device__ __forceinline__ Red4 blk_red(uint64_t a0, uint64_t a1, uint64_t a2, uint64_t a3,
-                                        SkRed& red, int& rs) {
+                                        SkRedT<NW>& red, int& rs) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const uint64_t x0 = sk_wave_op<O0>(a0), x1 = sk_wave_op<O1>(a1);
   const uint64_t x2 = sk_wave_op<O2>(a2), x3 = sk_wave_op<O3>(a3);
@@ -188,7 +190,7 @@ __device__ __forceinline__ Red4 blk_red(uint64_t a0, uint64_t a1, uint64_t a2, u
   __syncthreads();
   Red4 r = {{sk_ident<O0>(), sk_ident<O1>(), sk_ident<O2>(), sk_ident<O3>()}};
 #pragma unroll
-  for (int i = 0; i < SK_NW; ++i) {
+  for (int i = 0; i < NW; ++i) {
     r.v[0] = sk_comb<O0>(r.v[0], red.v[rs][0][i]);
     if (O1) r.v[1] = sk_comb<O1>(r.v[1], red.v[rs][1][i]);
     if (O2) r.v[2] = sk_comb<O2>(r.v[2], red.v[rs][2][i]);
@@ -197,27 +199,33 @@ __device__ __forceinline__ Red4 blk_red(uint64_t a0, uint64_t a1, uint64_t a2, u
   rs ^= 1;
   return r;
 }
-__device__ __forceinline__ uint32_t blk_min_u32(uint32_t v, SkRed& red, int& rs) {
+template <int NW>
+__device__ __forceinline__ uint32_t blk_min_u32(uint32_t v, SkRedT<NW>& red, int& rs) {
   return (uint32_t)blk_red<kOpMin32>(v, 0, 0, 0, red, rs).v[0];
 }
-__device__ __forceinline__ uint32_t blk_max_u32(uint32_t v, SkRed& red, int& rs) {
+template <int NW>
+__device__ __forceinline__ uint32_t blk_max_u32(uint32_t v, SkRedT<NW>& red, int& rs) {
   return (uint32_t)blk_red<kOpMax32>(v, 0, 0, 0, red, rs).v[0];
 }
-__device__ __forceinline__ uint32_t blk_sum_u32(uint32_t v, SkRed& red, int& rs) {
+template <int NW>
+__device__ __forceinline__ uint32_t blk_sum_u32(uint32_t v, SkRedT<NW>& red, int& rs) {
   return (uint32_t)blk_red<kOpSum32>(v, 0, 0, 0, red, rs).v[0];
 }
-__device__ __forceinline__ uint64_t blk_sum_u64(uint64_t v, SkRed& red, int& rs) {
+template <int NW>
+__device__ __forceinline__ uint64_t blk_sum_u64(uint64_t v, SkRedT<NW>& red, int& rs) {
   return blk_red<kOpSum64>(v, 0, 0, 0, red, rs).v[0];
 }
 // Inclusive block scan, one barrier; *total gets the block sum.
-__device__ __forceinline__ uint64_t blk_incl_u64(uint64_t v, SkRed& red, int& rs, uint64_t* total) {
+template <int NW>
+__device__ __forceinline__ uint64_t blk_incl_u64(uint64_t v, SkRedT<NW>& red, int& rs,
+                                                 uint64_t* total) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const uint64_t incl = wave_incl_scan_u64(v, lane);
   if (lane == kWave - 1) red.v[rs][0][w] = incl;
   __syncthreads();
   uint64_t off = 0, tot = 0;
 #pragma unroll
-  for (int i = 0; i < SK_NW; ++i) {
+  for (int i = 0; i < NW; ++i) {
     const uint64_t x = red.v[rs][0][i];
     off += i < w ? x : 0ull;
     tot += x;
@@ -226,14 +234,16 @@ __device__ __forceinline__ uint64_t blk_incl_u64(uint64_t v, SkRed& red, int& rs
   *total = tot;
   return off + incl;
 }
-__device__ __forceinline__ uint32_t blk_incl_u32(uint32_t v, SkRed& red, int& rs, uint32_t* total) {
+template <int NW>
+__device__ __forceinline__ uint32_t blk_incl_u32(uint32_t v, SkRedT<NW>& red, int& rs,
+                                                 uint32_t* total) {
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const uint32_t incl = wave_incl_scan_u32(v, lane);
   if (lane == kWave - 1) red.v[rs][0][w] = incl;
   __syncthreads();
   uint32_t off = 0, tot = 0;
 #pragma unroll
-  for (int i = 0; i < SK_NW; ++i) {
+  for (int i = 0; i < NW; ++i) {
     const uint32_t x = (uint32_t)red.v[rs][0][i];
     off += i < w ? x : 0u;
     tot += x;
@@ -244,15 +254,18 @@ __device__ __forceinline__ uint32_t blk_incl_u32(uint32_t v, SkRed& red, int& rs
 }
 
 // Whole block: the largest key of the row (padding / -NaN code 0xFFFF has key 0).
-__device__ uint32_t exact_kmax(const uint16_t* __restrict__ ptr, int64_t V, SkRed& red, int& rs) {
+template <int NW>
+__device__ uint32_t exact_kmax(const uint16_t* __restrict__ ptr, int64_t V, SkRedT<NW>& red,
+                               int& rs) {
   uint32_t mx = 0;
-  for (int64_t i = threadIdx.x; i < V; i += SK_NT) mx = max(mx, key_of_code16(ptr[i]));
+  for (int64_t i = threadIdx.x; i < V; i += NW * kWave) mx = max(mx, key_of_code16(ptr[i]));
   return blk_max_u32(mx, red, rs);
 }
 // Whole block: counts the row's elements into `hist` under an anchored map.
+template <int NT>
 __device__ void restream_anchored(const uint16_t* __restrict__ ptr, int64_t V, const BinMap& bm,
                                   uint32_t* hist) {
-  for (int64_t e0 = (int64_t)threadIdx.x * 8; e0 < V; e0 += (int64_t)SK_NT * 8) {
+  for (int64_t e0 = (int64_t)threadIdx.x * 8; e0 < V; e0 += (int64_t)NT * 8) {
     uint32_t c[8];
     if (e0 + 8 <= V) {
       const uint4 v = *reinterpret_cast<const uint4*>(ptr + e0);
@@ -273,11 +286,12 @@ __device__ void restream_anchored(const uint16_t* __restrict__ ptr, int64_t V, c
 struct Extremes {
   uint32_t below_max, zkey_min, ze_min, ze_max;
 };
+template <int NW>
 __device__ Extremes key_extremes(const uint16_t* __restrict__ ptr, int64_t V, uint32_t lo,
-                                 uint32_t zlo, uint32_t zhi, double invT, float m, SkRed& red,
-                                 int& rs) {
+                                 uint32_t zlo, uint32_t zhi, double invT, float m,
+                                 SkRedT<NW>& red, int& rs) {
   uint32_t b = 0, z0 = 0xFFFFu, e0 = 0xFFFFFFFFu, e1 = 0;
-  for (int64_t i = threadIdx.x; i < V; i += SK_NT) {
+  for (int64_t i = threadIdx.x; i < V; i += NW * kWave) {
     const uint32_t k = key_of_code16(ptr[i]);
     if (k < lo) b = max(b, k);
     if (k >= zlo && k <= zhi) {
@@ -297,10 +311,11 @@ __device__ Extremes key_extremes(const uint16_t* __restrict__ ptr, int64_t V, ui
 }
 // Whole block: sum over elements with key < lo of fixed62(exp_det(x/T - m) / div),
 // exact in 128 bits (split as sum lo32 + 2^32 sum hi32, each below 2^63).
+template <int NW>
 __device__ U128 below_sum(const uint16_t* __restrict__ ptr, int64_t V, uint32_t lo, double invT,
-                          float m, float div, SkRed& red, int& rs) {
+                          float m, float div, SkRedT<NW>& red, int& rs) {
   uint64_t slo = 0, shi = 0;
-  for (int64_t i = threadIdx.x; i < V; i += SK_NT) {
+  for (int64_t i = threadIdx.x; i < V; i += NW * kWave) {
     const uint32_t k = key_of_code16(ptr[i]);
     if (k < lo) {
       const float e = exp_det(sk_d(k, invT, m));
@@ -327,6 +342,7 @@ __device__ U128 below_sum(const uint16_t* __restrict__ ptr, int64_t V, uint32_t 
 // (vmcnt(0)) before its relaxed agent-scope counter increment. A plain store or
 // load of the handed-off data added here would race across XCDs.
 typedef uint32_t sk_u32x4 __attribute__((ext_vector_type(4)));
+template <int NT>
 __device__ __forceinline__ int split_merge(const uint32_t* magic, uint32_t* __restrict__ cnt,
                                            uint8_t* parts, int P, int64_t sidx, int part,
                                            uint32_t* hist, uint32_t* omx, uint32_t* cp,
@@ -335,7 +351,7 @@ __device__ __forceinline__ int split_merge(const uint32_t* magic, uint32_t* __re
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
       parts + sidx * P * (int64_t)SK_SPLIT_BYTES, (short)0, (int)(P * SK_SPLIT_BYTES), 0x00020000);
   const uint32_t mine = (uint32_t)part * SK_SPLIT_BYTES;
-  for (int c = tid; c < SK_SPLIT_CHUNKS; c += SK_NT) {
+  for (int c = tid; c < SK_SPLIT_CHUNKS; c += NT) {
     const uint4 h0 = *reinterpret_cast<const uint4*>(hist + 8 * c);
     const uint4 h1 = *reinterpret_cast<const uint4*>(hist + 8 * c + 4);
     const sk_u32x4 w = {h0.x | (h0.y << 16), h0.z | (h0.w << 16), h1.x | (h1.y << 16),
@@ -363,28 +379,29 @@ __device__ __forceinline__ int split_merge(const uint32_t* magic, uint32_t* __re
   }
   __syncthreads();
   if (flag[0] != 1) return flag[0];
-  // thread t owns chunks t, t + SK_NT, t + 2 SK_NT (SK_SPLIT_CHUNKS <= 3 SK_NT)
-  static_assert(SK_SPLIT_CHUNKS <= 3 * SK_NT, "chunks per thread");
-  uint32_t acc[3][8];
+  // thread t owns chunks t, t + NT, ... (KC of them)
+  constexpr int KC = (SK_SPLIT_CHUNKS + NT - 1) / NT;
+  static_assert(KC >= 1 && KC <= 3, "chunks per thread");
+  uint32_t acc[KC][8];
 #pragma unroll
-  for (int k = 0; k < 3; ++k)
+  for (int k = 0; k < KC; ++k)
 #pragma unroll
     for (int t = 0; t < 8; ++t) acc[k][t] = 0u;
   uint32_t om = *omx, cc = *cp;
   for (int o = 0; o < P; ++o) {  // uniform
     if (o == part) continue;
     const int so = o * (int)SK_SPLIT_BYTES;
-    sk_u32x4 x[3];
+    sk_u32x4 x[KC];
 #pragma unroll
-    for (int k = 0; k < 3; ++k) {  // clamped: every thread loads, unowned chunks unused
-      const int c = min(tid + k * SK_NT, SK_SPLIT_CHUNKS - 1);
+    for (int k = 0; k < KC; ++k) {  // clamped: every thread loads, unowned chunks unused
+      const int c = min(tid + k * NT, SK_SPLIT_CHUNKS - 1);
       x[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, c * 16, so, SK_SC1);
     }
     const sk_u32x4 h = __builtin_amdgcn_raw_buffer_load_b128(rsrc, SK_SPLIT_CHUNKS * 16, so, SK_SC1);
     om = max(om, h[0]);
     cc += h[1];
 #pragma unroll
-    for (int k = 0; k < 3; ++k)
+    for (int k = 0; k < KC; ++k)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         acc[k][2 * j] += x[k][j] & 0xFFFFu;
@@ -392,8 +409,8 @@ __device__ __forceinline__ int split_merge(const uint32_t* magic, uint32_t* __re
       }
   }
 #pragma unroll
-  for (int k = 0; k < 3; ++k) {
-    const int c = tid + k * SK_NT;
+  for (int k = 0; k < KC; ++k) {
+    const int c = tid + k * NT;
     if (c < SK_SPLIT_CHUNKS) {
 #pragma unroll
       for (int t = 0; t < 8; ++t) hist[8 * c + t] += acc[k][t];
@@ -407,16 +424,18 @@ __device__ __forceinline__ int split_merge(const uint32_t* magic, uint32_t* __re
 
 // All LDS of the kernel in one object, histogram first (LDS address 0, so the
 // streaming atomics address it by byte offset alone).
-struct SkLds {
+template <int NT>
+struct SkLdsT {
   uint32_t hist[SK_SPLIT_CHUNKS * 8];  // SK_NB bins, zero padding to whole chunks
   float etop[SK_ETOP];  // exp values of the top SK_ETOP bins (bmax - i); occupied ones only
-  uint32_t zq[SK_NW][SK_ZQ];  // per-wave queues of occupied bins for the normaliser
-  SkRed red;
+  uint32_t zq[NT / kWave][SK_ZQ];  // per-wave queues of occupied bins for the normaliser
+  SkRedT<NT / kWave> red;
   int32_t i32[12];
   int32_t pw[5];  // top-p walk of wave 0: boundary bin (or -1), its group bins and counts
   uint64_t x64[2];
   uint32_t unit_ctr;  // next 4 KB unit of the row to stream
 };
+using SkLds = SkLdsT<SK_NT>;
 
 // Outputs of a row: plain stores, or device-coherent ones (agent-scope atomic
 // stores, which no XCD's L2 keeps back) when the draw that reads them runs in
@@ -450,8 +469,9 @@ __device__ __forceinline__ int64_t jm_row(int64_t q, int32_t k, int64_t ntgt) {
 // One block's share of the row statistics (block blk of the launch). Returns
 // the row whose statistics this block completed (written), or -1 (a split
 // row's part that did not merge).
-template <bool FUSED>
-__device__ __forceinline__ int64_t rowstream_body(const RowStatArgs& a, SkLds& L, int64_t blk) {
+template <bool FUSED, int NT = SK_NT>
+__device__ __forceinline__ int64_t rowstream_body(const RowStatArgs& a, SkLdsT<NT>& L,
+                                                  int64_t blk) {
   uint32_t* const hist = L.hist;
   int rs = 0;
 
@@ -483,7 +503,7 @@ __device__ __forceinline__ int64_t rowstream_body(const RowStatArgs& a, SkLds& L
   if (tid == 0 && part <= 0 && row < a.nzero) a.zero[row] = 0u;
   if (tid == 0 && part <= 0 && a.rank_acc) a.rank_acc[row] = 0ull;
 
-  for (int b = tid; b < SK_SPLIT_CHUNKS * 8; b += SK_NT) hist[b] = 0u;
+  for (int b = tid; b < SK_SPLIT_CHUNKS * 8; b += NT) hist[b] = 0u;
   if (tid == 0) L.unit_ctr = 0u;
   __syncthreads();
 
@@ -631,7 +651,7 @@ __device__ __forceinline__ int64_t rowstream_body(const RowStatArgs& a, SkLds& L
     uint32_t cp = 0;
     if (g_in_groups || g_in_tail) cp = snap + blk_sum_u32(pre, L.red, rs);
     else if (has_g && gid >= (int64_t)g1 * 8) cp = hist[bin_g];
-    const int mg = split_merge(a.ws_header, a.split_cnt, a.split_parts, P, sidx, part, hist,
+    const int mg = split_merge<NT>(a.ws_header, a.split_cnt, a.split_parts, P, sidx, part, hist,
                                &omx_b, &cp, L.i32 + 11);
     if (mg == 2 && part == 0 && tid == 0) {  // uninitialised workspace: flag the row
       RowStat st = {};
@@ -702,9 +722,9 @@ __device__ __forceinline__ int64_t rowstream_body(const RowStatArgs& a, SkLds& L
       below_lo = bm.lo;
       below_mass = false;
       __syncthreads();
-      for (int b = tid; b < SK_NB; b += SK_NT) hist[b] = 0u;
+      for (int b = tid; b < SK_NB; b += NT) hist[b] = 0u;
       __syncthreads();
-      restream_anchored(ptr, V, bm, hist);
+      restream_anchored<NT>(ptr, V, bm, hist);
       __syncthreads();
       if (bm.lo > 0 && hist[0] != 0 && exp_det(sk_d(bm.lo - 1, invT, m)) > 0.0f) {
         below_top = key_extremes(ptr, V, bm.lo, 1u, 0u, invT, m, L.red, rs).below_max;
@@ -717,7 +737,7 @@ __device__ __forceinline__ int64_t rowstream_body(const RowStatArgs& a, SkLds& L
   auto e_of_bin = [&](int b) -> float { return exp_det(sk_d(bm.key_rep(b), invT, m)); };
 
   // ---- 3. exact normaliser: sum c * fixed62(e) as sum c * lo32 + 2^32 sum c * hi32
-  // (sum c <= V < 2^31 keeps both below 2^63). Thread t reads bins bmax - t - j*SK_NT;
+  // (sum c <= V < 2^31 keeps both below 2^63). Thread t reads bins bmax - t - j*NT;
   // each wave queues its occupied bins as (bin << 18 | count) in LDS and
   // evaluates them 128 at a time, two independent exp evaluations per lane
   // (sparse stretches of the window cost no idle lanes). The top SK_ETOP bins'
@@ -739,17 +759,17 @@ __device__ __forceinline__ int64_t rowstream_body(const RowStatArgs& a, SkLds& L
       slo += (uint64_t)c0 * (uint32_t)f0 + (uint64_t)c1 * (uint32_t)f1;
       shi += (uint64_t)c0 * (uint32_t)(f0 >> 32) + (uint64_t)c1 * (uint32_t)(f1 >> 32);
     };
-    const int nround = bmax >= 1 ? (bmax - 1) / SK_NT + 1 : 0;
+    const int nround = bmax >= 1 ? (bmax - 1) / NT + 1 : 0;
     for (int j0 = 0; j0 < nround; j0 += 4) {
       uint32_t cc[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int b = bmax - tid - SK_NT * (j0 + u);
+        const int b = bmax - tid - NT * (j0 + u);
         cc[u] = b >= 1 ? hist[b] : 0u;
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int b = bmax - tid - SK_NT * (j0 + u);
+        const int b = bmax - tid - NT * (j0 + u);
         const uint64_t mk = __ballot(cc[u] != 0);
         const uint32_t below = __builtin_amdgcn_mbcnt_hi(
             (uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u));
@@ -788,7 +808,7 @@ __device__ __forceinline__ int64_t rowstream_body(const RowStatArgs& a, SkLds& L
   if (a.use_k) {
     uint32_t before = 0;
     int kb = -1;
-    for (int top = bmax; top >= 1; top -= SK_NT) {
+    for (int top = bmax; top >= 1; top -= NT) {
       const int b = top - tid;
       const uint32_t c = b >= 1 ? hist[b] : 0u;
       uint32_t tot;
@@ -844,7 +864,7 @@ __device__ __forceinline__ int64_t rowstream_body(const RowStatArgs& a, SkLds& L
     // every lane the mass above its bins, and every bin's keep test follows with
     // no further dependence. A nucleus of a few hundred values ends here in one
     // or two scans, and the other blocks on the CU keep their issue slots. Past
-    // them the block takes over in rounds of SK_NT bins.
+    // them the block takes over in rounds of NT bins.
     constexpr int PJ = 4;  // bins per lane and chunk (more spills at this register budget)
     static_assert(SK_PW % (PJ * kWave) == 0, "whole chunks");
     if (tid < kWave) {
@@ -925,7 +945,7 @@ __device__ __forceinline__ int64_t rowstream_body(const RowStatArgs& a, SkLds& L
     } else {
       S = L.x64[0];
     }
-    for (int top = bmax - SK_PW; bb < 0 && top >= klo_bin; top -= SK_NT) {
+    for (int top = bmax - SK_PW; bb < 0 && top >= klo_bin; top -= NT) {
       const int b = top - tid;
       const uint32_t c = b >= klo_bin ? hist[b] : 0u;
       const float p = c ? p_of_bin(b) : 0.0f;
@@ -1028,7 +1048,7 @@ __device__ __forceinline__ int64_t rowstream_body(const RowStatArgs& a, SkLds& L
   const bool keep_below = !k_cut && !has_group;
   if (!a.use_p) {  // no nucleus: the kept mass is every bin from klo_bin up
     uint64_t acc = 0;
-    for (int b = bmax - tid; b >= klo_bin; b -= SK_NT) {
+    for (int b = bmax - tid; b >= klo_bin; b -= NT) {
       const uint32_t c = hist[b];
       if (c) acc += (uint64_t)c * fixed62(p_of_bin(b));
     }
@@ -1045,7 +1065,7 @@ __device__ __forceinline__ int64_t rowstream_body(const RowStatArgs& a, SkLds& L
   // ---- 6. table of final probabilities for the top keys
   const int32_t tbl_lo = max(klo, (int32_t)kmax - (kTbl - 1));
   const int32_t ntbl = (int32_t)kmax - tbl_lo + 1;
-  for (int t = tid; t < ntbl; t += SK_NT) {
+  for (int t = tid; t < ntbl; t += NT) {
     const uint32_t kk = kmax - (uint32_t)t;
     const int b = bm.bin(kk);
     float v;
