@@ -11,9 +11,10 @@
 // first (all whole chunks, then the rows' last partial chunks by decreasing
 // size), each with its row's shape, so the hardware's in-order dispatch ends on
 // the shortest work and a workgroup learns everything about its chunk in one
-// load; the KV heads of a chunk are adjacent workgroups and stream the same
-// page rows together. A workgroup's query rows are the q_b positions x group
-// heads that share the KV head (q_b * group <= 64, padded to 16-row MFMA
+// load; the KV heads of a chunk run on one XCD (workgroup index % 8) and stream
+// the same page rows together, so each token's 2 KB row is read as eight
+// 256-byte slices close in time. A workgroup's query rows are the q_b positions
+// x group heads that share the KV head (q_b * group <= 64, padded to 16-row MFMA
 // tiles; wave w owns rows 16w .. 16w + 15). The chunk's token -> pool slot map
 // is built in LDS once from the block table (read alongside the row's shape);
 // its keys then stream through LDS
@@ -195,8 +196,13 @@ verify_attn_kernel(AttnArgs a) {
   __shared__ int64_t sRow[VA_MAXM];  // query row i -> element offset of its q / out vector
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
-  const int kvh = (int)(blockIdx.x % a.hkv);
-  const AttnUnit un = a.units[blockIdx.x / a.hkv];
+  // a chunk's KV heads on one XCD (workgroup % 8): blocks 8 hkv g .. cover chunks
+  // 8g .. 8g + 7, chunk 8g + x's head h at 8 hkv g + 8 h + x
+  const int64_t grp = blockIdx.x / (8 * a.hkv), rem = blockIdx.x % (8 * a.hkv);
+  const int kvh = (int)(rem / 8);
+  const int64_t unit = 8 * grp + rem % 8;
+  if (unit >= a.nunits) return;
+  const AttnUnit un = a.units[unit];
   if (un.b < 0) return;  // uniform: no chunk in this slot
   const int64_t b = un.b, q0 = un.q0, qb = un.qb, kvl = un.kvl;
   const int c = un.c, n = un.n;
@@ -509,7 +515,8 @@ hipError_t launch_verify_attn(const AttnArgs& a, int64_t batch, hipStream_t s) {
   hipLaunchKernelGGL(verify_attn_plan_kernel, dim3(1), dim3(VA_PLAN_NT), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(verify_attn_kernel, dim3((unsigned)(a.nunits * a.hkv)), dim3(VA_NT), 0, s, a);
+  hipLaunchKernelGGL(verify_attn_kernel, dim3((unsigned)((a.nunits + 7) / 8 * 8 * a.hkv)),
+                     dim3(VA_NT), 0, s, a);
   e = hipGetLastError();
   if (e != hipSuccess || a.nchunk == 1) return e;
   hipLaunchKernelGGL(verify_attn_merge_kernel, dim3((unsigned)(batch * a.hkv)), dim3(VA_NT), 0, s, a);
