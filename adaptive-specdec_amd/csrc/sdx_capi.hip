@@ -180,6 +180,8 @@ int sdx_to_probs(const void* logits, int dtype, int64_t rows, int64_t vocab, int
   a.T = temperature; a.top_p = top_p; a.top_k = top_k;
   a.use_p = sw.use_p; a.use_k = sw.use_k; a.greedy = sw.greedy;
   a.stats = st; a.tables = tb;
+  // the output kernel's per-chunk member counts start at zero in every call
+  a.zero = counts; a.nzero = rows; a.zero_per_row = nchunk;
   if (int e = row_stats16(dtype, a, rows, s)) return e;
   sdx::RowSource16 src{(const uint16_t*)logits, ld, (const uint16_t*)logits, ld, rows, true};
   return hip_status(sdx::launch_materialize16(dtype, src, st, tb, temperature, rows, vocab, chunk,

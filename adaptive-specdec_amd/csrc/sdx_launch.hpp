@@ -37,8 +37,9 @@ struct RowStatArgs {
   int32_t use_p, use_k, greedy;
   RowStat* stats;
   float* tables;  // [rows, kTbl]
-  uint32_t* zero;  // words [0, nzero) cleared (block `row` clears word `row`), or null
-  int64_t nzero;
+  uint32_t* zero;  // rows [0, nzero) of zero_per_row words (0 meaning 1) cleared by the
+  int64_t nzero;   // block of the row, or null
+  int32_t zero_per_row;
   uint64_t* rank_acc;  // [rows] rank accumulators, cleared by the row kernel, or null
   int64_t late_block;  // bf16 streaming kernel: blocks from here stream at raised wave
                        // priority (set by launch_rowstream_bf16)

@@ -97,7 +97,10 @@ __global__ void __launch_bounds__(RS_NT) rowstat16_kernel(RowStatArgs a) {
   const int64_t we = min(V, wb + cw);
   RowStat* st_out = a.stats + row;
   float* tbl_out = a.tables + row * kTbl;
-  if (tid == 0 && row < a.nzero) a.zero[row] = 0u;
+  if (row < a.nzero) {
+    const int zpr = a.zero_per_row > 0 ? a.zero_per_row : 1;
+    if (tid < zpr) a.zero[row * zpr + tid] = 0u;
+  }
 
   // Element (j, t) of this lane is id wb + j*512 + lane*8 + t; it exists iff
   // j*512 + t < rem. All per-slot checks compare one register with constants.

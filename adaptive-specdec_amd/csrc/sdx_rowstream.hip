@@ -500,7 +500,10 @@ __device__ __forceinline__ int64_t rowstream_body(const RowStatArgs& a, SkLdsT<N
   const int64_t V = a.V;
   RowStat* st_out = a.stats + row;
   float* tbl_out = a.tables + row * kTbl;
-  if (tid == 0 && part <= 0 && row < a.nzero) a.zero[row] = 0u;
+  if (part <= 0 && row < a.nzero) {
+    const int zpr = a.zero_per_row > 0 ? a.zero_per_row : 1;
+    if (tid < zpr) a.zero[row * zpr + tid] = 0u;
+  }
   if (tid == 0 && part <= 0 && a.rank_acc) a.rank_acc[row] = 0ull;
 
   for (int b = tid; b < SK_SPLIT_CHUNKS * 8; b += NT) hist[b] = 0u;

@@ -615,18 +615,26 @@ draw16_kernel(Draw16Args<FMT> a) {
 
 // ---------------------------------------------------------------- to_probs output
 // Rows are cut into chunks of kMatRounds block rounds (SM_ROUND ids each), one
-// workgroup each. A row whose boundary tie group is partially kept needs, in
-// every chunk, the number of group members before it (members are kept lowest
-// ids first): one pass counts them per chunk, then the output pass writes the
-// chunk.
+// workgroup each, which writes the chunk's probabilities. A row whose boundary
+// tie group is partially kept needs, in every chunk, the number of group members
+// before it (members are kept lowest ids first). One pass does both, with a
+// decoupled look-back: each workgroup counts the members of its chunk from the
+// codes it has loaded anyway, publishes the count (bit 31 marks it published),
+// then sums the counts of the row's earlier chunks as they appear. The words are
+// cleared by the row statistics kernel of the same call (zero_per_row = nchunk).
+// The wait ends: a chunk waits only for chunks of lower workgroup index, which
+// are dispatched before it and publish before they wait. It is bounded all the
+// same (kMatWaitTicks of the 100 MHz counter); a chunk that gives up writes NaN.
 constexpr int kMatRounds = (int)(kMatChunk / SM_ROUND);
 static_assert(kMatChunk % SM_ROUND == 0, "whole block rounds per chunk");
+constexpr uint64_t kMatWaitTicks = 2000000;  // 20 ms
+constexpr uint32_t kMatPublished = 0x80000000u;
 
 struct MaterializeArgs {
   int64_t V;
   int64_t chunk;     // ids per chunk, kMatRounds * SM_ROUND
   int32_t nchunk;
-  uint32_t* counts;  // [rows, nchunk] group members per chunk (partial rows only)
+  uint32_t* counts;  // [rows, nchunk] group members per chunk | kMatPublished
   float* out;
   int64_t ld_out;
   bool vec_out;      // out 16-byte aligned and ld_out % 4 == 0
@@ -637,61 +645,10 @@ __device__ __forceinline__ bool partial_group(const RowStat& st) {
 }
 
 template <int FMT>
-__global__ void __launch_bounds__(SM_NT) member_count_kernel(Eval16<FMT> ev, MaterializeArgs a) {
-  __shared__ uint32_t red[SM_NW];
-  const int64_t row = (int64_t)blockIdx.x / a.nchunk;
-  const int64_t cidx = (int64_t)blockIdx.x % a.nchunk;
-  const RowStat st = ev.stats[row];
-  if (!partial_group(st)) return;
-  const uint16_t* ptr = row < ev.split ? ev.base + row * ev.ld : ev.base2 + (row - ev.split) * ev.ld2;
-  const int64_t c0 = cidx * a.chunk;
-  const int64_t c1 = min(a.V, c0 + a.chunk);
-  uint4 raw[kMatRounds];
-#pragma unroll
-  for (int u = 0; u < kMatRounds; ++u) {  // every load in flight before any count
-    const int64_t idx = c0 + (int64_t)u * SM_ROUND + (int64_t)threadIdx.x * 8;
-    raw[u] = idx + 8 <= c1 ? *reinterpret_cast<const uint4*>(ptr + idx) : make_uint4(0, 0, 0, 0);
-  }
-  // whole 8-id groups on packed keys: key - glo (mod 2^16) is at most ghi - glo
-  // exactly for a member (a partial group is not empty), so the saturating
-  // (ghi - glo + 1) - (key - glo), capped at 1, is 1 for a member and 0 otherwise
-  typedef unsigned short mc_us2 __attribute__((ext_vector_type(2)));
-  const mc_us2 glo2 = {(unsigned short)st.glo, (unsigned short)st.glo};
-  const mc_us2 span2 = {(unsigned short)(st.ghi - st.glo + 1), (unsigned short)(st.ghi - st.glo + 1)};
-  mc_us2 pk = {0, 0};  // per half at most 4 x 8 members
-  uint32_t cnt = 0;
-#pragma unroll
-  for (int u = 0; u < kMatRounds; ++u) {
-    const int64_t idx = c0 + (int64_t)u * SM_ROUND + (int64_t)threadIdx.x * 8;
-    const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
-    if (idx + 8 <= c1) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const mc_us2 d = __builtin_bit_cast(mc_us2, keys2_of_codes2(w[t])) - glo2;
-        pk += __builtin_elementwise_min(__builtin_elementwise_sub_sat(span2, d), (mc_us2){1, 1});
-      }
-    } else {
-      for (int64_t i = idx; i < c1; ++i) {  // the row's last ids (V % 8)
-        const int32_t kk = (int32_t)key_of_code16(ptr[i]);
-        cnt += (kk >= st.glo && kk <= st.ghi) ? 1u : 0u;
-      }
-    }
-  }
-  cnt += (uint32_t)pk[0] + (uint32_t)pk[1];
-  cnt = wave_sum_u32(cnt);
-  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = cnt;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t t = 0;
-    for (int w = 0; w < SM_NW; ++w) t += red[w];
-    a.counts[row * a.nchunk + cidx] = t;
-  }
-}
-
-template <int FMT>
 __global__ void __launch_bounds__(SM_NT) materialize16_kernel(Eval16<FMT> ev, MaterializeArgs a) {
   __shared__ float tbl[kTbl];
   __shared__ uint32_t s32[SM_NW];
+  __shared__ int32_t s_fail;
   const int64_t row = (int64_t)blockIdx.x / a.nchunk;
   const int64_t cidx = (int64_t)blockIdx.x % a.nchunk;
   const int64_t c0 = cidx * a.chunk;
@@ -706,19 +663,70 @@ __global__ void __launch_bounds__(SM_NT) materialize16_kernel(Eval16<FMT> ev, Ma
     raw[u] = idx < c1 ? ev.fetch(r, idx, c1) : make_uint4(0, 0, 0, 0);
   }
   ev.stage(row, tbl);
+  if (threadIdx.x == 0) s_fail = 0;
   __syncthreads();
   ev.bind(r, row, tbl);
   float* o = a.out + row * a.ld_out;
+  const bool part = partial_group(r.st);
+  uint32_t* const cnt_row = a.counts + row * a.nchunk;
+  if (part) {  // uniform: this chunk's members, published before anything waits
+    // whole 8-id groups on packed keys: key - glo (mod 2^16) is at most ghi - glo
+    // exactly for a member (a partial group is not empty), so the saturating
+    // (ghi - glo + 1) - (key - glo), capped at 1, is 1 for a member and 0 otherwise;
+    // the padding of fetch() past the row's end (code 0xFFFF, key 0) is no member
+    typedef unsigned short mc_us2 __attribute__((ext_vector_type(2)));
+    const mc_us2 glo2 = {(unsigned short)r.st.glo, (unsigned short)r.st.glo};
+    const mc_us2 span2 = {(unsigned short)(r.st.ghi - r.st.glo + 1),
+                          (unsigned short)(r.st.ghi - r.st.glo + 1)};
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int u = 0; u < kMatRounds; ++u) {
+      const int64_t idx = c0 + (int64_t)u * SM_ROUND + (int64_t)threadIdx.x * 8;
+      if (idx < c1) {
+        mc_us2 pk = {0, 0};
+        const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const mc_us2 d = __builtin_bit_cast(mc_us2, keys2_of_codes2(w[t])) - glo2;
+          pk += __builtin_elementwise_min(__builtin_elementwise_sub_sat(span2, d), (mc_us2){1, 1});
+        }
+        cnt += (uint32_t)pk[0] + (uint32_t)pk[1];
+      }
+    }
+    uint32_t tot;
+    block_excl_u32(cnt, s32, &tot);
+    if (threadIdx.x == 0)
+      __hip_atomic_store(cnt_row + cidx, tot | kMatPublished, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
   if (r.st.flags & kRowUnsupported) {  // outside the row kernel's windows: mark, don't guess
     for (int64_t i = c0 + threadIdx.x; i < c1; i += SM_NT) o[i] = __builtin_nanf("");
     return;
   }
-  const bool part = partial_group(r.st);
   uint32_t rank = 0;
-  if (part) {  // members in earlier chunks
+  if (part) {  // uniform: members in earlier chunks, as they are published
     uint32_t v = 0;
-    for (int64_t c = threadIdx.x; c < cidx; c += SM_NT) v += a.counts[row * a.nchunk + c];
+    for (int64_t c = threadIdx.x; c < cidx; c += SM_NT) {
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      for (;;) {
+        const uint32_t w =
+            __hip_atomic_load(cnt_row + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (w & kMatPublished) {
+          v += w & ~kMatPublished;
+          break;
+        }
+        if (__builtin_amdgcn_s_memrealtime() - t0 > kMatWaitTicks) {
+          s_fail = 1;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
     block_excl_u32(v, s32, &rank);
+    if (s_fail) {  // uniform (read after the scan's barrier)
+      for (int64_t i = c0 + threadIdx.x; i < c1; i += SM_NT) o[i] = __builtin_nanf("");
+      return;
+    }
   }
 #pragma unroll
   for (int u = 0; u < kMatRounds; ++u) {
@@ -999,11 +1007,9 @@ hipError_t launch_materialize16(int fmt, const RowSource16& src, const RowStat* 
   const dim3 grid((unsigned)(nchunk * rows));
   if (fmt == SDX_BF16) {
     Eval16<SDX_BF16> ev{src.base, src.ld, src.base2, src.ld2, src.split, stats, tables, T};
-    hipLaunchKernelGGL((member_count_kernel<SDX_BF16>), grid, dim3(SM_NT), 0, s, ev, ma);
     hipLaunchKernelGGL((materialize16_kernel<SDX_BF16>), grid, dim3(SM_NT), 0, s, ev, ma);
   } else {
     Eval16<SDX_F16> ev{src.base, src.ld, src.base2, src.ld2, src.split, stats, tables, T};
-    hipLaunchKernelGGL((member_count_kernel<SDX_F16>), grid, dim3(SM_NT), 0, s, ev, ma);
     hipLaunchKernelGGL((materialize16_kernel<SDX_F16>), grid, dim3(SM_NT), 0, s, ev, ma);
   }
   return hipGetLastError();
