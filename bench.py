@@ -381,7 +381,7 @@ def bench_probs(args, torch):
     ach_tp = alg_tp / (ms_tp_call / 1e3) / 1e9
     ach_sp = alg_sp / (ms_sp / 1e3) / 1e9
     lname = "f32" if f32 else "bf16"
-    kname = "to_probs_f32_big_kernel" if f32 else "rowstream + member_count + materialize16"
+    kname = "to_probs_f32_big_kernel" if f32 else "rowstream + materialize16"
     return {"metric": f"to_probs + sample_from_probs, 256 x 151936 {lname} logits, GB/s",
             "value": round((alg_tp + alg_sp) / ((ms_tp_call + ms_sp) / 1e3) / 1e9, 1),
             "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
