@@ -22,6 +22,7 @@
 // 16-bit logits, or dense fp32 probability rows (which have no groups).
 #include "sdx_draw16.hpp"
 
+#include <cstdlib>
 #include <type_traits>
 
 namespace sdx {
@@ -624,7 +625,8 @@ draw16_kernel(Draw16Args<FMT> a) {
 // cleared by the row statistics kernel of the same call (zero_per_row = nchunk).
 // The wait ends: a chunk waits only for chunks of lower workgroup index, which
 // are dispatched before it and publish before they wait. It is bounded all the
-// same (kMatWaitTicks of the 100 MHz counter); a chunk that gives up writes NaN.
+// same (kMatWaitTicks of the 100 MHz counter, or the smaller bound the launcher
+// passes); a chunk that gives up writes NaN.
 constexpr int kMatRounds = (int)(kMatChunk / SM_ROUND);
 static_assert(kMatChunk % SM_ROUND == 0, "whole block rounds per chunk");
 constexpr uint64_t kMatWaitTicks = 2000000;  // 20 ms
@@ -638,6 +640,7 @@ struct MaterializeArgs {
   float* out;
   int64_t ld_out;
   bool vec_out;      // out 16-byte aligned and ld_out % 4 == 0
+  uint64_t wait_ticks;  // look-back bound, at most kMatWaitTicks
 };
 
 __device__ __forceinline__ bool partial_group(const RowStat& st) {
@@ -715,7 +718,7 @@ __global__ void __launch_bounds__(SM_NT) materialize16_kernel(Eval16<FMT> ev, Ma
           v += w & ~kMatPublished;
           break;
         }
-        if (__builtin_amdgcn_s_memrealtime() - t0 > kMatWaitTicks) {
+        if (__builtin_amdgcn_s_memrealtime() - t0 > a.wait_ticks) {
           s_fail = 1;
           break;
         }
@@ -996,6 +999,18 @@ hipError_t launch_chunk_mass_probs(const RowSourceF32& src, SampleJob* jobs, int
   return launch_draw(ev, nullptr, jobs, njobs, V, recs, nullptr, nullptr, s);
 }
 
+// The look-back bound: kMatWaitTicks, or a smaller bound from SDX_PROBS_WAIT_TICKS
+// (read at every launch; tests set 0 so that a chunk whose earlier chunks have not
+// all published at its first poll gives up, while every kernel exits normally).
+static uint64_t mat_wait_ticks() {
+  const char* e = getenv("SDX_PROBS_WAIT_TICKS");
+  if (!e || !*e) return kMatWaitTicks;
+  char* end = nullptr;
+  const unsigned long long v = strtoull(e, &end, 10);
+  if (!end || *end != '\0') return kMatWaitTicks;
+  return v < kMatWaitTicks ? (uint64_t)v : kMatWaitTicks;
+}
+
 hipError_t launch_materialize16(int fmt, const RowSource16& src, const RowStat* stats,
                                 const float* tables, float T, int64_t rows, int64_t V,
                                 int64_t chunk, int nchunk, uint32_t* counts, float* out,
@@ -1003,7 +1018,7 @@ hipError_t launch_materialize16(int fmt, const RowSource16& src, const RowStat* 
   if (!src.vec) return hipErrorInvalidValue;
   if (chunk != (int64_t)kMatRounds * SM_ROUND) return hipErrorInvalidValue;
   MaterializeArgs ma{V, chunk, nchunk, counts, out, ld_out,
-                     ((uintptr_t)out & 15u) == 0 && (ld_out % 4) == 0};
+                     ((uintptr_t)out & 15u) == 0 && (ld_out % 4) == 0, mat_wait_ticks()};
   const dim3 grid((unsigned)(nchunk * rows));
   if (fmt == SDX_BF16) {
     Eval16<SDX_BF16> ev{src.base, src.ld, src.base2, src.ld2, src.split, stats, tables, T};

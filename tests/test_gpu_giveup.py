@@ -58,3 +58,51 @@ def test_wait_give_up_flags_then_marks_workspace():
     v.reset_workspace()
     n3, y3, f3 = _run(v, inp)
     assert np.array_equal(n3, rn) and np.array_equal(y3, ry) and np.array_equal(f3, rf)
+
+
+CHUNK = 16384  # ids per to_probs output chunk (the output kernel's workgroup)
+
+
+def _probs_chunks_exact_or_nan(got, ref):
+    """Every output chunk equals the oracle bit for bit or is NaN throughout."""
+    given_up = 0
+    for r in range(got.shape[0]):
+        for c0 in range(0, got.shape[1], CHUNK):
+            g, e = got[r, c0:c0 + CHUNK], ref[r, c0:c0 + CHUNK]
+            nan = np.isnan(g)
+            if nan.all():
+                given_up += 1
+                continue
+            assert not nan.any(), f"row {r} chunk {c0 // CHUNK} partly NaN"
+            assert np.array_equal(g.view(np.uint32), e.view(np.uint32)), \
+                f"row {r} chunk {c0 // CHUNK} differs"
+    return given_up
+
+
+@pytest.mark.parametrize("case", ["zipf", "one_group"])
+def test_to_probs_look_back_give_up(case):
+    """SDX_PROBS_WAIT_TICKS=0: an output chunk whose row has a partly kept tie group
+    polls the earlier chunks' member counts once and gives up (NaN) if one is not
+    yet published. Each chunk is then exact or NaN; the next call is exact."""
+    from specdec import sampling as S
+    from specdec.workloads import zipf_logits
+    V, T, tp = 151936, 0.8, 0.95
+    if case == "zipf":
+        g = torch.Generator(device=DEV).manual_seed(5)
+        x = zipf_logits(64, V, g, DEV)
+    else:  # one tie group over the whole row, cut by top-p: every chunk holds members
+        x = torch.zeros((16, V), dtype=torch.bfloat16, device=DEV)
+        tp = 0.5
+    print(f"[giveup] to_probs {case} rows={x.shape[0]} V={V}", flush=True)
+    ref = O.to_probs(_np(x), T, tp, 0)
+    os.environ["SDX_PROBS_WAIT_TICKS"] = "0"
+    try:
+        got = _np(S.to_probs(x, T, tp, 0))
+        torch.cuda.synchronize()
+    finally:
+        del os.environ["SDX_PROBS_WAIT_TICKS"]
+    n = _probs_chunks_exact_or_nan(got, ref)
+    print(f"[giveup] chunks given up: {n}", flush=True)
+    assert n > 0, "no chunk gave up at a zero wait bound"
+    got2 = _np(S.to_probs(x, T, tp, 0))
+    assert _probs_chunks_exact_or_nan(got2, ref) == 0
