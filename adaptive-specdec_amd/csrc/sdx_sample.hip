@@ -647,10 +647,14 @@ __device__ __forceinline__ bool partial_group(const RowStat& st) {
   return st.rstar > 0 && st.rstar < st.gcount;
 }
 
+typedef unsigned short mat_us2 __attribute__((ext_vector_type(2)));
+static_assert(kMatRounds <= 8, "member counts of a chunk's rounds: two 64-bit scans of 16-bit fields");
+
 template <int FMT>
 __global__ void __launch_bounds__(SM_NT) materialize16_kernel(Eval16<FMT> ev, MaterializeArgs a) {
-  __shared__ float tbl[kTbl];
+  __shared__ float tbl[kTbl + 1];  // + the "not kept" entry of the one-lookup form
   __shared__ uint32_t s32[SM_NW];
+  __shared__ uint64_t s64[SM_NW];
   __shared__ int32_t s_fail;
   const int64_t row = (int64_t)blockIdx.x / a.nchunk;
   const int64_t cidx = (int64_t)blockIdx.x % a.nchunk;
@@ -730,6 +734,95 @@ __global__ void __launch_bounds__(SM_NT) materialize16_kernel(Eval16<FMT> ev, Ma
       for (int64_t i = c0 + threadIdx.x; i < c1; i += SM_NT) o[i] = __builtin_nanf("");
       return;
     }
+  }
+  // One lookup per id, for rows whose kept keys [klo, kmax] all lie in the table
+  // (nearly every row; klo >= 1 keeps key 0, the padding past the row's end, out):
+  // entry kmax - key holds the output of a kept non-member, the group's entries
+  // hold the output of a kept member (its value, or 0 when no member is kept),
+  // and entry Z = kmax - klo + 1, where every key below klo lands, holds 0. Packed
+  // 16-bit: index = min(sat(kmax - key), Z) for two ids at once. Outputs equal
+  // eval()'s: live ids take tbl[kmax - key] or the group value, the others 0.
+  const int32_t kmax = r.st.kmax, klo = r.st.klo;
+  if ((r.st.flags & kRowNonfinite) == 0 && klo >= 1 && klo <= kmax &&
+      kmax - klo <= r.st.ntbl - 1) {  // uniform
+    const int32_t Z = kmax - klo + 1;
+    const int32_t gl = max(r.st.glo, klo), gh = min(r.st.ghi, kmax);
+    const float bv = r.st.rstar <= 0 ? 0.0f : r.vg;
+    __syncthreads();  // every bind() has read the table
+    for (int32_t e = kmax - gh + (int32_t)threadIdx.x; e <= kmax - gl; e += SM_NT) tbl[e] = bv;
+    if (threadIdx.x == 0) tbl[Z] = 0.0f;
+    // member ranks (a partially kept group): bits per round, then two block scans
+    // of the per-thread counts packed four rounds to a 64-bit word (16-bit fields:
+    // a round holds at most SM_ROUND members)
+    uint32_t mk[kMatRounds];
+    uint64_t ea = 0, eb = 0, ta = 0, tb = 0;
+    if (part) {  // uniform
+      const mat_us2 gl2 = {(unsigned short)gl, (unsigned short)gl};
+      const mat_us2 sp2 = {(unsigned short)(gh - gl + 1), (unsigned short)(gh - gl + 1)};
+      uint64_t ca = 0, cb = 0;
+#pragma unroll
+      for (int u = 0; u < kMatRounds; ++u) {
+        const int64_t idx = c0 + (int64_t)u * SM_ROUND + (int64_t)threadIdx.x * 8;
+        uint32_t m = 0;
+        if (idx < c1) {
+          const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const mat_us2 d = __builtin_bit_cast(mat_us2, keys2_of_codes2(w[i])) - gl2;
+            const mat_us2 b = __builtin_elementwise_min(__builtin_elementwise_sub_sat(sp2, d),
+                                                        (mat_us2){1, 1});
+            m |= ((uint32_t)b[0] << (2 * i)) | ((uint32_t)b[1] << (2 * i + 1));
+          }
+        }
+        mk[u] = m;
+        if (u < 4) ca |= (uint64_t)__popc(m) << (16 * u);
+        else cb |= (uint64_t)__popc(m) << (16 * (u - 4));
+      }
+      ea = block_excl_u64(ca, s64, &ta);  // (its barriers also order the table's patch)
+      eb = block_excl_u64(cb, s64, &tb);
+    } else {
+      __syncthreads();
+    }
+    const mat_us2 kmax2 = {(unsigned short)kmax, (unsigned short)kmax};
+    const mat_us2 z2 = {(unsigned short)Z, (unsigned short)Z};
+    uint32_t base = rank;
+#pragma unroll
+    for (int u = 0; u < kMatRounds; ++u) {
+      const int64_t r0 = c0 + (int64_t)u * SM_ROUND;
+      if (r0 >= c1) break;  // uniform
+      const int64_t idx = r0 + (int64_t)threadIdx.x * 8;
+      float p[8];
+      const uint32_t w[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const mat_us2 d = __builtin_elementwise_min(
+            __builtin_elementwise_sub_sat(kmax2, __builtin_bit_cast(mat_us2, keys2_of_codes2(w[i]))),
+            z2);
+        p[2 * i] = tbl[d[0]];
+        p[2 * i + 1] = tbl[d[1]];
+      }
+      if (part) {
+        const int sh = 16 * (u & 3);
+        const uint64_t e = u < 4 ? ea : eb, t = u < 4 ? ta : tb;
+        uint32_t rk = base + (uint32_t)((e >> sh) & 0xFFFFu);
+        base += (uint32_t)((t >> sh) & 0xFFFFu);
+        const uint32_t m = mk[u];
+        if (m != 0u) {
+#pragma unroll
+          for (int t2 = 0; t2 < 8; ++t2)
+            if ((m >> t2) & 1u) { if ((int32_t)rk >= r.st.rstar) p[t2] = 0.0f; ++rk; }
+        }
+      }
+      if (a.vec_out && idx + 8 <= c1) {
+        *reinterpret_cast<float4*>(o + idx) = make_float4(p[0], p[1], p[2], p[3]);
+        *reinterpret_cast<float4*>(o + idx + 4) = make_float4(p[4], p[5], p[6], p[7]);
+      } else if (idx < c1) {
+#pragma unroll
+        for (int t2 = 0; t2 < 8; ++t2)
+          if (idx + t2 < c1) o[idx + t2] = p[t2];
+      }
+    }
+    return;
   }
 #pragma unroll
   for (int u = 0; u < kMatRounds; ++u) {
