@@ -129,6 +129,15 @@ struct BinMap {
   __device__ uint32_t key_rep(int b) const {
     return (!anchored && b == SK_BIN_ZERO) ? zrep : key_lo(b);
   }
+  // key_rep(b) for b >= 1 by selects alone (no divergent branches), for the
+  // normaliser's per-bin evaluations; b = 0 gives a key whose exp is unused
+  __device__ uint32_t key_rep_sel(int b) const {
+    const uint32_t ub = (uint32_t)b;
+    const uint32_t kf = ub <= (uint32_t)SK_WIN ? SK_NEG_LO - 1u + ub
+                                               : SK_POS_LO - (uint32_t)SK_BIN_ZERO - 1u + ub;
+    const uint32_t kz = ub == (uint32_t)SK_BIN_ZERO ? zrep : kf;
+    return anchored ? lo - 1u + ub : kz;
+  }
   __device__ int bin(uint32_t k) const {
     if (anchored) return k < lo ? 0 : (int)(k - lo) + 1;
     return sk_bin_of_key(k);
@@ -754,8 +763,8 @@ __device__ __forceinline__ int64_t rowstream_body(const RowStatArgs& a, SkLdsT<N
     auto zterm2 = [&](uint32_t e0, uint32_t e1) {
       const uint32_t c0 = e0 & 0x3FFFFu, c1 = e1 & 0x3FFFFu;
       const int b0 = (int)(e0 >> 18), b1 = (int)(e1 >> 18);
-      const float x0 = exp_det_sel(sk_d(bm.key_rep(b0), invT, m));
-      const float x1 = exp_det_sel(sk_d(bm.key_rep(b1), invT, m));
+      const float x0 = exp_det_sel(sk_d(bm.key_rep_sel(b0), invT, m));
+      const float x1 = exp_det_sel(sk_d(bm.key_rep_sel(b1), invT, m));
       if (c0 != 0 && bmax - b0 < SK_ETOP) L.etop[bmax - b0] = x0;
       if (c1 != 0 && bmax - b1 < SK_ETOP) L.etop[bmax - b1] = x1;
       const uint64_t f0 = fixed62(x0), f1 = fixed62(x1);
