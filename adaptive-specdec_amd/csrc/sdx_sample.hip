@@ -648,7 +648,7 @@ __device__ __forceinline__ bool partial_group(const RowStat& st) {
 }
 
 typedef unsigned short mat_us2 __attribute__((ext_vector_type(2)));
-static_assert(kMatRounds <= 8, "member counts of a chunk's rounds: two 64-bit scans of 16-bit fields");
+constexpr int kMatScans = (kMatRounds + 3) / 4;  // 64-bit scans of four 16-bit round counts
 
 template <int FMT>
 __global__ void __launch_bounds__(SM_NT) materialize16_kernel(Eval16<FMT> ev, MaterializeArgs a) {
@@ -751,15 +751,19 @@ __global__ void __launch_bounds__(SM_NT) materialize16_kernel(Eval16<FMT> ev, Ma
     __syncthreads();  // every bind() has read the table
     for (int32_t e = kmax - gh + (int32_t)threadIdx.x; e <= kmax - gl; e += SM_NT) tbl[e] = bv;
     if (threadIdx.x == 0) tbl[Z] = 0.0f;
-    // member ranks (a partially kept group): bits per round, then two block scans
-    // of the per-thread counts packed four rounds to a 64-bit word (16-bit fields:
-    // a round holds at most SM_ROUND members)
-    uint32_t mk[kMatRounds];
-    uint64_t ea = 0, eb = 0, ta = 0, tb = 0;
+    // member ranks (a partially kept group): bits per round (four rounds to a
+    // word), then block scans of the per-thread counts packed four rounds to a
+    // 64-bit word (16-bit fields: a round holds at most SM_ROUND members)
+    uint32_t mk[kMatScans];
+    uint64_t es[kMatScans], ts[kMatScans];
+#pragma unroll
+    for (int i = 0; i < kMatScans; ++i) mk[i] = 0u, es[i] = 0ull, ts[i] = 0ull;
     if (part) {  // uniform
       const mat_us2 gl2 = {(unsigned short)gl, (unsigned short)gl};
       const mat_us2 sp2 = {(unsigned short)(gh - gl + 1), (unsigned short)(gh - gl + 1)};
-      uint64_t ca = 0, cb = 0;
+      uint64_t cs[kMatScans];
+#pragma unroll
+      for (int i = 0; i < kMatScans; ++i) cs[i] = 0ull;
 #pragma unroll
       for (int u = 0; u < kMatRounds; ++u) {
         const int64_t idx = c0 + (int64_t)u * SM_ROUND + (int64_t)threadIdx.x * 8;
@@ -774,12 +778,12 @@ __global__ void __launch_bounds__(SM_NT) materialize16_kernel(Eval16<FMT> ev, Ma
             m |= ((uint32_t)b[0] << (2 * i)) | ((uint32_t)b[1] << (2 * i + 1));
           }
         }
-        mk[u] = m;
-        if (u < 4) ca |= (uint64_t)__popc(m) << (16 * u);
-        else cb |= (uint64_t)__popc(m) << (16 * (u - 4));
+        mk[u >> 2] |= m << (8 * (u & 3));
+        cs[u >> 2] |= (uint64_t)__popc(m) << (16 * (u & 3));
       }
-      ea = block_excl_u64(ca, s64, &ta);  // (its barriers also order the table's patch)
-      eb = block_excl_u64(cb, s64, &tb);
+#pragma unroll
+      for (int i = 0; i < kMatScans; ++i)  // (the barriers also order the table's patch)
+        es[i] = block_excl_u64(cs[i], s64, &ts[i]);
     } else {
       __syncthreads();
     }
@@ -803,10 +807,9 @@ __global__ void __launch_bounds__(SM_NT) materialize16_kernel(Eval16<FMT> ev, Ma
       }
       if (part) {
         const int sh = 16 * (u & 3);
-        const uint64_t e = u < 4 ? ea : eb, t = u < 4 ? ta : tb;
-        uint32_t rk = base + (uint32_t)((e >> sh) & 0xFFFFu);
-        base += (uint32_t)((t >> sh) & 0xFFFFu);
-        const uint32_t m = mk[u];
+        uint32_t rk = base + (uint32_t)((es[u >> 2] >> sh) & 0xFFFFu);
+        base += (uint32_t)((ts[u >> 2] >> sh) & 0xFFFFu);
+        const uint32_t m = (mk[u >> 2] >> (8 * (u & 3))) & 0xFFu;
         if (m != 0u) {
 #pragma unroll
           for (int t2 = 0; t2 < 8; ++t2)
