@@ -795,29 +795,6 @@ int sdx_draft_step(const void* logits, int dtype, int64_t batch, int64_t vocab, 
   a.stats = st; a.tables = tb;
   a.split_ws = split_ws; a.split_bytes = split_bytes; a.ws_header = header;
   sdx::RowSource16 src{(const uint16_t*)logits, ld, (const uint16_t*)logits, ld, batch, true};
-  if (dtype == SDX_BF16 && batch <= sdx::kWsFusedMaxJobs && fused_enabled()) {
-    // one launch: the fused verify at k = 0 (one row per batch row, no accept
-    // test: its bonus draw from the row is the draft's draw on u), whose row
-    // counters sit in the workspace header like the verify's
-    sdx::AcceptArgs aa{st,      batch,   0,       u,       u,       nullptr, jobs,
-                       nullptr, nullptr, nullptr, nullptr, nullptr, batch};
-    if (int r = hip_status(sdx::launch_verify_fused_bf16(a, batch, src, aa, batch, vocab,
-                                                         temperature, recs,
-                                                         sdx::fused_draw_words(header),
-                                                         sdx::fused_job_words(header), x, s,
-                                                         nullptr),
-                           "draft_fused_bf16"))
-      return r;
-  } else {
-    if (int r = row_stats16(dtype, a, batch, s)) return r;
-    hipLaunchKernelGGL(sdx_jobs_from_u, dim3((unsigned)((batch + 255) / 256)), dim3(256), 0, s,
-                       jobs, u, batch, (int64_t)-1, counters);
-    if (int r = hip_status(hipGetLastError(), "jobs")) return r;
-    if (int r = hip_status(sdx::launch_draw_rows16(dtype, src, st, tb, temperature, jobs, batch,
-                                                   vocab, recs, counters, x, s),
-                           "draw_rows16"))
-      return r;
-  }
   e.fmt = dtype;
   e.codes = (const uint16_t*)logits;
   e.ld = ld;
@@ -832,6 +809,28 @@ int sdx_draft_step(const void* logits, int dtype, int64_t batch, int64_t vocab, 
     e.sig = header + sdx::kWsDraftSigWord;
     e.top_p = tp;
     e.top_k = (int32_t)sig[5];
+  }
+  if (dtype == SDX_BF16 && batch <= sdx::kWsFusedMaxJobs && fused_enabled()) {
+    // one launch: the fused verify at k = 0 (one row per batch row, no accept
+    // test: its bonus draw from the row is the draft's draw on u), whose row
+    // counters sit in the workspace header like the verify's, with the
+    // epilogue done by the blocks that complete the draws
+    sdx::AcceptArgs aa{st,      batch,   0,       u,       u,       nullptr, jobs,
+                       nullptr, nullptr, nullptr, nullptr, nullptr, batch};
+    return hip_status(sdx::launch_draft_fused_bf16(a, src, aa, batch, vocab, temperature, recs,
+                                                   sdx::fused_draw_words(header),
+                                                   sdx::fused_job_words(header), x, e,
+                                                   header + sdx::kWsDraftDoneWord, s),
+                      "draft_fused_bf16");
+  } else {
+    if (int r = row_stats16(dtype, a, batch, s)) return r;
+    hipLaunchKernelGGL(sdx_jobs_from_u, dim3((unsigned)((batch + 255) / 256)), dim3(256), 0, s,
+                       jobs, u, batch, (int64_t)-1, counters);
+    if (int r = hip_status(hipGetLastError(), "jobs")) return r;
+    if (int r = hip_status(sdx::launch_draw_rows16(dtype, src, st, tb, temperature, jobs, batch,
+                                                   vocab, recs, counters, x, s),
+                           "draw_rows16"))
+      return r;
   }
   return hip_status(sdx::launch_draft_epilogue(e, s), "draft_epilogue");
 }

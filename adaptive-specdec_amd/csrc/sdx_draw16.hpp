@@ -438,7 +438,9 @@ __device__ __forceinline__ uint32_t sel_word(const uint4& v, int i) {
 // (bp[i], bq[i]) at its start; returns its mass (residual when use_r, else p)
 // in m[i]. With `find` (NR == 1, base <= t): the id whose prefix mass, counted
 // from `base`, first exceeds t goes to *found. `s32` / `s64` hold SM_NW words.
-template <int FMT, int NR, int NW = SM_NW>
+// FP: the found id's p value (its final probability, member rank applied) goes
+// to s32[0] as float bits, read after the walk's last barrier.
+template <int FMT, int NR, int NW = SM_NW, bool FP = false>
 __device__ void block_walk16(const Eval16<FMT>& ev, const typename Eval16<FMT>::Row& rp,
                              const typename Eval16<FMT>::Row& rq, bool use_r,
                              const int64_t (&i0)[NR], const int64_t (&i1)[NR],
@@ -484,6 +486,7 @@ __device__ void block_walk16(const Eval16<FMT>& ev, const typename Eval16<FMT>::
     for (int x = 0; x < 8; ++x) {
       float pv = p[x];
       if ((mp >> x) & 1u) { pv = (int32_t)rk_p < sp ? pv : 0.0f; ++rk_p; }
+      if constexpr (FP) p[x] = pv;
       if (use_r) {
         float qv = q[x];
         if ((mq >> x) & 1u) { qv = (int32_t)rk_q < sq ? qv : 0.0f; ++rk_q; }
@@ -509,12 +512,17 @@ __device__ void block_walk16(const Eval16<FMT>& ev, const typename Eval16<FMT>::
       if (s0 <= t && s0 + mine > t) {
         uint64_t acc = s0;
         int64_t f = -1;
+        float fpv = 0.0f;
 #pragma unroll
         for (int x = 0; x < 8; ++x) {
           acc += wv[x];
-          if (f < 0 && acc > t) f = idx + x;
+          if (f < 0 && acc > t) {
+            f = idx + x;
+            if constexpr (FP) fpv = p[x];
+          }
         }
         *found = f;
+        if constexpr (FP) s32[0] = __float_as_uint(fpv);  // every thread has read s32
       }
     }
     __syncthreads();  // s32 / s64 reused
@@ -690,8 +698,9 @@ using Draw16Lds = Draw16LdsT<SM_NW>;
 
 // One job's accept chain and draw, run by a block of SM_NT threads: block bi of
 // the job's blocks (wave w of it owns record bi * SM_NW + w); the block that
-// completes the job's records draws y.
-template <int FMT, bool COH, int NT = SM_NT, int R = kRec16Rounds>
+// completes the job's records draws y. FP: that block also leaves the drawn
+// id's p value in S.s32w[0] (float bits) when y >= 0.
+template <int FMT, bool COH, int NT = SM_NT, int R = kRec16Rounds, bool FP = false>
 __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a,
                                             Draw16LdsT<NT / kWave>& S, int64_t j, int bi) {
   constexpr int NW = NT / kWave;
@@ -1004,8 +1013,8 @@ __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a,
     const int64_t i0[1] = {rec_star * REC}, i1[1] = {min(V, rec_star * REC + REC)};
     const uint32_t bp1[1] = {(uint32_t)(packed & 0xFFFFFFFF)}, bq1[1] = {(uint32_t)(packed >> 32)};
     uint64_t mm[1];
-    block_walk16<FMT, 1, NW>(ev, rp, rq, use_r, i0, i1, bp1, bq1, mm, (uint64_t)s_pick[2], true, t,
-                         &s_found, s32w, s64w);
+    block_walk16<FMT, 1, NW, FP>(ev, rp, rq, use_r, i0, i1, bp1, bq1, mm, (uint64_t)s_pick[2],
+                                 true, t, &s_found, s32w, s64w);
   }
   finish(s_found);
 }

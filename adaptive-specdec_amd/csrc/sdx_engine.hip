@@ -84,8 +84,10 @@ __global__ void __launch_bounds__(256) draft_gather_kernel(DraftGatherArgs a) {
   const int64_t b = blockIdx.x;
   const int i = (int)blockIdx.y;
   const uint8_t* ws = a.ws[i];
+  // the draft step's workspace must still be trusted (a draw wait that gave up
+  // overwrote its magic word) and its statistics made for this configuration
   const uint32_t* sig = reinterpret_cast<const uint32_t*>(ws) + kWsDraftSigWord;
-  bool ok = true;
+  bool ok = reinterpret_cast<const uint32_t*>(ws)[0] == kWsMagic;
   for (int w = 0; w < kDraftSigWords; ++w) ok = ok && sig[w] == a.sig[w];
   const int64_t row = a.ntgt + b * a.k + i;
   RowStat* dst = a.stats + row;

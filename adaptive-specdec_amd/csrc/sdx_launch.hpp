@@ -281,6 +281,9 @@ hipError_t launch_draw_rows16(int fmt, const RowSource16& src, const RowStat* st
 constexpr int kWsDraftSigWord = 3072;
 constexpr uint32_t kDraftSig = 0x44524654u;
 constexpr int kDraftSigWords = 6;
+// The fused draft step's count of batch rows whose epilogue is written (the
+// last one resets it to zero).
+constexpr int kWsDraftDoneWord = kWsDraftSigWord + kDraftSigWords;
 constexpr int kMaxDraftK = 31;  // the fused verify's 2k + 1 <= 64
 struct DraftEpiArgs {
   int fmt;                 // SDX_BF16 / SDX_F16 (16-bit rows)
@@ -305,6 +308,14 @@ struct DraftEpiArgs {
   int64_t* xcopy;          // [B] the drawn ids kept in the workspace, or null
 };
 hipError_t launch_draft_epilogue(const DraftEpiArgs& a, hipStream_t s);
+// sdx_draft_fused.hip: the draft step for bf16 rows in one launch (the fused
+// verify at k = 0 with the epilogue folded into the blocks that complete the
+// draws); x is the draw's output, `done` the header word kWsDraftDoneWord.
+hipError_t launch_draft_fused_bf16(const RowStatArgs& rs, const RowSource16& src,
+                                   const AcceptArgs& acc, int64_t batch, int64_t V, float T,
+                                   ChunkRec* recs, uint32_t* counters, uint32_t* job_cnt,
+                                   int64_t* x, const DraftEpiArgs& e, uint32_t* done,
+                                   hipStream_t s);
 // The statistics of k draft steps (their workspaces ws[i]: RowStat[B] at st_off,
 // tables [B][kTbl] at tb_off) copied to the verify workspace's draft rows
 // (row ntgt + b k + i), with the drafted token's probability and tie flags set as

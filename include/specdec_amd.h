@@ -169,8 +169,8 @@ int sdx_verify_noalloc(const void* target_logits, const void* draft_logits, int 
  * in full, plus the draft rows of the final residual draws (the row statistics
  * then the draw, two launches). Outputs, rules and workspace as sdx_verify, and
  * the same results as sdx_verify on the same inputs. A draft workspace whose
- * statistics were made for another shape or sampling configuration flags its
- * rows SDX_FLAG_WORKSPACE. Other dtypes, temperature <= 0 and k > 31 run
+ * statistics were made for another shape or sampling configuration, or whose draft
+ * step's wait gave up, flags its rows SDX_FLAG_WORKSPACE. Other dtypes, temperature <= 0 and k > 31 run
  * sdx_verify and ignore the draft workspaces. No reference counterpart: the
  * reference's verify recomputes q from the draft logits (engine.py:250,288). */
 int sdx_verify_drafted(const void* target_logits, const void* draft_logits, int dtype,
@@ -245,7 +245,11 @@ int sdx_verify_greedy(const void* target_logits, int dtype, int64_t batch, int32
  * a sequential fp32 sum in row order over batch (ConfidenceEarlyExit.
  * should_stop_drafting), else 0. logits [batch, ld] (dtype); workspace from
  * sdx_draft_step_workspace, prepared once by sdx_workspace_init. Every output stays on
- * the device: the reference's float(conf.mean()) host sync becomes a device flag. */
+ * the device: the reference's float(conf.mean()) host sync becomes a device flag.
+ * With bf16 rows the call is one launch, whose draw blocks wait (bounded) for their
+ * row's statistics; a wait that gives up leaves that row x -1, qx 0, conf *= 0 and
+ * *stop = 1, and marks the workspace (its statistics are no longer taken over by
+ * sdx_verify_drafted) until sdx_workspace_init prepares it again. */
 size_t sdx_draft_step_workspace(int64_t batch, int64_t vocab, int dtype);
 int sdx_draft_step(const void* logits, int dtype, int64_t batch, int64_t vocab, int64_t ld,
                    float temperature, float top_p, int32_t top_k, const float* u, int64_t* x,

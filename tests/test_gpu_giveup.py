@@ -106,3 +106,62 @@ def test_to_probs_look_back_give_up(case):
     assert n > 0, "no chunk gave up at a zero wait bound"
     got2 = _np(S.to_probs(x, T, tp, 0))
     assert _probs_chunks_exact_or_nan(got2, ref) == 0
+
+
+def test_draft_step_wait_give_up_marks_workspace():
+    """The one-launch bf16 draft step with SDX_VERIFY_WAIT_TICKS=0: a row whose
+    draw blocks did not all find its statistics in gives up (x -1, qx 0,
+    conf 0, stop 1); every other row equals the oracle. The workspace is then
+    marked: the next step gives up on every row, and a verify that would take
+    its statistics over flags its rows. Prepared again, the step is exact."""
+    from specdec import _lib
+    from specdec.sampling import draft_step
+    from specdec.workloads import uniforms, zipf_logits
+    B, V, T, tp = 64, 151936, 0.8, 0.95
+    g = torch.Generator(device=DEV).manual_seed(91)
+    x = zipf_logits(B, V, g, DEV)
+    u = uniforms((B,), g, DEV)
+    conf0 = 0.3 + 0.7 * uniforms((B,), g, DEV)
+    print(f"[giveup] draft step B={B} V={V}", flush=True)
+    rx, rq, rconf, rstop = O.draft_step(_np(x), _np(u), T, tp, 0, conf=_np(conf0), tau=0.5,
+                                        step=2, min_k=1)
+    ws = _lib.workspace(_lib.lib().sdx_draft_step_workspace(B, V, _lib.dtype_code(x)), DEV)
+
+    def step():
+        conf = conf0.clone()
+        xs, qx, stop = draft_step(x, u, T, tp, 0, conf=conf, tau=0.5, step=2, min_k=1,
+                                  workspace=ws)
+        torch.cuda.synchronize()
+        return (xs.cpu().numpy(), qx.cpu().numpy(), conf.cpu().numpy(), int(stop.item()))
+
+    os.environ["SDX_VERIFY_WAIT_TICKS"] = "0"
+    try:
+        x1, q1, c1, s1 = step()
+    finally:
+        del os.environ["SDX_VERIFY_WAIT_TICKS"]
+    gave = x1 == -1
+    print(f"[giveup] draft rows given up: {int(gave.sum())} of {B}", flush=True)
+    assert gave.any(), "no draft row gave up at a zero wait bound"
+    assert np.all(q1[gave] == 0.0) and np.all(c1[gave] == 0.0) and s1 == 1
+    ok = ~gave
+    assert np.array_equal(x1[ok], rx[ok])
+    assert np.array_equal(q1[ok].view(np.uint32), rq[ok].view(np.uint32))
+    assert np.array_equal(c1[ok].view(np.uint32), rconf[ok].view(np.uint32))
+    # marked: every row of the next step gives up ...
+    x2, q2, c2, s2 = step()
+    assert np.all(x2 == -1) and np.all(q2 == 0.0) and s2 == 1
+    # ... and a verify does not take the marked workspace's statistics over
+    k = 1
+    inp = verify_inputs(B, k, V, seed=92, device=DEV, temperature=T, top_p=tp)
+    v = Verifier(B, k, V, torch.bfloat16, temperature=T, top_p=tp, device=DEV)
+    draft = x.view(B, 1, V)
+    ids = torch.as_tensor(rx, device=DEV).view(B, 1)
+    _, _, f3 = v.drafted(inp["target"], draft, ids, inp["u_accept"], inp["u_final"], [ws])
+    torch.cuda.synchronize()
+    assert np.all((f3.cpu().numpy() & FLAG_WORKSPACE) != 0)
+    # prepared again, the step equals the oracle
+    _lib.prepare(ws)
+    x4, q4, c4, s4 = step()
+    assert np.array_equal(x4, rx) and s4 == rstop
+    assert np.array_equal(q4.view(np.uint32), rq.view(np.uint32))
+    assert np.array_equal(c4.view(np.uint32), rconf.view(np.uint32))
