@@ -33,7 +33,7 @@ for _p in (REPO, os.path.join(REPO, "adaptive-specdec_amd")):
 METRIC = "verified tokens/sec at B=64,k=4,V=151936; % of HBM peak; speedup vs host CPU"
 HBM_PEAK_GBS = 8000.0
 STAT_CHAIN = 8
-STEP_CHAIN = 4
+STEP_CHAIN = 16  # default of --chain
 
 
 def log(msg):
@@ -63,16 +63,16 @@ def timed_graphs(graphs, steps, torch):
     return e0.elapsed_time(e1) / steps
 
 
-def timed_steps(chains, singles, steps, torch):
-    """Exactly `steps` verify steps: steps // STEP_CHAIN replays of the chained
+def timed_steps(chains, singles, steps, torch, chain):
+    """Exactly `steps` verify steps: steps // chain replays of the chained
     graphs, then the remainder as single-step graphs, all between two events;
     ms per step."""
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for i in range(steps // STEP_CHAIN):
+    for i in range(steps // chain):
         chains[i % len(chains)].replay()
-    for i in range(steps % STEP_CHAIN):
+    for i in range(steps % chain):
         singles[i % len(singles)].replay()
     e1.record()
     torch.cuda.synchronize()
@@ -139,12 +139,12 @@ def bench_verify(args, torch):
                 ok = (torch.equal(v.n_acc, n) and torch.equal(v.y, y) and torch.equal(v.flags, f))
                 if not ok:
                     raise RuntimeError("graph replay differs from the eager verify")
-        # the timed graphs hold STEP_CHAIN consecutive verify steps over the rotating
+        # the timed graphs hold args.chain consecutive verify steps over the rotating
         # sets (as an engine's captured decode loop would), so the host's per-replay
-        # launch cost is paid once per STEP_CHAIN steps
-        chains = [capture(lambda i=i: [calls[(i + j) % len(calls)]() for j in range(STEP_CHAIN)],
+        # launch cost is paid once per args.chain steps
+        chains = [capture(lambda i=i: [calls[(i + j) % len(calls)]() for j in range(args.chain)],
                           torch) for i in range(len(calls))]
-        ms = timed_steps(chains, graphs, args.steps, torch)
+        ms = timed_steps(chains, graphs, args.steps, torch, args.chain)
         ms_single = timed_graphs(graphs, args.steps, torch)
         stat_ms = timed_graphs(sgraphs, max(args.steps // STAT_CHAIN, 10), torch) / STAT_CHAIN
     # eager timing too (host launch path), for the record
@@ -666,6 +666,8 @@ def main():
     ap.add_argument("--logits", default="bf16", choices=["bf16", "f32"],
                     help="probs workload: dtype of the logits")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--chain", type=int, default=STEP_CHAIN,
+                    help="verify steps per timed graph replay (the headline workload)")
     ap.add_argument("--cpu-runs", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
