@@ -55,6 +55,7 @@ struct RowStatArgs {
   uint32_t* split_cnt;  // the header's counters (set by launch_rowstream_bf16)
   uint8_t* split_parts;
   int32_t jm_k;  // fused verify kernel: rows are taken in batch-row order at this k
+  int32_t jm_xcd;  // ... with batch row b's rows on blocks of XCD b % 8 (batch % 8 == 0)
   const int32_t* jm_order;  // ... or, at per-row k, in this order (block's q -> row)
 };
 

@@ -204,6 +204,7 @@ hipError_t launch_verify_fused_bf16(const RowStatArgs& rs, int64_t rows, const R
   FusedArgs a = {};
   a.rs = rs;
   a.rs.jm_k = rs.k;
+  a.rs.jm_xcd = !ragged && njobs % 8 == 0 ? 1 : 0;
   if (!ragged) a.rs.jm_order = nullptr;
   a.rowjob = ragged ? rowjob : nullptr;
   a.rs.zero = nullptr;  // the draw counters reset themselves (a row block could clear one late)

@@ -470,9 +470,23 @@ __device__ __forceinline__ void st_f32(float* dst, float v, bool coh) {
 
 // Rows in batch-row order (jm_k = k > 0): the q-th row taken is position
 // q % (2k + 1) of batch row q / (2k + 1), target positions first, so the rows of
-// one batch row finish close together.
-__device__ __forceinline__ int64_t jm_row(int64_t q, int32_t k, int64_t ntgt) {
-  const int64_t b = q / (2 * k + 1), i = q % (2 * k + 1);
+// one batch row finish close together. With `xcd` (batch % 8 == 0) the order is
+// kept per XCD instead: block q runs on XCD q % 8 (blocks are dealt to the XCDs
+// in index order), and the (q / 8)-th row taken there is position
+// (q / 8) % (2k + 1) of batch row q % 8 + 8 ((q / 8) / (2k + 1)). A batch row's
+// rows then stream on the XCD its draw blocks run on, which reads two of them
+// again.
+__device__ __forceinline__ int64_t jm_row(int64_t q, int32_t k, int64_t ntgt, bool xcd) {
+  const int64_t n = 2 * k + 1;
+  int64_t b, i;
+  if (xcd) {
+    const int64_t s = q >> 3;
+    b = (q & 7) + 8 * (s / n);
+    i = s % n;
+  } else {
+    b = q / n;
+    i = q % n;
+  }
   return i <= k ? b * (k + 1) + i : ntgt + b * k + (i - k - 1);
 }
 
@@ -502,7 +516,8 @@ __device__ __forceinline__ int64_t rowstream_body(const RowStatArgs& a, SkLdsT<N
     }
     row = a.nwhole + sidx;
   }
-  if (FUSED) row = a.jm_order ? (int64_t)a.jm_order[row] : jm_row(row, a.jm_k, a.nrows[0]);
+  if (FUSED)
+    row = a.jm_order ? (int64_t)a.jm_order[row] : jm_row(row, a.jm_k, a.nrows[0], a.jm_xcd != 0);
   const int g = row < a.nrows[0] ? 0 : 1;
   const int64_t r = g ? row - a.nrows[0] : row;
   const uint16_t* __restrict__ ptr = a.base[g] + r * a.ld[g];
