@@ -36,12 +36,13 @@ namespace sdx {
 
 constexpr int VA_NT = 256;
 constexpr int VA_NW = VA_NT / kWave;
-constexpr int VA_D = 128;     // head dim
+constexpr int VA_D = 128;     // largest head dim (workspace partial rows are sized for it)
 constexpr int VA_TOK = 32;    // tokens per tile
 constexpr int VA_MAXM = 64;   // query rows per workgroup (q_b * group)
 // LDS row strides (bf16 elements): 2 mod 4 dwords, so the 8-byte MFMA operand
 // reads of 16 consecutive rows hit 32 distinct banks
-constexpr int VA_KS = VA_D + 4;
+template <int D>
+constexpr int va_ks() { return D + 4; }
 constexpr int VA_VS = VA_TOK + 4;
 constexpr int VA_PS = VA_TOK + 4;
 constexpr int VA_CHMAX = 1024;  // most tokens per chunk (multiple of 2 tiles)
@@ -187,10 +188,16 @@ __global__ void __launch_bounds__(VA_PLAN_NT) verify_attn_plan_kernel(AttnArgs a
   for (int64_t u = carry + tid; u < a.nunits; u += VA_PLAN_NT) a.units[u].b = -1;
 }
 
+// D: head dim, 64 or 128.
+template <int D>
 __global__ void __launch_bounds__(VA_NT) __attribute__((amdgpu_waves_per_eu(3)))
 verify_attn_kernel(AttnArgs a) {
-  __shared__ __align__(16) uint16_t sK[VA_TOK][VA_KS];
-  __shared__ __align__(16) uint16_t sVt[VA_D][VA_VS];
+  static_assert(D == 64 || D == 128, "head dims of 64 or 128");
+  constexpr int TPT = D / 8;           // threads per token of a K tile (16 bytes each)
+  constexpr int TPP = VA_NT / TPT;     // tokens per pass of the block
+  constexpr int KH = VA_TOK / TPP;     // passes per K tile
+  __shared__ __align__(16) uint16_t sK[VA_TOK][va_ks<D>()];
+  __shared__ __align__(16) uint16_t sVt[D][VA_VS];
   __shared__ __align__(16) uint16_t sP[VA_NW][16][VA_PS];
   __shared__ __align__(16) uint32_t sSlot[VA_CHMAX];  // chunk token -> head slice (256 B) of the pool
   __shared__ int64_t sRow[VA_MAXM];  // query row i -> element offset of its q / out vector
@@ -216,7 +223,7 @@ verify_attn_kernel(AttnArgs a) {
   const int M = (int)qb * a.group;
   const bool whole = kvl <= a.chunk;  // the row is one chunk: write the output directly
   // row i = j * group + g is query head kvh * group + g of position j
-  if (tid < M) sRow[tid] = ((q0 + tid / a.group) * a.hq + kvh * a.group + tid % a.group) * VA_D;
+  if (tid < M) sRow[tid] = ((q0 + tid / a.group) * a.hq + kvh * a.group + tid % a.group) * D;
   __syncthreads();  // page ids and row offsets in LDS
 
   // ---- the chunk's slots: token t -> (page * bs + (c0 + t) % bs) * hkv + kvh
@@ -229,22 +236,23 @@ verify_attn_kernel(AttnArgs a) {
     sSlot[t] = ok ? (uint32_t)((((int64_t)page * a.bs + pos % a.bs) * a.hkv) + kvh) : VA_NOSLOT;
   }
 
-  // ---- tile loads. K: thread t moves 16 bytes (8 dims) of tokens t / 16 and
-  // 16 + t / 16. V: wave w moves tokens 8w .. 8w + 7, lane l dims 2l, 2l + 1 of
-  // each (a 256-byte row per load), so a lane can write V transposed in 8-byte
-  // runs of 4 tokens.
-  const int ltok = tid / 16, lpart = tid % 16;
+  // ---- tile loads. K: thread t moves 16 bytes (8 dims) of tokens t / TPT,
+  // TPP + t / TPT, ... (two passes at D = 128, one at 64). V: wave w moves tokens
+  // 8w .. 8w + 7, lane l < D / 2 dims 2l, 2l + 1 of each (a 2D-byte row per
+  // load), so a lane can write V transposed in 8-byte runs of 4 tokens.
+  const int ltok = tid / TPT, lpart = tid % TPT;
+  const bool vlane = D >= 2 * kWave || 2 * lane < D;  // this lane holds V dims (all at D = 128)
   // Loads are unconditional, so they stay in flight across the tile loop: a
   // token past the chunk or with a page outside the pool reads slice 0 instead;
   // its K only meets masked scores (or an error-flagged row) and its V is zeroed
   // when staged.
-  auto gather = [&](int t0, uint4 (&kk)[2], uint32_t (&vv)[8], uint32_t& vok) {
+  auto gather = [&](int t0, uint4 (&kk)[KH], uint32_t (&vv)[8], uint32_t& vok) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int t = t0 + ltok + 16 * h;
+    for (int h = 0; h < KH; ++h) {
+      const int t = t0 + ltok + TPP * h;
       const uint32_t sl = sSlot[min(t, n - 1)];
       const bool ok = t < n && sl != VA_NOSLOT;
-      kk[h] = *reinterpret_cast<const uint4*>(a.k_pool + (size_t)(ok ? sl : 0u) * VA_D + lpart * 8);
+      kk[h] = *reinterpret_cast<const uint4*>(a.k_pool + (size_t)(ok ? sl : 0u) * D + lpart * 8);
     }
     const int tb = t0 + 8 * w;  // the wave's 8 tokens: slots read as two 16-byte words
     const int tr = min(tb, VA_CHMAX - 8);
@@ -256,14 +264,14 @@ verify_attn_kernel(AttnArgs a) {
     for (int e = 0; e < 8; ++e) {
       const bool ok = tb + e < n && sl[e] != VA_NOSLOT;
       vok |= (uint32_t)ok << e;
-      vv[e] = *reinterpret_cast<const uint32_t*>(a.v_pool + (size_t)(ok ? sl[e] : 0u) * VA_D +
-                                                 2 * lane);
+      vv[e] = *reinterpret_cast<const uint32_t*>(a.v_pool + (size_t)(ok ? sl[e] : 0u) * D +
+                                                 (vlane ? 2 * lane : 0));
     }
   };
-  auto stage = [&](const uint4 (&kk)[2], const uint32_t (&vr)[8], uint32_t vok) {
+  auto stage = [&](const uint4 (&kk)[KH], const uint32_t (&vr)[8], uint32_t vok) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      uint2* dst = reinterpret_cast<uint2*>(&sK[ltok + 16 * h][lpart * 8]);  // rows are 8-byte aligned
+    for (int h = 0; h < KH; ++h) {
+      uint2* dst = reinterpret_cast<uint2*>(&sK[ltok + TPP * h][lpart * 8]);  // rows are 8-byte aligned
       dst[0] = make_uint2(kk[h].x, kk[h].y);
       dst[1] = make_uint2(kk[h].z, kk[h].w);
     }
@@ -277,21 +285,24 @@ verify_attn_kernel(AttnArgs a) {
       lo[e] = (vv[2 * e] & 0xFFFFu) | (vv[2 * e + 1] << 16);
       hi[e] = (vv[2 * e] >> 16) | (vv[2 * e + 1] & 0xFFFF0000u);
     }
-    uint2* d0 = reinterpret_cast<uint2*>(&sVt[2 * lane][8 * w]);
-    uint2* d1 = reinterpret_cast<uint2*>(&sVt[2 * lane + 1][8 * w]);
-    d0[0] = make_uint2(lo[0], lo[1]);
-    d0[1] = make_uint2(lo[2], lo[3]);
-    d1[0] = make_uint2(hi[0], hi[1]);
-    d1[1] = make_uint2(hi[2], hi[3]);
+    if (vlane) {
+      uint2* d0 = reinterpret_cast<uint2*>(&sVt[2 * lane][8 * w]);
+      uint2* d1 = reinterpret_cast<uint2*>(&sVt[2 * lane + 1][8 * w]);
+      d0[0] = make_uint2(lo[0], lo[1]);
+      d0[1] = make_uint2(lo[2], lo[3]);
+      d1[0] = make_uint2(hi[0], hi[1]);
+      d1[1] = make_uint2(hi[2], hi[3]);
+    }
   };
 
   // ---- per-wave state: rows r0 + 4 * (lane / 16) + r, r < 4
   const int r0 = 16 * w;
   const bool active = r0 < M;  // uniform per wave
   const int lr = 4 * (lane / 16), lc = lane % 16;
-  va_f4 o[8];
+  constexpr int OJ = D / 16;  // 16-wide output column blocks per wave
+  va_f4 o[OJ];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) o[j] = (va_f4){0.0f, 0.0f, 0.0f, 0.0f};
+  for (int j = 0; j < OJ; ++j) o[j] = (va_f4){0.0f, 0.0f, 0.0f, 0.0f};
   float m_run[4], l_run[4];
   int lim[4];  // last visible key of the lane's rows, relative to the chunk (-1: none;
                // at most n - 1, so a tile past the chunk's end is all masked)
@@ -307,13 +318,13 @@ verify_attn_kernel(AttnArgs a) {
   // the wave's query operands, in registers: lane holds row r0 + lc, dims
   // 32 kc + lk .. + 7 (lk = 8 (lane / 16), the operand layout of the 16x16x32 form)
   const int lk = 8 * (lane / 16);
-  va_s8 qa[VA_D / 32];
+  va_s8 qa[D / 32];
   {
     const int i = r0 + lc;
     const bool has = active && i < M;
     const uint16_t* src = a.q + (has ? sRow[i] : 0);
 #pragma unroll
-    for (int kc = 0; kc < VA_D / 32; ++kc)
+    for (int kc = 0; kc < D / 32; ++kc)
       qa[kc] = has ? *reinterpret_cast<const va_s8*>(src + kc * 32 + lk)
                    : (va_s8){0, 0, 0, 0, 0, 0, 0, 0};
   }
@@ -325,7 +336,7 @@ verify_attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) s[j] = (va_f4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int kc = 0; kc < VA_D / 32; ++kc) {
+    for (int kc = 0; kc < D / 32; ++kc) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) s[j] = va_mfma32(qa[kc], va_ld8(&sK[j * 16 + lc][kc * 32 + lk]), s[j]);
     }
@@ -349,7 +360,7 @@ verify_attn_kernel(AttnArgs a) {
       l_run[r] = l_run[r] * alpha + va_rowsum16(psum);
       m_run[r] = mnew;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o[j][r] *= alpha;
+      for (int j = 0; j < OJ; ++j) o[j][r] *= alpha;
     }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_wave_barrier();  // P written by the whole wave before it is read
@@ -358,12 +369,12 @@ verify_attn_kernel(AttnArgs a) {
     static_assert(VA_TOK == 32, "one K step of the 16x16x32 form per tile");
     const va_s8 pa = va_ld8(&sP[w][lc][lk]);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = va_mfma32(pa, va_ld8(&sVt[j * 16 + lc][lk]), o[j]);
+    for (int j = 0; j < OJ; ++j) o[j] = va_mfma32(pa, va_ld8(&sVt[j * 16 + lc][lk]), o[j]);
   };
 
   __syncthreads();  // the slot map is complete
   // two tiles in flight while one is used: A holds tiles 0, 2, 4, ..., B 1, 3, 5, ...
-  uint4 kA[2], kB[2];
+  uint4 kA[KH], kB[KH];
   uint32_t vA[8], vB[8], okA, okB;
   gather(0, kA, vA, okA);
   gather(VA_TOK, kB, vB, okB);
@@ -397,7 +408,7 @@ verify_attn_kernel(AttnArgs a) {
         uint16_t* dst = a.out + sRow[i];
         const float inv = l_run[r] > 0.0f ? 1.0f / l_run[r] : 0.0f;
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) dst[jj * 16 + lc] = va_bf16(o[jj][r] * inv);
+        for (int jj = 0; jj < OJ; ++jj) dst[jj * 16 + lc] = va_bf16(o[jj][r] * inv);
       }
     }
     return;
@@ -409,9 +420,9 @@ verify_attn_kernel(AttnArgs a) {
   for (int r = 0; r < 4; ++r) {
     const int i = r0 + lre + r;
     if (i < M) {
-      float* po = a.part_o + (part + i) * VA_D;
+      float* po = a.part_o + (part + i) * D;
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) po[jj * 16 + lc] = o[jj][r];
+      for (int jj = 0; jj < OJ; ++jj) po[jj * 16 + lc] = o[jj][r];
       if (lc == 0) *reinterpret_cast<float2*>(a.part_ml + (part + i) * 2) = make_float2(m_run[r], l_run[r]);
     }
   }
@@ -424,6 +435,7 @@ verify_attn_kernel(AttnArgs a) {
 // the loads of several chunks in flight.
 constexpr int VA_MERGE_W = 4096;  // weights held in LDS (chunks x query rows)
 
+template <int D>
 __global__ void __launch_bounds__(VA_NT) verify_attn_merge_kernel(AttnArgs a) {
   __shared__ float sW[VA_MERGE_W], sL[VA_MERGE_W];
   const int64_t b = blockIdx.x / a.hkv;
@@ -458,15 +470,15 @@ __global__ void __launch_bounds__(VA_NT) verify_attn_merge_kernel(AttnArgs a) {
     }
     __syncthreads();
   }
-  for (int e = threadIdx.x; e < M * (VA_D / 4); e += VA_NT) {
-    const int i = e / (VA_D / 4), d4 = e % (VA_D / 4);
+  for (int e = threadIdx.x; e < M * (D / 4); e += VA_NT) {
+    const int i = e / (D / 4), d4 = e % (D / 4);
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (staged) {
 #pragma unroll 4
       for (int ch = 0; ch < nch; ++ch) {
         const float wgt = sW[ch * M + i];
         const float4 v = *reinterpret_cast<const float4*>(
-            a.part_o + (part0 + (int64_t)ch * a.max_m + i) * VA_D + d4 * 4);
+            a.part_o + (part0 + (int64_t)ch * a.max_m + i) * D + d4 * 4);
         acc.x += wgt * v.x;
         acc.y += wgt * v.y;
         acc.z += wgt * v.z;
@@ -483,7 +495,7 @@ __global__ void __launch_bounds__(VA_NT) verify_attn_merge_kernel(AttnArgs a) {
         if (ml.x == -INFINITY) continue;  // the chunk holds none of the row's visible keys
         const float f = exp2f(ml.x - mx);
         den += f * ml.y;
-        const float4 v = *reinterpret_cast<const float4*>(a.part_o + p * VA_D + d4 * 4);
+        const float4 v = *reinterpret_cast<const float4*>(a.part_o + p * D + d4 * 4);
         acc.x += f * v.x;
         acc.y += f * v.y;
         acc.z += f * v.z;
@@ -496,7 +508,7 @@ __global__ void __launch_bounds__(VA_NT) verify_attn_merge_kernel(AttnArgs a) {
       acc.w *= inv;
     }
     const int64_t j = i / a.group, g = i % a.group;
-    uint16_t* dst = a.out + ((q0 + j) * a.hq + kvh * a.group + g) * VA_D + d4 * 4;
+    uint16_t* dst = a.out + ((q0 + j) * a.hq + kvh * a.group + g) * D + d4 * 4;
     const uint32_t lo = (uint32_t)va_bf16(acc.x) | ((uint32_t)va_bf16(acc.y) << 16);
     const uint32_t hi = (uint32_t)va_bf16(acc.z) | ((uint32_t)va_bf16(acc.w) << 16);
     *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
@@ -511,16 +523,23 @@ int attn_chunk_tokens(int64_t batch, int32_t hkv, int64_t max_tokens, int32_t ch
   return ch;
 }
 
+template <int D>
+static hipError_t launch_attn_d(const AttnArgs& a, int64_t batch, hipStream_t s) {
+  hipLaunchKernelGGL(verify_attn_kernel<D>, dim3((unsigned)((a.nunits + 7) / 8 * 8 * a.hkv)),
+                     dim3(VA_NT), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.nchunk == 1) return e;
+  hipLaunchKernelGGL(verify_attn_merge_kernel<D>, dim3((unsigned)(batch * a.hkv)), dim3(VA_NT), 0,
+                     s, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_verify_attn(const AttnArgs& a, int64_t batch, hipStream_t s) {
+  if (a.d != 64 && a.d != 128) return hipErrorInvalidValue;
   hipLaunchKernelGGL(verify_attn_plan_kernel, dim3(1), dim3(VA_PLAN_NT), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(verify_attn_kernel, dim3((unsigned)((a.nunits + 7) / 8 * 8 * a.hkv)),
-                     dim3(VA_NT), 0, s, a);
-  e = hipGetLastError();
-  if (e != hipSuccess || a.nchunk == 1) return e;
-  hipLaunchKernelGGL(verify_attn_merge_kernel, dim3((unsigned)(batch * a.hkv)), dim3(VA_NT), 0, s, a);
-  return hipGetLastError();
+  return a.d == 64 ? launch_attn_d<64>(a, batch, s) : launch_attn_d<128>(a, batch, s);
 }
 
 }  // namespace sdx

@@ -1000,8 +1000,8 @@ int sdx_verify_attention_paged(const void* q, int dtype, int64_t batch, const in
   if (!q || !cu_q || !k_pool || !v_pool || !block_table || !kv_len || !out || num_blocks < 1 ||
       !(scale > 0.0f))
     return fail(SDX_EINVAL, "sdx_verify_attention_paged: bad arguments");
-  if (dtype != SDX_BF16 || head_dim != 128)
-    return fail(SDX_EUNSUPPORTED, "sdx_verify_attention_paged: bf16 with head_dim 128 only");
+  if (dtype != SDX_BF16 || (head_dim != 64 && head_dim != 128))
+    return fail(SDX_EUNSUPPORTED, "sdx_verify_attention_paged: bf16 with head_dim 64 or 128 only");
   int32_t ch = 0, nch = 0;
   size_t need = 0;
   const int rc = attn_plan(batch, max_q, num_q_heads, num_kv_heads, block_size, max_blocks,
@@ -1039,6 +1039,7 @@ int sdx_verify_attention_paged(const void* q, int dtype, int64_t batch, const in
   a.group = group;
   a.bs = block_size;
   a.max_q = max_q;
+  a.d = head_dim;
   a.chunk = ch;
   a.nchunk = nch;
   a.max_m = max_q * group;
@@ -1047,7 +1048,7 @@ int sdx_verify_attention_paged(const void* q, int dtype, int64_t batch, const in
   a.units = (sdx::AttnUnit*)workspace;
   const int64_t nparts = batch * num_kv_heads * (int64_t)nch * a.max_m;
   a.part_o = nch > 1 ? (float*)((char*)workspace + ubytes) : nullptr;
-  a.part_ml = nch > 1 ? a.part_o + nparts * 128 : nullptr;
+  a.part_ml = nch > 1 ? a.part_o + nparts * head_dim : nullptr;
   a.scale_log2 = scale * 1.4426950408889634f;
   return hip_status(sdx::launch_verify_attn(a, batch, (hipStream_t)stream), "verify_attn");
 }

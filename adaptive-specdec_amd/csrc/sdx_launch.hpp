@@ -383,22 +383,23 @@ struct AttnUnit {   // one key chunk of one row (b < 0: no chunk)
   int64_t q0, kvl;      // the row's first query row and its keys
 };
 struct AttnArgs {
-  const uint16_t* q;        // [T, hq, 128] bf16
+  const uint16_t* q;        // [T, hq, d] bf16
   const int64_t* cu_q;      // [B + 1] query-row offsets
-  const uint16_t* k_pool;   // [num_blocks, bs, hkv * 128] bf16
+  const uint16_t* k_pool;   // [num_blocks, bs, hkv * d] bf16
   const uint16_t* v_pool;
   const int32_t* block_table;  // [B, max_blocks]
   const int64_t* kv_len;    // [B] keys per row, the new positions included
-  uint16_t* out;            // [T, hq, 128] bf16
+  uint16_t* out;            // [T, hq, d] bf16
   int32_t* error;           // set when a row's shape or pages are out of range
   AttnUnit* units;          // [nunits] the chunks in launch order (written by the plan kernel)
-  float* part_o;            // [B, hkv, nchunk, max_m, 128] chunk partials (nchunk > 1)
+  float* part_o;            // [B, hkv, nchunk, max_m, d] chunk partials (nchunk > 1)
   float* part_ml;           // [B, hkv, nchunk, max_m, 2] their (max, sum)
   int64_t max_blocks, num_blocks, batch;
   int32_t hq, hkv, group, bs, max_q;
   int32_t chunk, nchunk, max_m;  // tokens per chunk, chunks of the longest row, max_q * group
   int64_t nunits;           // batch * nchunk: the launch's chunk slots
   float scale_log2;         // softmax scale * log2(e)
+  int32_t d;                // head dim: 64 or 128
 };
 // tokens per key chunk (chunk > 0: that value, else the default for the shape)
 int attn_chunk_tokens(int64_t batch, int32_t hkv, int64_t max_tokens, int32_t chunk);

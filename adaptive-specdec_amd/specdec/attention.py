@@ -29,11 +29,11 @@ def attention_workspace(B, max_q, hq, hkv, block_size, max_blocks, chunk_tokens=
 
 def verify_attention_paged(q, cu_q, k_pool, v_pool, block_table, kv_len, max_q, scale=None,
                            out=None, error=None, chunk_tokens=0, workspace=None):
-    """q [T, Hq, 128] bf16 (T = cu_q[-1]); cu_q [B+1] int64; k_pool / v_pool
-    [num_blocks, block_size, Hkv * 128] bf16 (one layer's K and V sides of a
-    PagedKVCache pool); block_table [B, max_blocks] int32; kv_len [B] int64 (keys
-    per row, the new positions included); max_q >= every row's q_b. Returns
-    out [T, Hq, 128] bf16. Rows whose shape or pages are out of range are
+    """q [T, Hq, d] bf16 (T = cu_q[-1], head dim d of 64 or 128); cu_q [B+1]
+    int64; k_pool / v_pool [num_blocks, block_size, Hkv * d] bf16 (one layer's K
+    and V sides of a PagedKVCache pool); block_table [B, max_blocks] int32;
+    kv_len [B] int64 (keys per row, the new positions included); max_q >= every
+    row's q_b. Returns out [T, Hq, d] bf16. Rows whose shape or pages are out of range are
     skipped and set `error` (an int32 [1] device tensor) when given. Each row's
     keys are split in chunks of `chunk_tokens` (0: the library's default) on
     separate workgroups; rows of several chunks merge fp32 partials held in

@@ -122,10 +122,10 @@ def test_c_abi_argument_errors():
     assert verify(B, 0, V, need) == EINVAL
     assert verify(B, k, V, need, draft_ids=None) == EINVAL
     assert verify(0, k, V, need) == OK  # an empty batch is a no-op
-    # verify attention: chunk sizes are 0 or multiples of 64 up to 1024; head_dim 128
+    # verify attention: chunk sizes are 0 or multiples of 64 up to 1024; head_dim 64 or 128
     assert L.sdx_verify_attention_workspace(8, 5, 32, 8, 16, 64, 96) == 0
     assert L.sdx_verify_attention_workspace(8, 5, 32, 8, 16, 64, 0) > 0
-    rc = L.sdx_verify_attention_paged(fake, BF16, 8, fake, 5, 32, 8, 64, fake, fake, 100, 16,
+    rc = L.sdx_verify_attention_paged(fake, BF16, 8, fake, 5, 32, 8, 96, fake, fake, 100, 16,
                                       fake, 64, fake, ctypes.c_float(0.125), 0, fake, 1 << 30,
                                       fake, None, None)
     assert rc == EUNSUP and b"head_dim" in L.sdx_last_error()

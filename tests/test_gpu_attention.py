@@ -1,5 +1,6 @@
-"""GPU parity of the MFMA verify attention (sdx_verify_attention_paged) against
-the float64 oracle (oracle/attention.py), at bf16 tolerance: q, K and V are
+"""GPU parity of the MFMA verify attention (sdx_verify_attention_paged, head
+dims 128 and 64) against the float64 oracle (oracle/attention.py), at bf16
+tolerance: q, K and V are
 bf16, the kernel accumulates in fp32 and rounds P (the softmax weights) and
 the output to bf16, so |gpu - oracle| <= 2e-2 + 2e-2 |oracle| elementwise."""
 import numpy as np
@@ -45,6 +46,28 @@ def test_verify_attention_matches_oracle(B, ctx_lo, ctx_hi, hq, hkv, k_max):
     inp = attn_inputs(B, seed=B * 7 + ctx_lo, device=DEV, ctx_lo=ctx_lo, ctx_hi=ctx_hi, hq=hq,
                       hkv=hkv, k_max=k_max, alpha_lo=0.85, alpha_hi=0.95)
     _check(inp, hq, hkv)
+
+
+@pytest.mark.parametrize("B,ctx_lo,ctx_hi,hq,hkv,k_max,chunk", [
+    (6, 0, 40, 32, 8, 8, 0),          # short contexts
+    (5, 100, 1500, 14, 2, 8, 128),    # 14 / 2 heads (group 7) over several chunks
+    (4, 37, 90, 16, 16, 3, 0),        # no grouping
+    (3, 2000, 2600, 32, 8, 8, 0),     # long rows, the library's chunking
+])
+def test_verify_attention_head_dim_64(B, ctx_lo, ctx_hi, hq, hkv, k_max, chunk):
+    """Head dim 64 (the kernel's D = 64 instantiation: one K pass per tile, V
+    held by half of each wave's lanes, four output column blocks)."""
+    inp = attn_inputs(B, seed=B * 11 + ctx_lo, device=DEV, ctx_lo=ctx_lo, ctx_hi=ctx_hi, hq=hq,
+                      hkv=hkv, d=64, k_max=k_max, alpha_lo=0.85, alpha_hi=0.95)
+    _check(inp, hq, hkv, chunk_tokens=chunk)
+
+
+def test_verify_attention_refuses_other_head_dims():
+    from specdec._lib import SpecdecError
+    inp = attn_inputs(2, seed=3, device=DEV, ctx_lo=10, ctx_hi=20, hq=8, hkv=2, d=96, k_max=3)
+    with pytest.raises(SpecdecError):
+        verify_attention_paged(inp["q"], inp["cu_q"], inp["k_pool"], inp["v_pool"],
+                               inp["block_table"], inp["kv_len"], inp["max_q"])
 
 
 @pytest.mark.parametrize("chunk", [64, 128, 1024])
