@@ -441,7 +441,7 @@ __device__ __forceinline__ uint32_t sel_word(const uint4& v, int i) {
 // FP: the found id's p value (its final probability, member rank applied) goes
 // to s32[0] as float bits, read after the walk's last barrier.
 template <int FMT, int NR, int NW = SM_NW, bool FP = false>
-__device__ void block_walk16(const Eval16<FMT>& ev, const typename Eval16<FMT>::Row& rp,
+__device__ __forceinline__ void block_walk16(const Eval16<FMT>& ev, const typename Eval16<FMT>::Row& rp,
                              const typename Eval16<FMT>::Row& rq, bool use_r,
                              const int64_t (&i0)[NR], const int64_t (&i1)[NR],
                              const uint32_t (&bp)[NR], const uint32_t (&bq)[NR], uint64_t (&m)[NR],
@@ -526,6 +526,154 @@ __device__ void block_walk16(const Eval16<FMT>& ev, const typename Eval16<FMT>::
       }
     }
     __syncthreads();  // s32 / s64 reused
+  }
+}
+
+// Table value of a non-member id of row r with key `key`, not past the row's
+// end: block_walk16's value of it (Eval16::eval) when *slow comes back false;
+// *slow: the key is kept but below the table (its value is val16_exp's).
+template <int FMT>
+__device__ __forceinline__ float tval_nonmember16(const typename Eval16<FMT>::Row& r, int32_t key,
+                                                  bool* slow) {
+  const bool live = key >= r.st.klo;
+  const int32_t tt = r.st.kmax - key, tmax = max(r.st.ntbl - 1, 0);
+  *slow = live && tt > tmax;
+  return live ? r.tbl[min(max(tt, 0), tmax)] : 0.0f;
+}
+
+// Whole block, wave w < R taking round w (512 ids) of each: the residual
+// masses m[i] of the NR <= 2 records [x0[i], x1[i]) in which p's or q's kept
+// group members run out, with member ranks (bp[i], bq[i]) at their starts and
+// r0[i] each record's mass of its ids in neither group. The members of either
+// group are the only ids whose value depends on the ranks: each is evaluated
+// with its rank applied and added to r0. Every term is block_walk16's term for
+// the id and fixed-point sums are exact in any order, so m[i] is block_walk16's
+// mass of the record. A term whose non-member side is kept below the table
+// (the exp path) waits for a rare pass after the others, which reloads that
+// id's codes and evaluates it inline: an out-of-line call there would make the
+// values live across it spill to scratch.
+// `cnt64`, `m0`, `m1`: NW words each, not read again before the block's next
+// barrier after this call.
+template <int FMT, int R, int NW, int NR>
+__device__ __forceinline__ void block_part_mass16(const Eval16<FMT>& ev,
+                                                  const typename Eval16<FMT>::Row& rp,
+                                                  const typename Eval16<FMT>::Row& rq,
+                                                  const int64_t (&x0)[NR], const int64_t (&x1)[NR],
+                                                  const uint32_t (&bp)[NR], const uint32_t (&bq)[NR],
+                                                  const uint64_t (&r0)[NR], uint64_t (&m)[NR],
+                                                  uint64_t* cnt64, uint64_t* m0, uint64_t* m1) {
+  static_assert(R <= NW, "one wave per round");
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  const int32_t sp = rp.st.rstar, sq = rq.st.rstar;
+  static_assert(NR == 1 || NR == 2, "one or two records");
+  uint4 P[NR], Q[NR];
+  int32_t nv[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int64_t idx = x0[i] + w * kDrawSub + (int64_t)lane * 8;
+    const bool on = w < R;  // uniform per wave
+    nv[i] = on ? (int32_t)min(max(x1[i] - idx, (int64_t)0), (int64_t)8) : 0;
+    P[i] = make_uint4(0, 0, 0, 0);
+    Q[i] = P[i];
+    if (nv[i] > 0) {
+      P[i] = ev.fetch(rp, idx, x1[i]);
+      Q[i] = ev.fetch(rq, idx, x1[i]);
+    }
+  }
+  uint32_t mp[NR], mq[NR], cnt[NR], incl[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const uint32_t pw[4] = {P[i].x, P[i].y, P[i].z, P[i].w};
+    const uint32_t qw[4] = {Q[i].x, Q[i].y, Q[i].z, Q[i].w};
+    mp[i] = 0;
+    mq[i] = 0;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const uint32_t kp2 = keys2_of_codes2(pw[t >> 1]), kq2 = keys2_of_codes2(qw[t >> 1]);
+      const int32_t kp = (int32_t)((t & 1) ? kp2 >> 16 : kp2 & 0xFFFFu);
+      const int32_t kq = (int32_t)((t & 1) ? kq2 >> 16 : kq2 & 0xFFFFu);
+      const bool in = t < nv[i];
+      mp[i] |= (in && kp >= rp.st.klo && kp >= rp.st.glo && kp <= rp.st.ghi ? 1u : 0u) << t;
+      mq[i] |= (in && kq >= rq.st.klo && kq >= rq.st.glo && kq <= rq.st.ghi ? 1u : 0u) << t;
+    }
+    cnt[i] = (uint32_t)__popc(mp[i]) | ((uint32_t)__popc(mq[i]) << 16);
+    incl[i] = wave_incl_scan_u32(cnt[i], lane);
+  }
+  if (lane == kWave - 1) cnt64[w] = (uint64_t)incl[0] | ((uint64_t)incl[NR - 1] << 32);
+  __syncthreads();
+  uint32_t off[2] = {0, 0};
+#pragma unroll
+  for (int v = 0; v < NW; ++v) {
+    const uint64_t x = cnt64[v];
+    off[0] += v < w ? (uint32_t)x : 0u;
+    off[1] += v < w ? (uint32_t)(x >> 32) : 0u;
+  }
+  uint64_t mine[2] = {0, 0};
+  uint32_t ex[NR], slow = 0;  // slow: bit 8i + t
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    ex[i] = off[i] + incl[i] - cnt[i];
+    if (mp[i] | mq[i]) {  // few lanes: the members of this lane's 8 ids, in id order
+      const uint32_t pw[4] = {P[i].x, P[i].y, P[i].z, P[i].w};
+      const uint32_t qw[4] = {Q[i].x, Q[i].y, Q[i].z, Q[i].w};
+      uint32_t rk_p = bp[i] + (ex[i] & 0xFFFFu), rk_q = bq[i] + (ex[i] >> 16);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const bool ip = (mp[i] >> t) & 1u, iq = (mq[i] >> t) & 1u;
+        if (ip || iq) {
+          const uint32_t kp2 = keys2_of_codes2(pw[t >> 1]), kq2 = keys2_of_codes2(qw[t >> 1]);
+          const int32_t kp = (int32_t)((t & 1) ? kp2 >> 16 : kp2 & 0xFFFFu);
+          const int32_t kq = (int32_t)((t & 1) ? kq2 >> 16 : kq2 & 0xFFFFu);
+          bool sl_p = false, sl_q = false;
+          const float pv = ip ? ((int32_t)rk_p < sp ? rp.vg : 0.0f)
+                              : tval_nonmember16<FMT>(rp, kp, &sl_p);
+          const float qv = iq ? ((int32_t)rk_q < sq ? rq.vg : 0.0f)
+                              : tval_nonmember16<FMT>(rq, kq, &sl_q);
+          if (sl_p || sl_q)
+            slow |= 1u << (8 * i + t);
+          else
+            mine[i] += fixed62(fmaxf(pv - qv, 0.0f));
+        }
+        rk_p += ip ? 1u : 0u;
+        rk_q += iq ? 1u : 0u;
+      }
+    }
+  }
+  if (__builtin_expect(__ballot(slow != 0) != 0, 0)) {  // rare: one term per pass
+    while (slow) {
+      const int b = __builtin_ctz(slow);
+      slow &= slow - 1;
+      const int i = NR == 2 ? b >> 3 : 0, t = b & 7;
+      const int64_t id = (i ? x0[NR - 1] : x0[0]) + w * kDrawSub + (int64_t)lane * 8 + t;
+      const uint32_t e = i ? ex[NR - 1] : ex[0], mpb = i ? mp[NR - 1] : mp[0];
+      const uint32_t mqb = i ? mq[NR - 1] : mq[0];
+      const uint32_t below = (1u << t) - 1u;
+      const uint32_t rk_p = (i ? bp[NR - 1] : bp[0]) + (e & 0xFFFFu) + (uint32_t)__popc(mpb & below);
+      const uint32_t rk_q = (i ? bq[NR - 1] : bq[0]) + (e >> 16) + (uint32_t)__popc(mqb & below);
+      const bool ip = (mpb >> t) & 1u, iq = (mqb >> t) & 1u;
+      const uint32_t cp = rp.ptr[id], cq = rq.ptr[id];
+      bool sl = false;
+      float pv = ip ? ((int32_t)rk_p < sp ? rp.vg : 0.0f)
+                    : tval_nonmember16<FMT>(rp, (int32_t)key_of_code16(cp), &sl);
+      if (sl) pv = val16_exp_inl<FMT>(cp, ev.T, rp.st.m, rp.st.zf, rp.st.totf);
+      sl = false;
+      float qv = iq ? ((int32_t)rk_q < sq ? rq.vg : 0.0f)
+                    : tval_nonmember16<FMT>(rq, (int32_t)key_of_code16(cq), &sl);
+      if (sl) qv = val16_exp_inl<FMT>(cq, ev.T, rq.st.m, rq.st.zf, rq.st.totf);
+      const uint64_t term = fixed62(fmaxf(pv - qv, 0.0f));
+      mine[0] += i ? 0ull : term;
+      mine[1] += i ? term : 0ull;
+    }
+  }
+  const uint64_t s0 = wave_sum_u64(mine[0]), s1 = wave_sum_u64(mine[1]);
+  if (lane == 0) { m0[w] = s0; m1[w] = s1; }
+  __syncthreads();
+  m[0] = r0[0];
+  if (NR == 2) m[NR - 1] = r0[NR - 1];
+#pragma unroll
+  for (int v = 0; v < NW; ++v) {
+    m[0] += m0[v];
+    if (NR == 2) m[NR - 1] += m1[v];
   }
 }
 
@@ -692,6 +840,7 @@ struct Draw16LdsT {
   int64_t found;
   uint32_t s32w[NW];
   uint64_t s64w[NW];
+  uint64_t pmass[2][NW];  // partial records' masses, per wave
   uint32_t fl;
 };
 using Draw16Lds = Draw16LdsT<SM_NW>;
@@ -889,22 +1038,18 @@ __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a,
   }
   uint64_t tot_n;
   const uint64_t ex_n = block_excl_u64<NW>(cntn, s64, &tot_n);
-  uint64_t sum_r = 0, sum_p = 0;
-  {
+  {  // at most one record where p's kept members run out, one for q's
     uint32_t bp = (uint32_t)ex_n, bq = (uint32_t)(ex_n >> 32);
     for (int r = rb0; r < rb1; ++r) {
       const ChunkRec rec = rec_at(r);
       uint64_t pm, rm;
       if (!rec_masses(rec, bp, bq, sp, sq, vp, vq, hasq, &pm, &rm)) {
-        // at most one record where p's kept members run out, one for q's
         const int64_t kp = min<int64_t>(max<int64_t>((int64_t)sp - bp, 0), rec.np);
         const int slot = (kp != 0 && kp != (int64_t)rec.np) ? 0 : 1;
         s_part[slot] = r;
         s_pbase[2 * slot] = bp;
         s_pbase[2 * slot + 1] = bq;
       }
-      sum_r += rm;
-      sum_p += pm;
       bp += rec.np;
       bq += rec.nq;
     }
@@ -913,32 +1058,44 @@ __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a,
   const int pa = s_part[0], pb = s_part[1];
   uint64_t rm_part[2] = {0, 0};
   if (pa >= 0 || pb >= 0) {  // uniform: the (at most two) records where kept members run out
+    // (only with a q row: without one, every record's p mass is exact)
     const int ra_ = pa >= 0 ? pa : pb, rb_ = (pa >= 0 && pb >= 0 && pb != pa) ? pb : -1;
-    const int64_t i0[2] = {(int64_t)ra_ * REC, rb_ >= 0 ? (int64_t)rb_ * REC : 0};
-    const int64_t i1[2] = {min(V, i0[0] + REC), rb_ >= 0 ? min(V, i0[1] + REC) : 0};
     const int sa = pa >= 0 ? 0 : 1;
-    const uint32_t bp2[2] = {s_pbase[2 * sa], s_pbase[2]};
-    const uint32_t bq2[2] = {s_pbase[2 * sa + 1], s_pbase[3]};
     uint64_t mm[2] = {0, 0};
-    // unrolled, so every array index is a constant (indexed at run time the
-    // arrays would live in scratch, and scratch slows the launch of every wave)
+    // one record at a time: the codes of both at once would not fit the
+    // registers left here
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      if (i == 0 || rb_ >= 0) {  // uniform
-        const int64_t a0[1] = {i0[i]}, a1[1] = {i1[i]};
-        const uint32_t p1[1] = {bp2[i]}, q1[1] = {bq2[i]};
+      const int rr = i == 0 ? ra_ : rb_;
+      if (rr >= 0) {  // uniform
+        const int64_t a0[1] = {(int64_t)rr * REC}, a1[1] = {min(V, a0[0] + REC)};
+        const int sl = i == 0 ? sa : 1;
+        const uint32_t p1[1] = {s_pbase[2 * sl]}, q1[1] = {s_pbase[2 * sl + 1]};
+        const uint64_t z1[1] = {lrec[rr].r0};
         uint64_t m1[1];
-        block_walk16<FMT, 1, NW>(ev, rp, rq, true, a0, a1, p1, q1, m1, 0, false, 0, &s_found, s32w,
-                             s64w);
+        block_part_mass16<FMT, R, NW, 1>(ev, rp, rq, a0, a1, p1, q1, z1, m1, s64w, S.pmass[0],
+                                         S.pmass[1]);
         mm[i] = m1[0];
       }
     }
     if (pa >= 0) rm_part[0] = mm[0];
     if (pb >= 0) rm_part[1] = pb == pa ? mm[0] : (pa >= 0 ? mm[1] : mm[0]);
   }
-  for (int i = 0; i < 2; ++i) {
-    const int rr = i == 0 ? pa : pb;
-    if (rr >= rb0 && rr < rb1 && !(i == 1 && rr == pa)) sum_r += rm_part[i];
+  // this thread's record's masses (evaluated again from the LDS copy rather
+  // than held in registers across the partial records' pass)
+  uint64_t sum_r = 0, sum_p = 0;
+  {
+    uint32_t bp = (uint32_t)ex_n, bq = (uint32_t)(ex_n >> 32);
+    for (int r = rb0; r < rb1; ++r) {
+      const ChunkRec rec = rec_at(r);
+      uint64_t pm, rm;
+      if (!rec_masses(rec, bp, bq, sp, sq, vp, vq, hasq, &pm, &rm))
+        rm = r == pa ? rm_part[0] : rm_part[1];
+      sum_r += rm;
+      sum_p += pm;
+      bp += rec.np;
+      bq += rec.nq;
+    }
   }
   uint64_t ex_r, ex_p, tot_r, tot_p;
   {

@@ -84,10 +84,15 @@ __device__ __forceinline__ int cls16(const RowStat& st, int32_t key) {
 // Final probability of a key below the table (out of line, so the compiler
 // cannot if-convert the fp64 exp into every table lookup).
 template <int FMT>
-__device__ __noinline__ float val16_exp(uint32_t code, float T, float m, float zf, float totf) {
+__device__ __forceinline__ float val16_exp_inl(uint32_t code, float T, float m, float zf,
+                                               float totf) {
   const float s = decode16<FMT>(code) / T;
   const float p = exp_det(s - m) / zf;
   return p / totf;
+}
+template <int FMT>
+__device__ __noinline__ float val16_exp(uint32_t code, float T, float m, float zf, float totf) {
+  return val16_exp_inl<FMT>(code, T, m, zf, totf);
 }
 // Final probability of a kept (class 2) or kept-member element.
 template <int FMT>
