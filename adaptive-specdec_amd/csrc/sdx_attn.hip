@@ -144,6 +144,8 @@ __global__ void __launch_bounds__(VA_PLAN_NT) verify_attn_plan_kernel(AttnArgs a
   __shared__ int sBin[VA_CHMAX];  // partial chunks by size, then their first slot
   const int tid = threadIdx.x;
   for (int r = tid; r < VA_CHMAX; r += VA_PLAN_NT) sBin[r] = 0;
+  if (a.arrive)  // the arrival counters of this call's chunk workgroups start at zero
+    for (int64_t i = tid; i < a.batch * a.hkv; i += VA_PLAN_NT) a.arrive[i] = 0;
   __syncthreads();
   long long carry = 0;  // whole chunks so far
   for (int64_t b0 = 0; b0 < a.batch; b0 += VA_PLAN_NT) {
@@ -186,6 +188,107 @@ __global__ void __launch_bounds__(VA_PLAN_NT) verify_attn_plan_kernel(AttnArgs a
     a.units[at] = AttnUnit{(int32_t)b, (int32_t)(kvl / a.chunk), rem, (int32_t)qb, q0, kvl};
   }
   for (int64_t u = carry + tid; u < a.nunits; u += VA_PLAN_NT) a.units[u].b = -1;
+}
+
+// Stores and loads of the chunk partials: agent-scope atomics, which go past
+// the XCD's own L2 (each XCD has one), since the partials of a row are written
+// by workgroups on several XCDs and read by one of them.
+__device__ __forceinline__ void va_st_f32(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void va_st_f2(float* p, float x, float y) {  // p 8-byte aligned
+  const uint64_t v = (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 va_ld_f2(const float* p) {  // p 8-byte aligned
+  const uint64_t v = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+}
+__device__ __forceinline__ float4 va_ld_f4(const float* p) {  // p 16-byte aligned
+  const float2 lo = va_ld_f2(p), hi = va_ld_f2(p + 2);
+  return make_float4(lo.x, lo.y, hi.x, hi.y);
+}
+
+// Merge of the chunk partials of row b, KV head kvh (a row longer than one
+// chunk) by the whole workgroup: out = sum_c w_c O_c with
+// w_c = 2^(m_c - m) / sum_c' 2^(m_c' - m) l_c' and m the row's largest m_c. The
+// (m, l) pairs go through LDS (sW, sL: `cap` floats each) and each query row's
+// weights are formed once; the O partials are then read as float4 with the
+// loads of several chunks in flight. With more chunks x rows than `cap` the
+// weights are formed per element.
+template <int D>
+__device__ __forceinline__ void va_merge(const AttnArgs& a, int64_t b, int kvh, int64_t q0, int M,
+                                         int nch, float* sW, float* sL, int cap) {
+  const int64_t part0 = (b * a.hkv + kvh) * a.nchunk * a.max_m;
+  const bool staged = nch * M <= cap;  // uniform
+  if (staged) {
+    for (int e = threadIdx.x; e < nch * M; e += VA_NT) {  // sW, sL [c * M + i] = m, l of (c, i)
+      const int ch = e / M, i = e % M;
+      const float2 ml = va_ld_f2(a.part_ml + (part0 + (int64_t)ch * a.max_m + i) * 2);
+      sW[e] = ml.x;
+      sL[e] = ml.y;
+    }
+    __syncthreads();
+    if (threadIdx.x < M) {  // one thread per query row: weights in place of the maxima
+      const int i = threadIdx.x;
+      float mx = -INFINITY;
+      for (int ch = 0; ch < nch; ++ch) mx = fmaxf(mx, sW[ch * M + i]);
+      float den = 0.0f;
+      for (int ch = 0; ch < nch; ++ch) {
+        const float m = sW[ch * M + i];
+        const float f = m == -INFINITY ? 0.0f : exp2f(m - mx);
+        sW[ch * M + i] = f;
+        den += f * sL[ch * M + i];
+      }
+      const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+      for (int ch = 0; ch < nch; ++ch) sW[ch * M + i] *= inv;
+    }
+    __syncthreads();
+  }
+  for (int e = threadIdx.x; e < M * (D / 4); e += VA_NT) {
+    const int i = e / (D / 4), d4 = e % (D / 4);
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (staged) {
+#pragma unroll 4
+      for (int ch = 0; ch < nch; ++ch) {
+        const float wgt = sW[ch * M + i];
+        const float4 v = va_ld_f4(a.part_o + (part0 + (int64_t)ch * a.max_m + i) * D + d4 * 4);
+        acc.x += wgt * v.x;
+        acc.y += wgt * v.y;
+        acc.z += wgt * v.z;
+        acc.w += wgt * v.w;
+      }
+    } else {
+      float mx = -INFINITY;
+      for (int ch = 0; ch < nch; ++ch)
+        mx = fmaxf(mx, va_ld_f2(a.part_ml + (part0 + (int64_t)ch * a.max_m + i) * 2).x);
+      float den = 0.0f;
+      for (int ch = 0; ch < nch; ++ch) {
+        const int64_t p = part0 + (int64_t)ch * a.max_m + i;
+        const float2 ml = va_ld_f2(a.part_ml + p * 2);
+        if (ml.x == -INFINITY) continue;  // the chunk holds none of the row's visible keys
+        const float f = exp2f(ml.x - mx);
+        den += f * ml.y;
+        const float4 v = va_ld_f4(a.part_o + p * D + d4 * 4);
+        acc.x += f * v.x;
+        acc.y += f * v.y;
+        acc.z += f * v.z;
+        acc.w += f * v.w;
+      }
+      const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+      acc.x *= inv;
+      acc.y *= inv;
+      acc.z *= inv;
+      acc.w *= inv;
+    }
+    const int64_t j = i / a.group, g = i % a.group;
+    uint16_t* dst = a.out + ((q0 + j) * a.hq + kvh * a.group + g) * D + d4 * 4;
+    const uint32_t lo = (uint32_t)va_bf16(acc.x) | ((uint32_t)va_bf16(acc.y) << 16);
+    const uint32_t hi = (uint32_t)va_bf16(acc.z) | ((uint32_t)va_bf16(acc.w) << 16);
+    *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+  }
 }
 
 // D: head dim, 64 or 128.
@@ -395,12 +498,12 @@ verify_attn_kernel(AttnArgs a) {
     if (t0 + 2 * VA_TOK >= n) break;
   }
   if (bad && a.error) *a.error = 1;
-  if (!active) return;
   // the row index is rebuilt here rather than kept live across the tile loop
   int lre = lr;
   asm volatile("" : "+v"(lre));
 
   if (whole) {  // out[q0 + j, kvh * group + g, :] = O / l
+    if (!active) return;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = r0 + lre + r;
@@ -416,103 +519,35 @@ verify_attn_kernel(AttnArgs a) {
   // the chunk's partial: O unnormalised and (max, sum) per query row, in the
   // part of (row b, KV head, chunk c)
   const int64_t part = ((b * a.hkv + kvh) * a.nchunk + c) * a.max_m;
+  if (active) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int i = r0 + lre + r;
-    if (i < M) {
-      float* po = a.part_o + (part + i) * D;
+    for (int r = 0; r < 4; ++r) {
+      const int i = r0 + lre + r;
+      if (i < M) {
+        float* po = a.part_o + (part + i) * D;
 #pragma unroll
-      for (int jj = 0; jj < OJ; ++jj) po[jj * 16 + lc] = o[jj][r];
-      if (lc == 0) *reinterpret_cast<float2*>(a.part_ml + (part + i) * 2) = make_float2(m_run[r], l_run[r]);
+        for (int jj = 0; jj < OJ; ++jj) va_st_f32(po + jj * 16 + lc, o[jj][r]);
+        if (lc == 0) va_st_f2(a.part_ml + (part + i) * 2, m_run[r], l_run[r]);
+      }
     }
   }
-}
-
-// merge of the chunk partials of every row longer than one chunk: one workgroup
-// per (row, KV head); out = sum_c w_c O_c with w_c = 2^(m_c - m) / sum_c' 2^(m_c' - m) l_c'
-// and m the row's largest m_c. The (m, l) pairs go through LDS and each query
-// row's weights are formed once; the O partials are then read as float4 with
-// the loads of several chunks in flight.
-constexpr int VA_MERGE_W = 4096;  // weights held in LDS (chunks x query rows)
-
-template <int D>
-__global__ void __launch_bounds__(VA_NT) verify_attn_merge_kernel(AttnArgs a) {
-  __shared__ float sW[VA_MERGE_W], sL[VA_MERGE_W];
-  const int64_t b = blockIdx.x / a.hkv;
-  const int kvh = (int)(blockIdx.x % a.hkv);
-  int64_t q0, qb, kvl;
-  if (!va_row(a, b, q0, qb, kvl) || kvl <= a.chunk) return;
+  // the workgroup's stores are done before it counts in on the (row, KV head):
+  // the one that counts in last merges the row's chunks
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // gfx9 encoding: vmcnt(0)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
   const int nch = (int)((kvl + a.chunk - 1) / a.chunk);
-  const int M = (int)qb * a.group;
-  const int64_t part0 = (b * a.hkv + kvh) * a.nchunk * a.max_m;
-  const bool staged = nch * M <= VA_MERGE_W;  // uniform
-  if (staged) {
-    for (int e = threadIdx.x; e < nch * M; e += VA_NT) {  // sW, sL [c * M + i] = m, l of (c, i)
-      const int ch = e / M, i = e % M;
-      const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (part0 + (int64_t)ch * a.max_m + i) * 2);
-      sW[e] = ml.x;
-      sL[e] = ml.y;
-    }
-    __syncthreads();
-    if (threadIdx.x < M) {  // one thread per query row: weights in place of the maxima
-      const int i = threadIdx.x;
-      float mx = -INFINITY;
-      for (int ch = 0; ch < nch; ++ch) mx = fmaxf(mx, sW[ch * M + i]);
-      float den = 0.0f;
-      for (int ch = 0; ch < nch; ++ch) {
-        const float m = sW[ch * M + i];
-        const float f = m == -INFINITY ? 0.0f : exp2f(m - mx);
-        sW[ch * M + i] = f;
-        den += f * sL[ch * M + i];
-      }
-      const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-      for (int ch = 0; ch < nch; ++ch) sW[ch * M + i] *= inv;
-    }
-    __syncthreads();
-  }
-  for (int e = threadIdx.x; e < M * (D / 4); e += VA_NT) {
-    const int i = e / (D / 4), d4 = e % (D / 4);
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (staged) {
-#pragma unroll 4
-      for (int ch = 0; ch < nch; ++ch) {
-        const float wgt = sW[ch * M + i];
-        const float4 v = *reinterpret_cast<const float4*>(
-            a.part_o + (part0 + (int64_t)ch * a.max_m + i) * D + d4 * 4);
-        acc.x += wgt * v.x;
-        acc.y += wgt * v.y;
-        acc.z += wgt * v.z;
-        acc.w += wgt * v.w;
-      }
-    } else {  // more chunks x rows than LDS holds: weights formed per element
-      float mx = -INFINITY;
-      for (int ch = 0; ch < nch; ++ch)
-        mx = fmaxf(mx, a.part_ml[(part0 + (int64_t)ch * a.max_m + i) * 2]);
-      float den = 0.0f;
-      for (int ch = 0; ch < nch; ++ch) {
-        const int64_t p = part0 + (int64_t)ch * a.max_m + i;
-        const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + p * 2);
-        if (ml.x == -INFINITY) continue;  // the chunk holds none of the row's visible keys
-        const float f = exp2f(ml.x - mx);
-        den += f * ml.y;
-        const float4 v = *reinterpret_cast<const float4*>(a.part_o + p * D + d4 * 4);
-        acc.x += f * v.x;
-        acc.y += f * v.y;
-        acc.z += f * v.z;
-        acc.w += f * v.w;
-      }
-      const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-      acc.x *= inv;
-      acc.y *= inv;
-      acc.z *= inv;
-      acc.w *= inv;
-    }
-    const int64_t j = i / a.group, g = i % a.group;
-    uint16_t* dst = a.out + ((q0 + j) * a.hq + kvh * a.group + g) * D + d4 * 4;
-    const uint32_t lo = (uint32_t)va_bf16(acc.x) | ((uint32_t)va_bf16(acc.y) << 16);
-    const uint32_t hi = (uint32_t)va_bf16(acc.z) | ((uint32_t)va_bf16(acc.w) << 16);
-    *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
-  }
+  uint32_t* const flag = reinterpret_cast<uint32_t*>(&sRow[0]);  // row offsets no longer needed
+  if (tid == 0)
+    *flag = __hip_atomic_fetch_add(a.arrive + b * a.hkv + kvh, 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(nch - 1);
+  __syncthreads();
+  if (!*flag) return;  // uniform
+  // the tile buffers hold the merge's weights
+  static_assert(sizeof(sK) <= sizeof(sVt), "merge weights sized by the K tile");
+  va_merge<D>(a, b, kvh, q0, M, nch, reinterpret_cast<float*>(&sK[0][0]),
+              reinterpret_cast<float*>(&sVt[0][0]), (int)(sizeof(sK) / sizeof(float)));
 }
 
 int attn_chunk_tokens(int64_t batch, int32_t hkv, int64_t max_tokens, int32_t chunk) {
@@ -524,13 +559,10 @@ int attn_chunk_tokens(int64_t batch, int32_t hkv, int64_t max_tokens, int32_t ch
 }
 
 template <int D>
-static hipError_t launch_attn_d(const AttnArgs& a, int64_t batch, hipStream_t s) {
+static hipError_t launch_attn_d(const AttnArgs& a, hipStream_t s) {
+  if (a.nchunk > 1 && !a.arrive) return hipErrorInvalidValue;
   hipLaunchKernelGGL(verify_attn_kernel<D>, dim3((unsigned)((a.nunits + 7) / 8 * 8 * a.hkv)),
                      dim3(VA_NT), 0, s, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || a.nchunk == 1) return e;
-  hipLaunchKernelGGL(verify_attn_merge_kernel<D>, dim3((unsigned)(batch * a.hkv)), dim3(VA_NT), 0,
-                     s, a);
   return hipGetLastError();
 }
 
@@ -539,7 +571,7 @@ hipError_t launch_verify_attn(const AttnArgs& a, int64_t batch, hipStream_t s) {
   hipLaunchKernelGGL(verify_attn_plan_kernel, dim3(1), dim3(VA_PLAN_NT), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return a.d == 64 ? launch_attn_d<64>(a, batch, s) : launch_attn_d<128>(a, batch, s);
+  return a.d == 64 ? launch_attn_d<64>(a, s) : launch_attn_d<128>(a, s);
 }
 
 }  // namespace sdx

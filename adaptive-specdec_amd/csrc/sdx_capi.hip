@@ -972,9 +972,12 @@ static int attn_plan(int64_t batch, int32_t max_q, int32_t num_q_heads, int32_t 
                 (long long)(nch * batch * num_kv_heads));
   *chunk = ch;
   *nchunk = (int32_t)nch;
-  // the chunk list, then (rows of several chunks) the parts
+  // the chunk list, then (rows of several chunks) the parts and the per-(row,
+  // KV head) arrival counters
   const size_t units = ((size_t)(batch * nch) * sizeof(sdx::AttnUnit) + 15) & ~(size_t)15;
-  *bytes = units + (nch > 1 ? (size_t)(batch * num_kv_heads * nch * m) * (128 + 2) * sizeof(float) : 0);
+  *bytes = units + (nch > 1 ? (size_t)(batch * num_kv_heads * nch * m) * (128 + 2) * sizeof(float) +
+                                  (size_t)(batch * num_kv_heads) * sizeof(uint32_t)
+                            : 0);
   return SDX_OK;
 }
 
@@ -1049,6 +1052,7 @@ int sdx_verify_attention_paged(const void* q, int dtype, int64_t batch, const in
   const int64_t nparts = batch * num_kv_heads * (int64_t)nch * a.max_m;
   a.part_o = nch > 1 ? (float*)((char*)workspace + ubytes) : nullptr;
   a.part_ml = nch > 1 ? a.part_o + nparts * head_dim : nullptr;
+  a.arrive = nch > 1 ? (uint32_t*)(a.part_ml + nparts * 2) : nullptr;
   a.scale_log2 = scale * 1.4426950408889634f;
   return hip_status(sdx::launch_verify_attn(a, batch, (hipStream_t)stream), "verify_attn");
 }

@@ -400,6 +400,8 @@ struct AttnArgs {
   int64_t nunits;           // batch * nchunk: the launch's chunk slots
   float scale_log2;         // softmax scale * log2(e)
   int32_t d;                // head dim: 64 or 128
+  uint32_t* arrive;         // [B, hkv] chunks of the row written so far (nchunk > 1; zeroed
+                            // by the plan kernel)
 };
 // tokens per key chunk (chunk > 0: that value, else the default for the shape)
 int attn_chunk_tokens(int64_t batch, int32_t hkv, int64_t max_tokens, int32_t chunk);
