@@ -364,9 +364,10 @@ int sdx_kv_append_paged(void* pool, int64_t layer_stride, int64_t side_stride,
  * bf16 for the P V product, output rounded to bf16. The keys of a row are split
  * in chunks of chunk_tokens (0: the library's default for the shape; else a
  * multiple of 64, at most 1024) handled by separate workgroups, longest chunks
- * first; rows of more than one chunk merge fp32 partials. `workspace` holds the
- * chunk list and the partials (sdx_verify_attention_workspace bytes, 16-byte
- * aligned, no initial contents). Three kernels are queued on `stream`. A row
+ * first; rows of more than one chunk merge fp32 partials (the row's last chunk
+ * to finish merges it). `workspace` holds the chunk list, the partials and the
+ * rows' arrival counters (sdx_verify_attention_workspace bytes, 16-byte aligned,
+ * no initial contents). Two kernels are queued on `stream`. A row
  * whose shape is out of range sets *error (nullable) and is skipped; page ids
  * outside the pool set *error and the row's output is unspecified. bf16,
  * head_dim 64 or 128, max_q * (num_q_heads / num_kv_heads) <= 64. */
