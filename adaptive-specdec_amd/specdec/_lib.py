@@ -14,6 +14,15 @@ _LIB = None
 
 F32, BF16, F16 = 0, 1, 2
 _DTYPE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+# Longest fp16 row the library's fp16 kernels take (their row kernel holds a row
+# in registers). The Python entry points widen longer fp16 rows to fp32, which
+# is exact, and run the fp32 kernels (rows up to 262,144).
+F16_MAX_VOCAB = 163840
+
+
+def widen_f16(x):
+    """fp16 rows longer than F16_MAX_VOCAB as fp32 (exact); anything else as is."""
+    return x.float() if x.dtype == torch.float16 and x.shape[-1] > F16_MAX_VOCAB else x
 
 P = ctypes.c_void_p
 I64 = ctypes.c_int64

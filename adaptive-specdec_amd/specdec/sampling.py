@@ -51,6 +51,7 @@ def _kernel_rows(x):
     4 (fp32) elements. Returns (tensor, ld)."""
     if x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
         x = x.float()                      # sampling.py:42 upcasts anything else
+    x = _lib.widen_f16(x)
     V = x.shape[-1]
     mult = 4 if x.dtype == torch.float32 else 8
     if x.is_contiguous() and V % mult == 0 and x.data_ptr() % 16 == 0:
@@ -174,8 +175,9 @@ def rejection_sample(target_logits, draft_logits, draft_ids, u_accept, u_final, 
     dl = None if greedy else draft_logits.to(tl.dtype)
     if not greedy and tuple(dl.shape) != (B, k, V):
         raise ValueError(f"draft_logits must be [{B}, {k}, {V}], got {tuple(dl.shape)}")
-    if tl.dtype != torch.float32 and V % 8 != 0:
-        # 16-bit rows must be 16-byte aligned; the fp32 path takes any vocab it supports
+    if tl.dtype != torch.float32 and (V % 8 != 0 or _lib.widen_f16(tl) is not tl):
+        # 16-bit rows must be 16-byte aligned and fp16 rows at most F16_MAX_VOCAB
+        # long; the fp32 path takes any vocab it supports
         tl = tl.float()
         dl = None if dl is None else dl.float()
     tl = tl.contiguous()
@@ -241,7 +243,7 @@ def rejection_sample_ragged(target_logits, draft_logits, draft_ids, u_accept, u_
     dl = None if greedy else draft_logits.to(tl.dtype)
     if not greedy and tuple(dl.shape) != (NT - B, V):
         raise ValueError(f"draft_logits must be [{NT - B}, {V}], got {tuple(dl.shape)}")
-    if tl.dtype != torch.float32 and V % 8 != 0:
+    if tl.dtype != torch.float32 and (V % 8 != 0 or _lib.widen_f16(tl) is not tl):
         tl = tl.float()
         dl = None if dl is None else dl.float()
     tl = tl.contiguous()
@@ -294,6 +296,14 @@ class Verifier:
         L = _lib.lib()
         self.L = L
         dev = torch.device(device)
+        # fp16 rows longer than the fp16 kernels take: each call copies them into
+        # fp32 buffers allocated here (exact) and runs the fp32 kernels
+        self._t32 = self._d32 = None
+        if self.dt == _lib.F16 and self.V > _lib.F16_MAX_VOCAB:
+            self.dt = _lib.F32
+            self._t32 = torch.empty((self.B, self.k + 1, self.V), dtype=torch.float32, device=dev)
+            if not self.greedy:
+                self._d32 = torch.empty((self.B, self.k, self.V), dtype=torch.float32, device=dev)
         nbytes = (L.sdx_verify_greedy_workspace(self.B, self.k) if self.greedy
                   else L.sdx_verify_workspace(self.B, self.k, self.V, self.dt))
         self.ws = _lib.workspace(nbytes, dev)
@@ -314,10 +324,20 @@ class Verifier:
             if t is not None and not t.is_contiguous():
                 raise ValueError("logits must be contiguous")
 
+    def _rows(self, target, draft):
+        """The logits the kernels read: the caller's, or their fp32 copies."""
+        if self._t32 is None:
+            return target, draft
+        self._t32.copy_(target)
+        if self._d32 is not None:
+            self._d32.copy_(draft)
+        return self._t32, self._d32
+
     def __call__(self, target, draft, draft_ids, u_accept, u_final, active=None):
         self._check(target, draft, draft_ids, u_accept, u_final)
         act = None if active is None else active.to(torch.uint8)
         st = _lib.stream_of(target)
+        target, draft = self._rows(target, draft)
         if self.greedy:
             rc = self.L.sdx_verify_greedy(_lib.ptr(target), self.dt, self.B, self.k, self.V,
                                           _lib.ptr(draft_ids), _lib.ptr(u_accept), _lib.ptr(act),
@@ -347,6 +367,7 @@ class Verifier:
         if self.greedy:
             return self(target, draft, draft_ids, u_accept, u_final, active)
         act = None if active is None else active.to(torch.uint8)
+        target, draft = self._rows(target, draft)
         arr = (ctypes.c_void_p * self.k)(*[w.data_ptr() for w in draft_workspaces])
         rc = self.L.sdx_verify_drafted(_lib.ptr(target), _lib.ptr(draft), self.dt, self.B, self.k,
                                        self.V, _lib.ptr(draft_ids), _lib.ptr(u_accept),
@@ -369,6 +390,7 @@ class Verifier:
         if self.greedy:
             raise ValueError("greedy verify has no statistics phase")
         ids = _lib.ptr(draft_ids) if draft_ids is not None else None
+        target, draft = self._rows(target, draft)
         rc = self.L.sdx_verify_stats(_lib.ptr(target), _lib.ptr(draft), self.dt, self.B, self.k,
                                      self.V, ids, self.T, self.tp, self.tk,
                                      _lib.ptr(self.ws), self.ws.numel(), _lib.stream_of(target))

@@ -94,7 +94,8 @@ int sdx_workspace_init(void* workspace, size_t bytes, sdx_stream_t stream);
  * the nucleus boundary region, at most 7,168 distinct probabilities: a row whose region is
  * larger is flagged SDX_FLAG_UNSUPPORTED with NaN probabilities); larger ones
  * return SDX_EUNSUPPORTED (here and in the verify entry points) before anything
- * is launched. */
+ * is launched. (The Python entry points widen longer fp16 rows to fp32, which
+ * is exact, and call the fp32 path.) */
 
 /* to_probs (sampling.py:34-67): logits [rows, vocab] (dtype) -> probs [rows, vocab] fp32.
  * probs may not overlap fp32 logits (SDX_EINVAL): above 8,192 tokens the fp32 kernel

@@ -2,7 +2,9 @@
 sizes of 200K-vocabulary models (202,048) and the largest bf16 row the row
 kernel takes (2^18 - 8, every per-bin count below 2^18). Same bar as the other
 sampling tests: probabilities bit-identical to the oracle, ids / counts / flags
-exact. fp16 rows stay limited to 163,840 (register-resident row kernel).
+exact. fp16 rows above 163,840 (the fp16 kernels' limit: their row kernel
+holds a row in registers) are widened to fp32 by the Python entry points and
+run on the fp32 kernels: the same bar, through every entry point.
 """
 import numpy as np
 import pytest
@@ -106,11 +108,46 @@ def test_sample_from_probs_large_vocab():
 
 def test_vocab_limits_by_dtype():
     """Above the limits the library refuses the shape (SDX_EUNSUPPORTED) before
-    any launch: bf16 past 2^18 - 8, fp16 past 163,840."""
+    any launch: bf16 past 2^18 - 8. fp16 past 163,840 is refused by the C ABI
+    (tests/test_boundary.py) and served by the Python entry points through the
+    fp32 kernels."""
     g = torch.Generator(device=DEV).manual_seed(3)
     with pytest.raises(RuntimeError, match="vocab"):
         S.to_probs(zipf_logits(1, V_MAX_BF16 + 8, g, DEV), 0.8, 0.95, 0)
-    with pytest.raises(RuntimeError, match="vocab"):
-        S.to_probs(zipf_logits(1, 163840 + 8, g, DEV, dtype=torch.float16), 0.8, 0.95, 0)
-    x = zipf_logits(1, 163840 + 8, g, DEV)  # bf16 at that size is served
-    _assert_probs_equal(_np(S.to_probs(x, 0.8, 0.95, 0)), O.to_probs(_np(x), 0.8, 0.95, 0))
+    for dt in (torch.bfloat16, torch.float16):  # both served at that size
+        x = zipf_logits(1, 163840 + 8, g, DEV, dtype=dt)
+        _assert_probs_equal(_np(S.to_probs(x, 0.8, 0.95, 0)), O.to_probs(_np(x), 0.8, 0.95, 0))
+
+
+@pytest.mark.parametrize("V", [163848, 202048])
+def test_fp16_rows_above_the_fp16_kernels(V):
+    """fp16 rows longer than the fp16 kernels take, through to_probs,
+    draft_step, rejection_sample, rejection_sample_ragged and the prepared
+    Verifier (its fp32 copies), against the oracle on the same fp16 values."""
+    T, tp, B, k = 0.8, 0.95, 4, 3
+    g = torch.Generator(device=DEV).manual_seed(V)
+    x = zipf_logits(3, V, g, DEV, dtype=torch.float16)
+    _assert_probs_equal(_np(S.to_probs(x, T, tp, 0)), O.to_probs(_np(x), T, tp, 0))
+    u = uniforms((3,), g, DEV)
+    xd, qx, _ = S.draft_step(x, u, T, tp)
+    rx = O.sample_from_probs(O.to_probs(_np(x), T, tp, 0), _np(u))
+    assert np.array_equal(xd.cpu().numpy(), rx)
+    inp = verify_inputs(B, k, V, seed=V + 1, device=DEV, temperature=T, top_p=tp,
+                        dtype=torch.float16)
+    args = (inp["target"], inp["draft"], inp["draft_ids"], inp["u_accept"], inp["u_final"])
+    rn, ry, rf = O.rejection_sample(_np(inp["target"]), _np(inp["draft"]),
+                                    inp["draft_ids"].cpu().numpy(), _np(inp["u_accept"]),
+                                    _np(inp["u_final"]), T, tp, 0)
+    outs = [S.rejection_sample(*args, temperature=T, top_p=tp)]
+    ver = S.Verifier(B, k, V, torch.float16, temperature=T, top_p=tp, device=DEV)
+    outs.append(ver(*args))
+    cu = torch.arange(0, B * k + 1, k, dtype=torch.int64, device=DEV)
+    tl = inp["target"].reshape(B * (k + 1), V)
+    dl = inp["draft"].reshape(B * k, V)
+    outs.append(S.rejection_sample_ragged(tl, dl, inp["draft_ids"].reshape(-1),
+                                          inp["u_accept"].reshape(-1), inp["u_final"], cu,
+                                          k_max=k, temperature=T, top_p=tp))
+    for n, y, f in outs:
+        assert np.array_equal(n.cpu().numpy(), rn)
+        assert np.array_equal(y.cpu().numpy(), ry)
+        assert np.array_equal(f.cpu().numpy(), rf)
