@@ -14,8 +14,9 @@
 // load; the KV heads of a chunk run on one XCD (workgroup index % 8) and stream
 // the same page rows together, so each token's 2 KB row is read as eight
 // 256-byte slices close in time. A workgroup's query rows are the q_b positions
-// x group heads that share the KV head (q_b * group <= 64, padded to 16-row MFMA
-// tiles; wave w owns rows 16w .. 16w + 15). The chunk's token -> pool slot map
+// x group heads that share the KV head, up to 64 of them (padded to 16-row MFMA
+// tiles; wave w owns rows 16w .. 16w + 15); a KV head with more query rows has a
+// workgroup per block of 64, each streaming the chunk. The chunk's token -> pool slot map
 // is built in LDS once from the block table (read alongside the row's shape);
 // its keys then stream through LDS
 // in tiles of 32 tokens (each token's head slice is 256 contiguous bytes of
@@ -38,7 +39,7 @@ constexpr int VA_NT = 256;
 constexpr int VA_NW = VA_NT / kWave;
 constexpr int VA_D = 128;     // largest head dim (workspace partial rows are sized for it)
 constexpr int VA_TOK = 32;    // tokens per tile
-constexpr int VA_MAXM = 64;   // query rows per workgroup (q_b * group)
+constexpr int VA_MAXM = 64;   // query rows per workgroup (a block of the q_b * group)
 // LDS row strides (bf16 elements): 2 mod 4 dwords, so the 8-byte MFMA operand
 // reads of 16 consecutive rows hit 32 distinct banks
 template <int D>
@@ -306,16 +307,24 @@ verify_attn_kernel(AttnArgs a) {
   __shared__ int64_t sRow[VA_MAXM];  // query row i -> element offset of its q / out vector
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
-  // a chunk's KV heads on one XCD (workgroup % 8): blocks 8 hkv g .. cover chunks
-  // 8g .. 8g + 7, chunk 8g + x's head h at 8 hkv g + 8 h + x
-  const int64_t grp = blockIdx.x / (8 * a.hkv), rem = blockIdx.x % (8 * a.hkv);
-  const int kvh = (int)(rem / 8);
+  // a chunk's workgroups on one XCD (workgroup % 8): one per (KV head, block of
+  // VA_MAXM query rows), hx = rb * hkv + kvh of nh = hkv * nrb; blocks 8 nh g ..
+  // cover chunks 8g .. 8g + 7, chunk 8g + x's hx at 8 nh g + 8 hx + x
+  const int64_t nh = (int64_t)a.hkv * a.nrb;
+  const int64_t grp = blockIdx.x / (8 * nh), rem = blockIdx.x % (8 * nh);
+  const int hx = (int)(rem / 8);
+  const int kvh = hx % a.hkv, rb = hx / a.hkv;
   const int64_t unit = 8 * grp + rem % 8;
   if (unit >= a.nunits) return;
   const AttnUnit un = a.units[unit];
   if (un.b < 0) return;  // uniform: no chunk in this slot
   const int64_t b = un.b, q0 = un.q0, qb = un.qb, kvl = un.kvl;
   const int c = un.c, n = un.n;
+  // the KV head's query rows of the row (qb positions x group heads), and this
+  // workgroup's block of them: rows rofs .. rofs + M - 1
+  const int Mt = (int)qb * a.group, rofs = VA_MAXM * rb;
+  if (rofs >= Mt) return;  // uniform: the row has fewer row blocks
+  const int M = min(Mt - rofs, VA_MAXM);
   const int64_t c0 = (int64_t)c * a.chunk;
   const int64_t p0 = c0 / a.bs;  // first page of the chunk
   const int np = (int)((c0 + n - 1) / a.bs - p0 + 1);
@@ -323,10 +332,13 @@ verify_attn_kernel(AttnArgs a) {
   int32_t* sPage = reinterpret_cast<int32_t*>(&sVt[0][0]);
   for (int i = tid; i < np; i += VA_NT) sPage[i] = a.block_table[b * a.max_blocks + p0 + i];
   const int64_t base = kvl - qb;
-  const int M = (int)qb * a.group;
   const bool whole = kvl <= a.chunk;  // the row is one chunk: write the output directly
-  // row i = j * group + g is query head kvh * group + g of position j
-  if (tid < M) sRow[tid] = ((q0 + tid / a.group) * a.hq + kvh * a.group + tid % a.group) * D;
+  // row i = j * group + g is query head kvh * group + g of position j; local row
+  // il of the block is row rofs + il
+  if (tid < M) {
+    const int i = rofs + tid;
+    sRow[tid] = ((q0 + i / a.group) * a.hq + kvh * a.group + i % a.group) * D;
+  }
   __syncthreads();  // page ids and row offsets in LDS
 
   // ---- the chunk's slots: token t -> (page * bs + (c0 + t) % bs) * hkv + kvh
@@ -414,7 +426,7 @@ verify_attn_kernel(AttnArgs a) {
     m_run[r] = -INFINITY;
     l_run[r] = 0.0f;
     const int i = r0 + lr + r;
-    const int64_t l = i < M ? base + i / a.group - c0 : -1;
+    const int64_t l = i < M ? base + (rofs + i) / a.group - c0 : -1;
     lim[r] = (int)max((int64_t)-1, min(l, (int64_t)n - 1));
   }
 
@@ -517,8 +529,8 @@ verify_attn_kernel(AttnArgs a) {
     return;
   }
   // the chunk's partial: O unnormalised and (max, sum) per query row, in the
-  // part of (row b, KV head, chunk c)
-  const int64_t part = ((b * a.hkv + kvh) * a.nchunk + c) * a.max_m;
+  // part of (row b, KV head, chunk c); the block's rows from rofs
+  const int64_t part = ((b * a.hkv + kvh) * a.nchunk + c) * a.max_m + rofs;
   if (active) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -538,15 +550,16 @@ verify_attn_kernel(AttnArgs a) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __syncthreads();
   const int nch = (int)((kvl + a.chunk - 1) / a.chunk);
+  const int nrbr = (Mt + VA_MAXM - 1) / VA_MAXM;  // the row's blocks of query rows
   uint32_t* const flag = reinterpret_cast<uint32_t*>(&sRow[0]);  // row offsets no longer needed
   if (tid == 0)
     *flag = __hip_atomic_fetch_add(a.arrive + b * a.hkv + kvh, 1u, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(nch - 1);
+                                   __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(nch * nrbr - 1);
   __syncthreads();
   if (!*flag) return;  // uniform
   // the tile buffers hold the merge's weights
   static_assert(sizeof(sK) <= sizeof(sVt), "merge weights sized by the K tile");
-  va_merge<D>(a, b, kvh, q0, M, nch, reinterpret_cast<float*>(&sK[0][0]),
+  va_merge<D>(a, b, kvh, q0, Mt, nch, reinterpret_cast<float*>(&sK[0][0]),
               reinterpret_cast<float*>(&sVt[0][0]), (int)(sizeof(sK) / sizeof(float)));
 }
 
@@ -561,7 +574,8 @@ int attn_chunk_tokens(int64_t batch, int32_t hkv, int64_t max_tokens, int32_t ch
 template <int D>
 static hipError_t launch_attn_d(const AttnArgs& a, hipStream_t s) {
   if (a.nchunk > 1 && !a.arrive) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(verify_attn_kernel<D>, dim3((unsigned)((a.nunits + 7) / 8 * 8 * a.hkv)),
+  hipLaunchKernelGGL(verify_attn_kernel<D>,
+                     dim3((unsigned)((a.nunits + 7) / 8 * 8 * a.hkv * a.nrb)),
                      dim3(VA_NT), 0, s, a);
   return hipGetLastError();
 }

@@ -967,9 +967,10 @@ static int attn_plan(int64_t batch, int32_t max_q, int32_t num_q_heads, int32_t 
   const int32_t ch = sdx::attn_chunk_tokens(batch, num_kv_heads, max_tokens, chunk_tokens);
   const int64_t nch = (max_tokens + ch - 1) / ch;
   const int64_t m = (int64_t)max_q * (num_q_heads / num_kv_heads);
-  if (nch * batch * num_kv_heads > 0x7FFFFFFF)
-    return fail(SDX_EUNSUPPORTED, "sdx_verify_attention: grid of %lld chunks is too large",
-                (long long)(nch * batch * num_kv_heads));
+  const int64_t nrb = (m + 63) / 64;  // workgroups per (chunk, KV head): 64 query rows each
+  if (m > 0x7FFFFFFF / 64 || nch * batch * num_kv_heads * nrb > 0x7FFFFFFF)
+    return fail(SDX_EUNSUPPORTED, "sdx_verify_attention: grid of %lld chunk workgroups is too large",
+                (long long)(nch * batch * num_kv_heads * nrb));
   *chunk = ch;
   *nchunk = (int32_t)nch;
   // the chunk list, then (rows of several chunks) the parts and the per-(row,
@@ -1011,10 +1012,6 @@ int sdx_verify_attention_paged(const void* q, int dtype, int64_t batch, const in
                            chunk_tokens, &ch, &nch, &need);
   if (rc != SDX_OK) return rc;
   const int32_t group = num_q_heads / num_kv_heads;
-  if ((int64_t)max_q * group > 64)
-    return fail(SDX_EUNSUPPORTED,
-                "sdx_verify_attention_paged: max_q * (query heads per KV head) must be <= 64 "
-                "(got %d * %d)", max_q, group);
   if (num_blocks * block_size * num_kv_heads >= (int64_t)0xFFFFFFFF)
     return fail(SDX_EUNSUPPORTED, "sdx_verify_attention_paged: pool of 2^32 or more head slices");
   if (!aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool) || !aligned16(out))
@@ -1046,6 +1043,7 @@ int sdx_verify_attention_paged(const void* q, int dtype, int64_t batch, const in
   a.chunk = ch;
   a.nchunk = nch;
   a.max_m = max_q * group;
+  a.nrb = (a.max_m + 63) / 64;
   a.nunits = batch * (int64_t)nch;
   const size_t ubytes = ((size_t)a.nunits * sizeof(sdx::AttnUnit) + 15) & ~(size_t)15;
   a.units = (sdx::AttnUnit*)workspace;

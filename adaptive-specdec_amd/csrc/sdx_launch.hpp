@@ -402,6 +402,7 @@ struct AttnArgs {
   int32_t d;                // head dim: 64 or 128
   uint32_t* arrive;         // [B, hkv] chunks of the row written so far (nchunk > 1; zeroed
                             // by the plan kernel)
+  int32_t nrb;              // blocks of 64 query rows per (chunk, KV head): ceil(max_m / 64)
 };
 // tokens per key chunk (chunk > 0: that value, else the default for the shape)
 int attn_chunk_tokens(int64_t batch, int32_t hkv, int64_t max_tokens, int32_t chunk);

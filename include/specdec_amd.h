@@ -371,7 +371,8 @@ int sdx_kv_append_paged(void* pool, int64_t layer_stride, int64_t side_stride,
  * no initial contents). Two kernels are queued on `stream`. A row
  * whose shape is out of range sets *error (nullable) and is skipped; page ids
  * outside the pool set *error and the row's output is unspecified. bf16,
- * head_dim 64 or 128, max_q * (num_q_heads / num_kv_heads) <= 64. */
+ * head_dim 64 or 128. A KV head with more than 64 query rows (max_q x query heads
+ * per KV head) takes a workgroup per block of 64 rows for each key chunk. */
 int sdx_verify_attention_paged(const void* q, int dtype, int64_t batch, const int64_t* cu_q,
                                int32_t max_q, int32_t num_q_heads, int32_t num_kv_heads,
                                int32_t head_dim, const void* k_pool, const void* v_pool,

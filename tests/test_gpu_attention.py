@@ -37,12 +37,10 @@ def _check(inp, hq, hkv, atol=2e-2, rtol=2e-2, chunk_tokens=0):
 @pytest.mark.parametrize("B,ctx_lo,ctx_hi,hq,hkv,k_max", [
     (6, 0, 40, 32, 8, 8),       # short contexts: tails inside the first tiles
     (5, 100, 300, 32, 8, 8),    # several tiles, ragged q_b from the controller
-    (3, 2000, 2600, 8, 1, 8),   # group 8: up to 72 > 64 rows -> k_max 7 below
+    (3, 2000, 2600, 8, 1, 8),   # group 8: up to 72 rows, two blocks of query rows
     (4, 37, 90, 16, 16, 3),     # no grouping (group 1)
 ])
 def test_verify_attention_matches_oracle(B, ctx_lo, ctx_hi, hq, hkv, k_max):
-    if (k_max + 1) * (hq // hkv) > 64:
-        k_max = 64 // (hq // hkv) - 1
     inp = attn_inputs(B, seed=B * 7 + ctx_lo, device=DEV, ctx_lo=ctx_lo, ctx_hi=ctx_hi, hq=hq,
                       hkv=hkv, k_max=k_max, alpha_lo=0.85, alpha_hi=0.95)
     _check(inp, hq, hkv)
@@ -59,6 +57,23 @@ def test_verify_attention_head_dim_64(B, ctx_lo, ctx_hi, hq, hkv, k_max, chunk):
     held by half of each wave's lanes, four output column blocks)."""
     inp = attn_inputs(B, seed=B * 11 + ctx_lo, device=DEV, ctx_lo=ctx_lo, ctx_hi=ctx_hi, hq=hq,
                       hkv=hkv, d=64, k_max=k_max, alpha_lo=0.85, alpha_hi=0.95)
+    _check(inp, hq, hkv, chunk_tokens=chunk)
+
+
+@pytest.mark.parametrize("B,ctx_lo,ctx_hi,hq,hkv,d,k_max,chunk", [
+    (4, 30, 200, 64, 8, 128, 8, 0),       # group 8, up to 72 rows: 2 row blocks, one chunk
+    (3, 1500, 2600, 64, 8, 128, 8, 256),  # the same over several chunks
+    (2, 100, 700, 32, 1, 128, 6, 128),    # group 32, up to 224 rows: 4 row blocks
+    (3, 300, 900, 48, 2, 64, 8, 128),     # head dim 64, group 24, up to 216 rows
+    (2, 4000, 4200, 64, 8, 128, 8, 64),   # 66 chunks x 72 rows: weights formed per element
+])
+def test_verify_attention_more_than_64_query_rows(B, ctx_lo, ctx_hi, hq, hkv, d, k_max, chunk):
+    """A KV head with more than 64 query rows (q_b positions x query heads per
+    KV head) gets a workgroup per block of 64 rows for each chunk; a row of
+    several chunks is merged by the last of its chunks x blocks to finish."""
+    inp = attn_inputs(B, seed=B * 13 + ctx_lo + hq, device=DEV, ctx_lo=ctx_lo, ctx_hi=ctx_hi,
+                      hq=hq, hkv=hkv, d=d, k_max=k_max, alpha_lo=0.9, alpha_hi=0.97)
+    assert inp["max_q"] * (hq // hkv) > 64
     _check(inp, hq, hkv, chunk_tokens=chunk)
 
 
@@ -127,16 +142,13 @@ def test_verify_attention_rejects_bad_rows():
                            inp["kv_len"], inp["max_q"], error=err)
     torch.cuda.synchronize()
     assert int(err.item()) == 1
-    with pytest.raises(RuntimeError):       # max_q * group > 64
-        verify_attention_paged(inp["q"], inp["cu_q"], inp["k_pool"], inp["v_pool"],
-                               inp["block_table"], inp["kv_len"], 17)
     with pytest.raises(RuntimeError):       # chunk not a multiple of 64
         verify_attention_paged(inp["q"], inp["cu_q"], inp["k_pool"], inp["v_pool"],
                                inp["block_table"], inp["kv_len"], inp["max_q"], chunk_tokens=96)
 
 
 def test_verify_attention_graph_replays():
-    """The call captured in a graph (plan, attention, merge; no memsets): every
+    """The call captured in a graph (plan and attention kernels; no memsets): every
     replay, with eager calls and synchronizations between replays, equals the
     eager output bit for bit (the kernels are deterministic)."""
     hq, hkv = 32, 8
@@ -169,13 +181,13 @@ def test_verify_attention_graph_replays():
 
 def test_verify_attention_long_rows_unstaged_merge():
     """Chunks of 64 keys over contexts near 8192 with 9 query positions x group 4
-    (36 rows per KV head): 128 chunks x 36 rows = 4608 > 4096 chunk weights, so
-    the merge kernel forms its weights per element instead of staging them in
-    LDS."""
+    (36 rows per KV head): 128 chunks x 36 rows = 4608 chunk weights, more than
+    the 2112 the merging workgroup's tile buffers hold at head dim 128, so the
+    merge forms its weights per element instead of staging them in LDS."""
     inp = attn_inputs(2, seed=64, device=DEV, ctx_lo=8000, ctx_hi=8192, hq=32, hkv=8, k_max=8,
                       alpha_lo=0.97, alpha_hi=0.99)
     nch = (int(inp["kv_len"].max()) + 63) // 64
-    assert nch * inp["max_q"] * 4 > 4096
+    assert nch * inp["max_q"] * 4 > 2112
     _check(inp, 32, 8, chunk_tokens=64)
 
 
