@@ -152,7 +152,7 @@ draft_fused_bf16_kernel(DraftFusedArgs a) {
   // conf[j] (written before this launch) loaded ahead of the draw, for the
   // block that completes it
   const float conf0 = threadIdx.x == 0 && a.e.conf ? a.e.conf[j] : 0.0f;
-  draw16_body<SDX_BF16, true, SK_NT, kRec16Rounds, true>(f.d, U.draw, j, bi);
+  draw16_body<SDX_BF16, true, SK_NT, kRec16Rounds, true, true>(f.d, U.draw, j, bi);
   // draw16_body leaves `last` set in the one block that completed the row's draw
   if (threadIdx.x < kWave && U.draw.last)
     draft_epilogue_row(a, j, __uint_as_float(U.draw.s32w[0]), conf0);

@@ -848,8 +848,10 @@ using Draw16Lds = Draw16LdsT<SM_NW>;
 // One job's accept chain and draw, run by a block of SM_NT threads: block bi of
 // the job's blocks (wave w of it owns record bi * SM_NW + w); the block that
 // completes the job's records draws y. FP: that block also leaves the drawn
-// id's p value in S.s32w[0] (float bits) when y >= 0.
-template <int FMT, bool COH, int NT = SM_NT, int R = kRec16Rounds, bool FP = false>
+// id's p value in S.s32w[0] (float bits) when y >= 0. NOQ: the caller's jobs
+// never have a q row (k = 0), so nothing of one is loaded or compiled in.
+template <int FMT, bool COH, int NT = SM_NT, int R = kRec16Rounds, bool FP = false,
+          bool NOQ = false>
 __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a,
                                             Draw16LdsT<NT / kWave>& S, int64_t j, int bi) {
   constexpr int NW = NT / kWave;
@@ -903,7 +905,7 @@ __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a,
   }
   __syncthreads();
   const SampleJob job = s_job;
-  const bool hasq = job.qrow >= 0;
+  const bool hasq = !NOQ && job.qrow >= 0;
   typename Eval16<FMT>::Row rp, rq;
   rp.ptr = job.prow < ev.split ? ev.base + job.prow * ev.ld : ev.base2 + (job.prow - ev.split) * ev.ld2;
   rp.st = s_st[0];
@@ -927,7 +929,7 @@ __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a,
   // addresses stay inside the rows / tables, unused values are replaced)
   const int t0 = threadIdx.x;  // first NT entries now, the rest (wide nuclei) after
   const float tp0 = ld_f32<COH>(ev.tables + job.prow * kTbl + t0);
-  const float tq0 = ld_f32<COH>(ev.tables + (hasq ? job.qrow : job.prow) * kTbl + t0);
+  const float tq0 = NOQ ? 0.0f : ld_f32<COH>(ev.tables + (hasq ? job.qrow : job.prow) * kTbl + t0);
   __builtin_amdgcn_sched_barrier(0);  // keep the issue order: tables, then rows
   const int rec = bi * NW + w;
   const bool has_rec = rec < a.nrec;  // uniform per wave
@@ -940,7 +942,8 @@ __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a,
     // are read only when the draw has a q row
     const int64_t ic = has_rec && idx < V ? idx : 0;  // V % 8 == 0: whole 16-byte groups
     put(P, u, *reinterpret_cast<const uint4*>(rp.ptr + ic));
-    put(Q, u, *reinterpret_cast<const uint4*>((hasq ? rq.ptr : rp.ptr) + ic));
+    put(Q, u, NOQ ? make_uint4(0, 0, 0, 0)
+                  : *reinterpret_cast<const uint4*>((hasq ? rq.ptr : rp.ptr) + ic));
   }
   __builtin_amdgcn_sched_barrier(0);
   if (t0 < rp.st.ntbl) tbl_p[t0] = tp0;
@@ -1057,7 +1060,7 @@ __device__ __forceinline__ void draw16_body(const Draw16Args<FMT>& a,
   __syncthreads();
   const int pa = s_part[0], pb = s_part[1];
   uint64_t rm_part[2] = {0, 0};
-  if (pa >= 0 || pb >= 0) {  // uniform: the (at most two) records where kept members run out
+  if (!NOQ && (pa >= 0 || pb >= 0)) {  // uniform: the (at most two) records where kept members run out
     // (only with a q row: without one, every record's p mass is exact)
     const int ra_ = pa >= 0 ? pa : pb, rb_ = (pa >= 0 && pb >= 0 && pb != pa) ? pb : -1;
     const int sa = pa >= 0 ? 0 : 1;
