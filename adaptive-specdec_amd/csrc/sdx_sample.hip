@@ -594,7 +594,8 @@ __global__ void __launch_bounds__(SM_NT) draw_kernel(Ev ev, DrawArgs a) {
 
 // ---------------------------------------------------------------- verify draw, 16-bit rows
 // The draw body (sdx_draw16.hpp) on its own grid: nblk blocks per batch row.
-template <int FMT>
+// NOQ: k = 0 (draft steps), no job has a q row.
+template <int FMT, bool NOQ = false>
 __global__ void __launch_bounds__(SM_NT) __attribute__((amdgpu_waves_per_eu(5)))
 draw16_kernel(Draw16Args<FMT> a) {
   __shared__ Draw16Lds S;
@@ -611,7 +612,7 @@ draw16_kernel(Draw16Args<FMT> a) {
     j = (int64_t)blockIdx.x / a.nblk;
     bi = (int)((int64_t)blockIdx.x % a.nblk);
   }
-  draw16_body<FMT, false>(a, S, j, bi);
+  draw16_body<FMT, false, SM_NT, kRec16Rounds, false, NOQ>(a, S, j, bi);
 }
 
 // ---------------------------------------------------------------- to_probs output
@@ -1053,7 +1054,12 @@ static hipError_t launch_draw16_fmt(const RowSource16& src, const RowStat* stats
   a.recs = recs;
   a.counters = counters;
   a.y = y;
-  hipLaunchKernelGGL((draw16_kernel<FMT>), dim3((unsigned)(a.nblk * njobs)), dim3(SM_NT), 0, s, a);
+  if (acc.k == 0 && !acc.cu_k)  // every job draws from its one p row
+    hipLaunchKernelGGL((draw16_kernel<FMT, true>), dim3((unsigned)(a.nblk * njobs)), dim3(SM_NT),
+                       0, s, a);
+  else
+    hipLaunchKernelGGL((draw16_kernel<FMT>), dim3((unsigned)(a.nblk * njobs)), dim3(SM_NT), 0, s,
+                       a);
   return hipGetLastError();
 }
 
