@@ -21,7 +21,10 @@ constexpr int kWsMaxCounters = 1024 - kWsCounterWord;
 constexpr int kWsFusedJobWord = 1024;   // fused verify: row arrivals per batch row
 constexpr int kWsFusedDrawWord = 2048;  // fused verify: the draw's counters per batch row
 constexpr int kWsFusedMaxJobs = 1024;   // batch rows the fused verify serves
-static_assert(kWsFusedDrawWord + kWsFusedMaxJobs <= (int)(kWsHeaderBytes / 4), "header words");
+static_assert(kWsCounterWord + kWsMaxCounters <= kWsFusedJobWord &&
+                  kWsFusedJobWord + kWsFusedMaxJobs <= kWsFusedDrawWord &&
+                  kWsFusedDrawWord + kWsFusedMaxJobs <= (int)(kWsHeaderBytes / 4),
+              "header word ranges in order, inside the header");
 
 struct RowStatArgs {
   const uint16_t* base[2];  // group 0: target rows, group 1: draft rows
@@ -285,6 +288,9 @@ constexpr int kDraftSigWords = 6;
 // The fused draft step's count of batch rows whose epilogue is written (the
 // last one resets it to zero).
 constexpr int kWsDraftDoneWord = kWsDraftSigWord + kDraftSigWords;
+static_assert(kWsDraftSigWord >= kWsFusedDrawWord + kWsFusedMaxJobs &&
+                  kWsDraftDoneWord < (int)(kWsHeaderBytes / 4),
+              "the draft step's header words past the fused verify's, inside the header");
 constexpr int kMaxDraftK = 31;  // the fused verify's 2k + 1 <= 64
 struct DraftEpiArgs {
   int fmt;                 // SDX_BF16 / SDX_F16 (16-bit rows)

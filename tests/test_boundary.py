@@ -173,3 +173,22 @@ def test_verify_counters_lie_in_the_header():
                             assert e0 <= b1, (dt, V, B, k, cus, used)
                         n_checked += 1
     assert n_checked > 1000
+
+
+def test_long_fp16_rows_are_widened_for_the_fp32_kernels():
+    """The Python entry points hand fp16 rows longer than the fp16 kernels take
+    (F16_MAX_VOCAB, the C ABI's fp16 limit) to the fp32 kernels, widened
+    exactly; every other row goes to the kernels as it is."""
+    from specdec import _lib
+    L = _lib.lib()
+    fake = ctypes.c_void_p(16)
+    EUNSUP = -2  # SDX_EUNSUPPORTED
+    # the C ABI's limit is the one the Python layer widens past
+    assert L.sdx_to_probs(fake, _lib.F16, 1, _lib.F16_MAX_VOCAB + 8, _lib.F16_MAX_VOCAB + 8,
+                          ctypes.c_float(0.8), ctypes.c_float(0.95), 0, fake,
+                          _lib.F16_MAX_VOCAB + 8, fake, 1 << 40, None) == EUNSUP
+    x = (torch.arange(2 * (_lib.F16_MAX_VOCAB + 8)) % 2000 - 1000).reshape(2, -1).to(torch.float16)
+    w = _lib.widen_f16(x)
+    assert w.dtype == torch.float32 and torch.equal(w, x.float())
+    for t in (x[:, :_lib.F16_MAX_VOCAB], x.to(torch.bfloat16), x.float()):
+        assert _lib.widen_f16(t) is t
