@@ -149,12 +149,18 @@ __global__ void __launch_bounds__(VA_PLAN_NT) verify_attn_plan_kernel(AttnArgs a
     for (int64_t i = tid; i < a.batch * a.hkv; i += VA_PLAN_NT) a.arrive[i] = 0;
   __syncthreads();
   long long carry = 0;  // whole chunks so far
+  // row tid's shape, kept for the partial chunks below (rows past VA_PLAN_NT are
+  // read again there)
+  bool ok0 = false;
+  int64_t q00 = 0, qb0 = 0, kvl0 = 0;
   for (int64_t b0 = 0; b0 < a.batch; b0 += VA_PLAN_NT) {
     const int64_t b = b0 + tid;
     long long nfull = 0;
     int64_t q0 = 0, qb = 0, kvl = 0;
     if (b < a.batch) {
-      if (va_row(a, b, q0, qb, kvl)) {
+      const bool ok = va_row(a, b, q0, qb, kvl);
+      if (b0 == 0) { ok0 = ok; q00 = q0; qb0 = qb; kvl0 = kvl; }
+      if (ok) {
         if (qb > 0) {
           nfull = kvl / a.chunk;
           const int rem = (int)(kvl % a.chunk);
@@ -181,8 +187,9 @@ __global__ void __launch_bounds__(VA_PLAN_NT) verify_attn_plan_kernel(AttnArgs a
     carry += tot;  // all chunks
   }
   for (int64_t b = tid; b < a.batch; b += VA_PLAN_NT) {
-    int64_t q0, qb, kvl;
-    if (!va_row(a, b, q0, qb, kvl) || qb <= 0) continue;
+    int64_t q0 = q00, qb = qb0, kvl = kvl0;
+    const bool ok = b < VA_PLAN_NT ? ok0 : va_row(a, b, q0, qb, kvl);
+    if (!ok || qb <= 0) continue;
     const int rem = (int)(kvl % a.chunk);
     if (rem == 0) continue;
     const int at = atomicAdd(&sBin[rem], 1);
