@@ -552,8 +552,8 @@ __device__ __forceinline__ float tval_nonmember16(const typename Eval16<FMT>::Ro
 // (the exp path) waits for a rare pass after the others, which reloads that
 // id's codes and evaluates it inline: an out-of-line call there would make the
 // values live across it spill to scratch.
-// `cnt64`, `m0`, `m1`: NW words each, not read again before the block's next
-// barrier after this call.
+// `cnt64`, `m0`, `m1`: LDS words (NW each) this call may overwrite; the other
+// code of the block does not read them between this call's barriers.
 template <int FMT, int R, int NW, int NR>
 __device__ __forceinline__ void block_part_mass16(const Eval16<FMT>& ev,
                                                   const typename Eval16<FMT>::Row& rp,
